@@ -1,0 +1,226 @@
+"""TEST INFRASTRUCTURE — independent float64 restatements used to pin the C++ oracle.
+
+Written from the mathematics of the recurrences, sharing no code with
+`cpu_ref.cpp`. Each uses a different evaluation structure from the C++ file,
+so a transcription slip there (a dropped term, a wrong index, a transposed
+operand, the wrong trapezoid neighbour under reverse) shows up as a mismatch:
+
+* `m1_scan`: vectorised over (batch, channel), with reverse implemented as
+  flip -> forward -> flip (the reference's definition, lib.rs:107-126).
+* `m3_siso_scan`: the sequential form with reverse as flip -> forward -> flip
+  applied AFTER the rotation (tests/reference/mamba3_ref.py:216-267 states why
+  the order matters).
+* `m3_siso_dense`: the O(L^2) dual (attention-like) form of the same SISO
+  recurrence — no state matrix at all.
+* `m3_mimo_scan`: the rank-r sequential form, einsum-free.
+
+Only for small shapes: these are loops in numpy.
+"""
+
+import numpy as np
+
+
+def softplus(x):
+    x = np.asarray(x, np.float64)
+    return np.where(x > 20.0, x, np.log1p(np.exp(np.minimum(x, 20.0))))
+
+
+def silu(x):
+    x = np.asarray(x, np.float64)
+    return x / (1.0 + np.exp(-x))
+
+
+def sigmoid(x):
+    x = np.asarray(x, np.float64)
+    return 0.5 * (1.0 + np.tanh(0.5 * x))
+
+
+def m1_scan(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_softplus=False,
+            reverse=False, h0=None):
+    """Mamba-1 selective scan in float64 -> (out (b,d,l), last_state (b,d,n))."""
+    u = np.asarray(u, np.float64)
+    delta = np.asarray(delta, np.float64)
+    A = np.asarray(A, np.float64)
+    B = np.asarray(B, np.float64)
+    C = np.asarray(C, np.float64)
+    b, d, L = u.shape
+    n = A.shape[1]
+    if B.ndim == 3:
+        B, C = B[:, None], C[:, None]
+    g = B.shape[1]
+    # channel d reads group d // (d_total / g) (lib.rs:82-83)
+    gidx = np.arange(d) // (d // g)
+    Bd = B[:, gidx]  # (b, d, n, L)
+    Cd = C[:, gidx]
+    if delta_bias is not None:
+        delta = delta + np.asarray(delta_bias, np.float64)[None, :, None]
+    if delta_softplus:
+        delta = softplus(delta)
+    if reverse:
+        u, delta = u[..., ::-1], delta[..., ::-1]
+        Bd, Cd = Bd[..., ::-1], Cd[..., ::-1]
+        zz = None if z is None else np.asarray(z, np.float64)[..., ::-1]
+    else:
+        zz = None if z is None else np.asarray(z, np.float64)
+    h = np.zeros((b, d, n)) if h0 is None else np.array(h0, np.float64)
+    out = np.empty((b, d, L))
+    for t in range(L):
+        h = np.exp(delta[:, :, t, None] * A[None]) * h \
+            + (delta[:, :, t] * u[:, :, t])[..., None] * Bd[:, :, :, t]
+        out[:, :, t] = (h * Cd[:, :, :, t]).sum(-1)
+    if D is not None:
+        out = out + u * np.asarray(D, np.float64)[None, :, None]
+    if zz is not None:
+        out = out * silu(zz)
+    if reverse:
+        out = out[..., ::-1]
+    return np.ascontiguousarray(out), h
+
+
+def _rope_interleaved(x, cos, sin):
+    a, b = x[..., 0::2], x[..., 1::2]
+    out = np.empty_like(x)
+    out[..., 0::2] = a * cos - b * sin
+    out[..., 1::2] = a * sin + b * cos
+    return out
+
+
+def _rope_split(x, cos, sin):
+    half = x.shape[-1] // 2
+    a, b = x[..., :half], x[..., half:]
+    return np.concatenate([a * cos - b * sin, a * sin + b * cos], axis=-1)
+
+
+def _m3_prep(q, k, v, adt, dt, trap, q_bias, k_bias, cos, sin, z, heads, rope):
+    """Bias, rotate and expand q/k to per-head (b, l, [r,] h, dqk) in float64."""
+    q = np.asarray(q, np.float64)
+    k = np.asarray(k, np.float64)
+    g = q.shape[-2]
+    hidx = np.arange(heads) // (heads // g)
+    q = q[..., hidx, :] + np.asarray(q_bias, np.float64)
+    k = k[..., hidx, :] + np.asarray(k_bias, np.float64)
+    cos = np.asarray(cos, np.float64)
+    sin = np.asarray(sin, np.float64)
+    if q.ndim == 5:  # (b, l, r, h, dqk): angles shared across rank
+        cos, sin = cos[:, :, None], sin[:, :, None]
+    return rope(q, cos, sin), rope(k, cos, sin)
+
+
+def _gates(adt, dt, trap):
+    dt = np.asarray(dt, np.float64)
+    lam = sigmoid(trap)
+    gamma = dt * lam
+    shifted = np.zeros_like(gamma)
+    shifted[..., :-1] = dt[..., 1:] * (1.0 - lam[..., 1:])
+    return gamma, gamma + shifted, np.exp(np.asarray(adt, np.float64))
+
+
+def m3_siso_scan(q, k, v, adt, dt, trap, q_bias, k_bias, cos, sin, D=None, z=None,
+                 reverse=False):
+    """Mamba-3 SISO in float64 -> (out time-major (b,l,h,dv), last_state (b,h,dv,dqk)).
+
+    q, k (b, l, g, dqk) with g dividing h; interleaved RoPE on (q + bias).
+    """
+    v = np.asarray(v, np.float64)
+    b, L, h, dv = v.shape
+    q, k = _m3_prep(q, k, v, adt, dt, trap, q_bias, k_bias, cos, sin, z, h,
+                    _rope_interleaved)
+    adt, dt, trap = (np.asarray(x, np.float64) for x in (adt, dt, trap))
+    zz = None if z is None else np.asarray(z, np.float64)
+    if reverse:
+        q, k, v = q[:, ::-1], k[:, ::-1], v[:, ::-1]
+        adt, dt, trap = adt[..., ::-1], dt[..., ::-1], trap[..., ::-1]
+        zz = None if zz is None else zz[:, ::-1]
+    gamma, scale, alpha = _gates(adt, dt, trap)
+    dqk = q.shape[-1]
+    S = np.zeros((b, h, dv, dqk))
+    out = np.empty((b, L, h, dv))
+    Dv = np.zeros(h) if D is None else np.asarray(D, np.float64)
+    for t in range(L):
+        qt, kt, vt = q[:, t], k[:, t], v[:, t]  # (b,h,dqk), (b,h,dqk), (b,h,dv)
+        y = alpha[:, :, t, None] * (S * qt[:, :, None, :]).sum(-1)
+        coef = Dv[None] + gamma[:, :, t] * (qt * kt).sum(-1)
+        out[:, t] = y + coef[..., None] * vt
+        S = alpha[:, :, t, None, None] * S \
+            + scale[:, :, t, None, None] * vt[..., None] * kt[..., None, :]
+    if zz is not None:
+        out = out * silu(zz)
+    if reverse:
+        out = out[:, ::-1]
+    return np.ascontiguousarray(out), S
+
+
+def m3_siso_dense(q, k, v, adt, dt, trap, q_bias, k_bias, cos, sin, D=None, z=None):
+    """Forward Mamba-3 SISO via the dual form, no state matrix.
+
+    y_t = sum_{s<=t} W_ts (q_t . k_s) v_s + D v_t, with
+    W_ts = exp(sum_{s<u<=t} adt_u) * scale_s for s < t and W_tt = gamma_t.
+    """
+    v = np.asarray(v, np.float64)
+    b, L, h, dv = v.shape
+    q, k = _m3_prep(q, k, v, adt, dt, trap, q_bias, k_bias, cos, sin, z, h,
+                    _rope_interleaved)
+    gamma, scale, _ = _gates(adt, dt, trap)
+    c = np.cumsum(np.asarray(adt, np.float64), axis=-1)  # (b, h, L)
+    G = np.einsum("bthn,bshn->bhts", q, k)  # (b, h, t, s)
+    decay = np.exp(c[..., :, None] - c[..., None, :])
+    W = np.where(np.tril(np.ones((L, L)), -1)[None, None] > 0,
+                 decay * scale[..., None, :], 0.0)
+    idx = np.arange(L)
+    W[..., idx, idx] = gamma
+    out = np.einsum("bhts,bshp->bthp", G * W, v)
+    if D is not None:
+        out = out + np.asarray(D, np.float64)[None, None, :, None] * v
+    if z is not None:
+        out = out * silu(z)
+    return out
+
+
+def m3_mimo_scan(q, k, v, adt, dt, trap, q_bias, k_bias, psi, zeta, phi, cos, sin,
+                 D=None, z=None, reverse=False):
+    """Mamba-3 MIMO in float64 -> (out time-major (b,l,h,dv), last_state).
+
+    q, k (b, l, r, g, dqk); split-halves RoPE; x_r = psi_r * v; gate per rank
+    silu(z * zeta_r); phi reduces the rank axis.
+    """
+    v = np.asarray(v, np.float64)
+    b, L, h, dv = v.shape
+    q, k = _m3_prep(q, k, v, adt, dt, trap, q_bias.transpose(1, 0, 2),
+                    k_bias.transpose(1, 0, 2), cos, sin, z, h, _rope_split)
+    # q, k: (b, l, r, h, dqk); biases were given (h, r, dqk)
+    adt, dt, trap = (np.asarray(x, np.float64) for x in (adt, dt, trap))
+    psi, zeta, phi = (np.asarray(x, np.float64).transpose(1, 0, 2) for x in (psi, zeta, phi))
+    x = v[:, :, None] * psi[None, None]  # (b, l, r, h, dv)
+    zz = None if z is None else np.asarray(z, np.float64)
+    if reverse:
+        q, k, x = q[:, ::-1], k[:, ::-1], x[:, ::-1]
+        adt, dt, trap = adt[..., ::-1], dt[..., ::-1], trap[..., ::-1]
+        zz = None if zz is None else zz[:, ::-1]
+    gamma, scale, alpha = _gates(adt, dt, trap)
+    r = q.shape[2]
+    dqk = q.shape[-1]
+    S = np.zeros((b, h, dv, dqk))
+    out = np.zeros((b, L, h, dv))
+    Dv = np.zeros(h) if D is None else np.asarray(D, np.float64)
+    for t in range(L):
+        qt, kt, xt = q[:, t], k[:, t], x[:, t]  # (b, r, h, *)
+        acc = np.empty((b, r, h, dv))
+        for ro in range(r):
+            y = (S * qt[:, ro, :, None, :]).sum(-1)  # (b, h, dv)
+            dsum = np.zeros((b, h, dv))
+            for ri in range(r):
+                dsum += (qt[:, ro] * kt[:, ri]).sum(-1)[..., None] * xt[:, ri]
+            acc[:, ro] = alpha[:, :, t, None] * y + gamma[:, :, t, None] * dsum \
+                + Dv[None, :, None] * xt[:, ro]
+        upd = np.zeros((b, h, dv, dqk))
+        for ri in range(r):
+            upd += xt[:, ri][..., None] * kt[:, ri][..., None, :]
+        S = alpha[:, :, t, None, None] * S + scale[:, :, t, None, None] * upd
+        for ro in range(r):
+            term = acc[:, ro] * phi[ro][None]
+            if zz is not None:
+                term = term * silu(zz[:, t] * zeta[ro][None])
+            out[:, t] += term
+    if reverse:
+        out = out[:, ::-1]
+    return np.ascontiguousarray(out), S
