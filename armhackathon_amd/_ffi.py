@@ -1,0 +1,205 @@
+"""ctypes bindings to libarm_scan_hip.so, the MI355X scan engine's C ABI.
+
+Mirrors the reference loader (python/arm_scan/_ffi.py:1-224): the same search
+order idea, the same ABI-version check, the same argtypes and the same
+error-code -> exception mapping. What differs is what ABI 8 differs in
+(include/arm_scan_hip.h): every tensor pointer is a device pointer, every entry
+point takes a trailing hipStream_t, ArmMamba3Dims carries `groups`, and there is
+one more entry point, arm_scan_ss2d_f32.
+
+Library search order:
+  1. the ARM_SCAN_LIB environment variable (full path to the library);
+  2. next to this package (where `make -C armhackathon_amd/csrc` writes it).
+
+There is no other implementation to fall back to: if the library is absent,
+`load()` raises OSError naming the paths it tried.
+"""
+
+import ctypes
+import os
+from pathlib import Path
+
+ABI_VERSION = 8
+
+LIB_NAME = "libarm_scan_hip.so"
+
+# arm-scan-ffi/src/lib.rs:53-58, plus code 6 (HIP launch / device error).
+ERROR_NAMES = {
+    0: "ok",
+    1: "null pointer",
+    2: "invalid dims/shapes",
+    3: "backend unavailable on this platform",
+    4: "bad backend/threading enum",
+    5: "panic inside kernel",
+    6: "HIP launch/device error",
+}
+
+BACKENDS = {"auto": 0, "scalar": 1, "neon": 2}
+THREADING = {"auto": 0, "sequential": 1, "seq": 1, "rayon": 2}
+SS2D_MERGES = {"none": 0, "sum": 1, "mean": 2}
+
+
+class ArmScanDims(ctypes.Structure):
+    # arm-scan-ffi/src/lib.rs:43-50 (unchanged in ABI 8)
+    _fields_ = [(n, ctypes.c_size_t) for n in ("batch", "dim", "len", "state", "groups")]
+
+
+class ArmMamba3Dims(ctypes.Structure):
+    # arm-scan-ffi/src/lib.rs:362-373 plus `groups` (ABI 8)
+    _fields_ = [(n, ctypes.c_size_t)
+                for n in ("batch", "heads", "dv", "dqk", "len", "rank", "groups")]
+
+
+class ArmSS2DDims(ctypes.Structure):
+    # ABI 8: the fused four-direction 2D scan
+    _fields_ = [(n, ctypes.c_size_t) for n in ("batch", "dim", "height", "width", "state")]
+
+
+class ArmScanError(RuntimeError):
+    """A nonzero return code from the C ABI; `.code` holds it."""
+
+    def __init__(self, fn, code, detail=""):
+        msg = f"{fn} failed with code {code}: {ERROR_NAMES.get(code, 'unknown')}"
+        if detail:
+            msg += f" ({detail})"
+        super().__init__(msg)
+        self.code = code
+
+
+def _candidate_paths():
+    env = os.environ.get("ARM_SCAN_LIB")
+    if env:
+        yield Path(env)
+    yield Path(__file__).resolve().parent / LIB_NAME
+
+
+_lib = None
+_lib_path = None
+
+_vp, _ci = ctypes.c_void_p, ctypes.c_int
+
+
+def _declare(lib):
+    lib.arm_scan_abi_version.restype = ctypes.c_uint32
+    lib.arm_scan_abi_version.argtypes = []
+    lib.arm_scan_last_error.restype = ctypes.c_char_p
+    lib.arm_scan_last_error.argtypes = []
+    f = lib.arm_scan_selective_scan_f32
+    f.restype = _ci
+    f.argtypes = [ctypes.POINTER(ArmScanDims),
+                  *([_vp] * 8),          # u delta a b c d_skip z delta_bias
+                  _ci, _ci, _ci, _ci,    # delta_softplus reverse backend threading
+                  _vp, _vp, _vp,         # out last_state h0
+                  _vp]                   # stream
+    f = lib.arm_scan_selective_scan_bidirectional_f32
+    f.restype = _ci
+    f.argtypes = [ctypes.POINTER(ArmScanDims),
+                  *([_vp] * 8),          # u delta a b c d_skip z delta_bias
+                  _ci, _ci, _ci,         # delta_softplus backend threading
+                  _vp, _vp, _vp, _vp,    # out_fwd out_bwd last_fwd last_bwd
+                  _vp]                   # stream
+    f = lib.arm_scan_mamba3_scan_f32
+    f.restype = _ci
+    f.argtypes = [ctypes.POINTER(ArmMamba3Dims),
+                  *([_vp] * 15),         # q k v adt dt trap q_bias k_bias cos sin d_skip z
+                                         # psi zeta phi
+                  _ci, _ci, _ci,         # reverse backend threading
+                  _vp, _vp, _vp,         # out last_state last_bx
+                  _vp]                   # stream
+    f = lib.arm_scan_ss2d_f32
+    f.restype = _ci
+    f.argtypes = [ctypes.POINTER(ArmSS2DDims),
+                  *([_vp] * 8),          # u delta a b4 c4 d_skip z delta_bias
+                  _ci, _ci,              # delta_softplus merge
+                  _vp, _vp,              # out last_states
+                  _vp]                   # stream
+
+
+def load():
+    """Load (once) and return the ctypes handle of libarm_scan_hip.so."""
+    global _lib, _lib_path
+    if _lib is not None:
+        return _lib
+    tried = []
+    for path in _candidate_paths():
+        tried.append(str(path))
+        if path.is_file():
+            lib = ctypes.CDLL(str(path))
+            version = lib.arm_scan_abi_version()
+            if version != ABI_VERSION:
+                raise RuntimeError(
+                    f"{path} has ABI version {version}, this package needs {ABI_VERSION}; "
+                    "rebuild with `make -C armhackathon_amd/csrc`")
+            _declare(lib)
+            _lib, _lib_path = lib, path
+            return lib
+    raise OSError("libarm_scan_hip.so not found; build it with "
+                  "`make -C armhackathon_amd/csrc` (searched: " + ", ".join(tried) + ")")
+
+
+def lib_path():
+    load()
+    return _lib_path
+
+
+def _check(fn, code):
+    if code != 0:
+        detail = load().arm_scan_last_error()
+        raise ArmScanError(fn, code, detail.decode() if detail else "")
+
+
+def _p(x):
+    return x or None
+
+
+def scan_raw(dims, ptr_u, ptr_delta, ptr_a, ptr_b, ptr_c, ptr_d_skip, ptr_z,
+             ptr_delta_bias, delta_softplus, backend, threading, ptr_out, ptr_last,
+             ptr_h0=0, *, reverse=False, stream=0):
+    """Call arm_scan_selective_scan_f32. Pointers are integer device addresses
+    (0 = null); `stream` is a hipStream_t handle (0 = the null stream).
+
+    `reverse` is keyword-only for the reason the reference gives
+    (python/arm_scan/_ffi.py:150-163): in C it sits mid-signature, so a
+    positional slot would let a caller shift `backend` into it.
+    """
+    code = load().arm_scan_selective_scan_f32(
+        ctypes.byref(dims), ptr_u, ptr_delta, ptr_a, ptr_b, ptr_c, _p(ptr_d_skip), _p(ptr_z),
+        _p(ptr_delta_bias), int(bool(delta_softplus)), int(bool(reverse)),
+        BACKENDS[backend], THREADING[threading], ptr_out, _p(ptr_last), _p(ptr_h0),
+        _p(stream))
+    _check("arm_scan_selective_scan_f32", code)
+
+
+def scan_bidir_raw(dims, ptr_u, ptr_delta, ptr_a, ptr_b, ptr_c, ptr_d_skip, ptr_z,
+                   ptr_delta_bias, delta_softplus, backend, threading, ptr_out_fwd,
+                   ptr_out_bwd, ptr_last_fwd=0, ptr_last_bwd=0, *, stream=0):
+    """Call arm_scan_selective_scan_bidirectional_f32 (both or neither last_*)."""
+    code = load().arm_scan_selective_scan_bidirectional_f32(
+        ctypes.byref(dims), ptr_u, ptr_delta, ptr_a, ptr_b, ptr_c, _p(ptr_d_skip), _p(ptr_z),
+        _p(ptr_delta_bias), int(bool(delta_softplus)), BACKENDS[backend],
+        THREADING[threading], ptr_out_fwd, ptr_out_bwd, _p(ptr_last_fwd), _p(ptr_last_bwd),
+        _p(stream))
+    _check("arm_scan_selective_scan_bidirectional_f32", code)
+
+
+def mamba3_raw(dims, ptrs, reverse, backend, threading, ptr_out, ptr_last_state,
+               ptr_last_bx, *, stream=0):
+    """Call arm_scan_mamba3_scan_f32 with the 15 input pointers in signature
+    order: q, k, v, adt, dt, trap, q_bias, k_bias, cos, sin, d_skip, z, psi,
+    zeta, phi (d_skip, z and the MIMO triple are nullable)."""
+    if len(ptrs) != 15:
+        raise ValueError(f"expected 15 input pointers, got {len(ptrs)}")
+    code = load().arm_scan_mamba3_scan_f32(
+        ctypes.byref(dims), *[_p(x) for x in ptrs], int(reverse), int(backend),
+        int(threading), ptr_out, _p(ptr_last_state), _p(ptr_last_bx), _p(stream))
+    _check("arm_scan_mamba3_scan_f32", code)
+
+
+def ss2d_raw(dims, ptr_u, ptr_delta, ptr_a, ptr_b4, ptr_c4, ptr_d_skip, ptr_z,
+             ptr_delta_bias, delta_softplus, merge, ptr_out, ptr_last_states=0, *, stream=0):
+    """Call arm_scan_ss2d_f32 (merge: "none" | "sum" | "mean")."""
+    code = load().arm_scan_ss2d_f32(
+        ctypes.byref(dims), ptr_u, ptr_delta, ptr_a, ptr_b4, ptr_c4, _p(ptr_d_skip), _p(ptr_z),
+        _p(ptr_delta_bias), int(bool(delta_softplus)), SS2D_MERGES[merge], ptr_out,
+        _p(ptr_last_states), _p(stream))
+    _check("arm_scan_ss2d_f32", code)

@@ -1,0 +1,281 @@
+// C ABI of libarm_scan_hip.so (declared in include/arm_scan_hip.h).
+//
+// Host-side validation follows the reference's FFI layer
+// (kernel/arm-scan-ffi/src/lib.rs:99-577) and its core checks
+// (arm-scan-core/src/lib.rs:181-249, mamba3/mod.rs:213-335): null pointers -> 1,
+// bad enums -> 4, zero / overflowing / non-dividing dims -> 2, unavailable
+// backend -> 3, all before any launch. Code 6 reports a HIP error.
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/arm_scan_hip.h"
+#include "scan_launch.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* where) {
+  return fail(ARM_SCAN_ERR_DEVICE, "%s: %s", where, hipGetErrorString(e));
+}
+
+bool mul_ok(size_t a, size_t b, size_t* out) { return !__builtin_mul_overflow(a, b, out); }
+bool prod_ok(std::initializer_list<size_t> xs) {
+  size_t acc = 1;
+  for (size_t x : xs)
+    if (!mul_ok(acc, x, &acc)) return false;
+  return true;
+}
+
+// backend 0 = auto (the HIP kernels); 1 scalar / 2 neon are CPU backends of the
+// reference. threading is accepted and ignored.
+int check_enums(int backend, int threading) {
+  if (backend < 0 || backend > 2 || threading < 0 || threading > 2)
+    return fail(ARM_SCAN_ERR_BAD_ENUM, "bad backend (%d) or threading (%d) enum", backend,
+                threading);
+  if (backend != 0)
+    return fail(ARM_SCAN_ERR_BACKEND_UNAVAILABLE,
+                "backend %d is a CPU backend; this library runs backend 0 (HIP)", backend);
+  return ARM_SCAN_OK;
+}
+
+int check_m1_dims(const ArmScanDims& d) {
+  if (!prod_ok({d.batch, d.dim, d.len}) || !prod_ok({d.batch, d.groups, d.state, d.len}) ||
+      !prod_ok({d.dim, d.state}) || !prod_ok({d.batch, d.dim, d.state}))
+    return fail(ARM_SCAN_ERR_INVALID_DIMS, "dims overflow size_t");
+  if (!d.batch || !d.dim || !d.len || !d.state || !d.groups)
+    return fail(ARM_SCAN_ERR_INVALID_DIMS, "a dimension is zero");
+  if (d.dim % d.groups)
+    return fail(ARM_SCAN_ERR_INVALID_DIMS, "groups (%zu) does not divide dim (%zu)", d.groups,
+                d.dim);
+  // device-side index arithmetic uses 32-bit row counts and 64-bit offsets
+  if (d.batch * d.dim > (1u << 30) || d.len > (1ull << 40))
+    return fail(ARM_SCAN_ERR_INVALID_DIMS, "problem too large for this build");
+  return ARM_SCAN_OK;
+}
+
+int run(hipError_t e, const char* where) {
+  if (e != hipSuccess) return hip_fail(e, where);
+  return ARM_SCAN_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+uint32_t arm_scan_abi_version(void) { return ARM_SCAN_ABI_VERSION; }
+
+const char* arm_scan_last_error(void) { return g_last_error.c_str(); }
+
+int arm_scan_selective_scan_f32(const ArmScanDims* dims, const float* u, const float* delta,
+                                const float* a, const float* b, const float* c,
+                                const float* d_skip, const float* z, const float* delta_bias,
+                                int delta_softplus, int reverse, int backend, int threading,
+                                float* out, float* last_state, const float* h0, void* stream) {
+  if (!dims || !u || !delta || !a || !b || !c || !out)
+    return fail(ARM_SCAN_ERR_NULL_POINTER, "a required pointer is null");
+  if (int rc = check_enums(backend, threading)) return rc;
+  if (int rc = check_m1_dims(*dims)) return rc;
+  armscan::M1Problem p{};
+  p.batch = dims->batch; p.dim = dims->dim; p.len = dims->len; p.state = dims->state;
+  p.groups = dims->groups;
+  p.u = u; p.delta = delta; p.A = a; p.B = b; p.C = c; p.D = d_skip; p.z = z;
+  p.bias = delta_bias; p.h0 = h0; p.out = out; p.last = last_state;
+  p.softplus = delta_softplus != 0; p.reverse = reverse != 0;
+  return run(armscan::m1_scan(p, (hipStream_t)stream), "selective_scan launch");
+}
+
+int arm_scan_selective_scan_bidirectional_f32(
+    const ArmScanDims* dims, const float* u, const float* delta, const float* a,
+    const float* b, const float* c, const float* d_skip, const float* z,
+    const float* delta_bias, int delta_softplus, int backend, int threading, float* out_fwd,
+    float* out_bwd, float* last_fwd, float* last_bwd, void* stream) {
+  if (!dims || !u || !delta || !a || !b || !c || !out_fwd || !out_bwd)
+    return fail(ARM_SCAN_ERR_NULL_POINTER, "a required pointer is null");
+  if (int rc = check_enums(backend, threading)) return rc;
+  if (int rc = check_m1_dims(*dims)) return rc;
+  if ((last_fwd == nullptr) != (last_bwd == nullptr))
+    return fail(ARM_SCAN_ERR_INVALID_DIMS, "last_fwd and last_bwd must both be set or null");
+  armscan::M1Problem p{};
+  p.batch = dims->batch; p.dim = dims->dim; p.len = dims->len; p.state = dims->state;
+  p.groups = dims->groups;
+  p.u = u; p.delta = delta; p.A = a; p.B = b; p.C = c; p.D = d_skip; p.z = z;
+  p.bias = delta_bias; p.softplus = delta_softplus != 0;
+  hipStream_t st = (hipStream_t)stream;
+  if (armscan::m1_bidir_fusable(p)) {
+    p.out = out_fwd; p.out2 = out_bwd; p.last = last_fwd; p.last2 = last_bwd;
+    return run(armscan::m1_bidir(p, st), "bidirectional launch");
+  }
+  // rows too long for one on-chip pass: the two directions separately
+  p.out = out_fwd; p.last = last_fwd; p.reverse = 0;
+  if (int rc = run(armscan::m1_scan(p, st), "bidirectional (forward) launch")) return rc;
+  p.out = out_bwd; p.last = last_bwd; p.reverse = 1;
+  return run(armscan::m1_scan(p, st), "bidirectional (reverse) launch");
+}
+
+int arm_scan_mamba3_scan_f32(const ArmMamba3Dims* dims, const float* q, const float* k,
+                             const float* v, const float* adt, const float* dt,
+                             const float* trap, const float* q_bias, const float* k_bias,
+                             const float* cos, const float* sin, const float* d_skip,
+                             const float* z, const float* mimo_psi, const float* mimo_zeta,
+                             const float* mimo_phi, int reverse, int backend, int threading,
+                             float* out, float* last_state, float* last_bx, void* stream) {
+  if (!dims || !q || !k || !v || !adt || !dt || !trap || !q_bias || !k_bias || !cos || !sin ||
+      !out)
+    return fail(ARM_SCAN_ERR_NULL_POINTER, "a required pointer is null");
+  const int n_mimo = (mimo_psi != nullptr) + (mimo_zeta != nullptr) + (mimo_phi != nullptr);
+  const bool mimo = n_mimo == 3;
+  if (n_mimo != 0 && n_mimo != 3)
+    return fail(ARM_SCAN_ERR_NULL_POINTER, "psi/zeta/phi must be all set or all null");
+  if (!mimo && (last_state == nullptr) != (last_bx == nullptr))
+    return fail(ARM_SCAN_ERR_NULL_POINTER, "last_state and last_bx must both be set or null");
+  if (int rc = check_enums(backend, threading)) return rc;
+  const ArmMamba3Dims& d = *dims;
+  if (d.dqk % 2) return fail(ARM_SCAN_ERR_INVALID_DIMS, "dqk (%zu) must be even", d.dqk);
+  if (!d.batch || !d.heads || !d.dv || !d.dqk || !d.len || !d.rank || !d.groups)
+    return fail(ARM_SCAN_ERR_INVALID_DIMS, "a dimension is zero");
+  if (!prod_ok({d.batch, d.len, d.rank, d.groups, d.dqk}) ||
+      !prod_ok({d.batch, d.len, d.heads, d.dv}) || !prod_ok({d.batch, d.heads, d.dv, d.dqk}) ||
+      !prod_ok({d.heads, d.rank, d.dqk}) || !prod_ok({d.heads, d.rank, d.dv}))
+    return fail(ARM_SCAN_ERR_INVALID_DIMS, "dims overflow size_t");
+  if (d.heads % d.groups)
+    return fail(ARM_SCAN_ERR_INVALID_DIMS, "groups (%zu) does not divide heads (%zu)", d.groups,
+                d.heads);
+  if (d.rank > 1 && !mimo)
+    return fail(ARM_SCAN_ERR_INVALID_DIMS, "rank > 1 requires the MIMO projections");
+  if (mimo && last_bx)
+    return fail(ARM_SCAN_ERR_INVALID_DIMS, "MIMO has no last_bx carry (rank > 1 k per step)");
+  if (d.len > (1u << 30) || d.batch * d.heads > (1u << 30))
+    return fail(ARM_SCAN_ERR_INVALID_DIMS, "problem too large for this build");
+  const size_t need = d.dv * (d.dqk + 1) + 2 * d.rank * (d.dqk + d.dv) + d.rank * d.rank + 4;
+  if (need > armscan::m3_max_state())
+    return fail(ARM_SCAN_ERR_INVALID_DIMS, "state dv*dqk (%zu x %zu) exceeds on-chip capacity",
+                d.dv, d.dqk);
+  armscan::M3Problem p{};
+  p.batch = d.batch; p.heads = d.heads; p.dv = d.dv; p.dqk = d.dqk; p.len = d.len;
+  p.rank = d.rank; p.groups = d.groups;
+  p.q = q; p.k = k; p.v = v; p.adt = adt; p.dt = dt; p.trap = trap; p.q_bias = q_bias;
+  p.k_bias = k_bias; p.cos = cos; p.sin = sin; p.D = d_skip; p.z = z;
+  p.psi = mimo_psi; p.zeta = mimo_zeta; p.phi = mimo_phi;
+  p.out = out; p.last_state = last_state; p.last_bx = last_bx; p.reverse = reverse != 0;
+  return run(armscan::m3_scan(p, (hipStream_t)stream), "mamba3 launch");
+}
+
+int arm_scan_ss2d_f32(const ArmSS2DDims* dims, const float* u, const float* delta,
+                      const float* a, const float* b4, const float* c4, const float* d_skip,
+                      const float* z, const float* delta_bias, int delta_softplus, int merge,
+                      float* out, float* last_states, void* stream) {
+  if (!dims || !u || !delta || !a || !b4 || !c4 || !out)
+    return fail(ARM_SCAN_ERR_NULL_POINTER, "a required pointer is null");
+  if (merge < 0 || merge > 2) return fail(ARM_SCAN_ERR_BAD_ENUM, "bad merge enum %d", merge);
+  const ArmSS2DDims& d = *dims;
+  if (!d.batch || !d.dim || !d.height || !d.width || !d.state)
+    return fail(ARM_SCAN_ERR_INVALID_DIMS, "a dimension is zero");
+  if (!prod_ok({4, d.batch, d.dim, d.height, d.width}) ||
+      !prod_ok({4, d.batch, d.state, d.height, d.width}) || d.height > (1u << 20) ||
+      d.width > (1u << 20) || d.batch * d.dim > (1u << 30))
+    return fail(ARM_SCAN_ERR_INVALID_DIMS, "dims overflow or too large");
+  hipStream_t st = (hipStream_t)stream;
+  const size_t H = d.height, W = d.width, L = H * W;
+  const size_t plane = d.batch * d.dim * L;    // one (b, d, H, W) plane
+  const size_t bcp = d.batch * d.state * L;    // one direction's B or C
+  const size_t bdn = d.batch * d.dim * d.state;
+
+  armscan::M1Problem p{};
+  p.batch = d.batch; p.dim = d.dim; p.len = L; p.state = d.state; p.groups = 1;
+  p.A = a; p.D = d_skip; p.bias = delta_bias; p.softplus = delta_softplus != 0;
+
+  // Scratch: the column-major views of u, delta, z and the column directions'
+  // B/C, plus the column pair's outputs before they are transposed back.
+  const size_t n_scratch = plane * (z ? 3 : 2) + 4 * bcp + 2 * plane;
+  float* scratch = nullptr;
+  hipError_t e = hipMallocAsync((void**)&scratch, n_scratch * sizeof(float), st);
+  if (e != hipSuccess) return hip_fail(e, "ss2d scratch allocation");
+  float* uT = scratch;
+  float* dT = uT + plane;
+  float* zT = z ? dT + plane : nullptr;
+  float* bT = (z ? zT : dT) + plane;  // b4[2], b4[3], c4[2], c4[3] transposed
+  float* colf = bT + 4 * bcp;
+  float* colb = colf + plane;
+
+  // One traversal pair (forward + reverse over the same ordering). `sum` asks
+  // for of = fwd + bwd (ob unused); otherwise of / ob receive the two planes.
+  auto pair = [&](const float* uu, const float* dd, const float* zz, const float* Bf,
+                  const float* Bb, const float* Cf, const float* Cb, float* of, float* ob,
+                  float* lf, float* lb, bool sum, float* tmp) -> hipError_t {
+    armscan::M1Problem q = p;
+    q.u = uu; q.delta = dd; q.z = zz;
+    q.B = Bf; q.C = Cf; q.B2 = Bb; q.C2 = Cb;
+    if (armscan::m1_bidir_fusable(q)) {
+      q.out = of; q.out2 = sum ? nullptr : ob; q.last = lf; q.last2 = lb;
+      q.merge = sum ? 1 : 0;
+      return armscan::m1_bidir(q, st);
+    }
+    q.B2 = q.C2 = nullptr;
+    q.out = of; q.last = lf; q.reverse = 0;
+    hipError_t r = armscan::m1_scan(q, st);
+    if (r != hipSuccess) return r;
+    q.B = Bb; q.C = Cb; q.out = sum ? tmp : ob; q.last = lb; q.reverse = 1;
+    r = armscan::m1_scan(q, st);
+    if (r != hipSuccess || !sum) return r;
+    return armscan::add_inplace(of, tmp, (long long)plane, st);
+  };
+
+  float* ls = last_states;
+  auto last_at = [&](int k) { return ls ? ls + (size_t)k * bdn : nullptr; };
+  const bool none = merge == 0;
+  int rc = ARM_SCAN_OK;
+  do {
+    // column-major views for the column directions
+    const long long bd = (long long)(d.batch * d.dim), bn = (long long)(d.batch * d.state);
+    if ((e = armscan::transpose_hw(u, uT, bd, (int)H, (int)W, false, st))) break;
+    if ((e = armscan::transpose_hw(delta, dT, bd, (int)H, (int)W, false, st))) break;
+    if (z && (e = armscan::transpose_hw(z, zT, bd, (int)H, (int)W, false, st))) break;
+    for (int kk = 0; kk < 2 && !e; ++kk) {
+      e = armscan::transpose_hw(b4 + (2 + kk) * bcp, bT + kk * bcp, bn, (int)H, (int)W, false,
+                                st);
+      if (!e)
+        e = armscan::transpose_hw(c4 + (2 + kk) * bcp, bT + (2 + kk) * bcp, bn, (int)H, (int)W,
+                                  false, st);
+    }
+    if (e) break;
+    // row pair over the row-major flattening: planes 0 / 1, or their sum into out
+    e = pair(u, delta, z, b4, b4 + bcp, c4, c4 + bcp, out, none ? out + plane : nullptr,
+             last_at(0), last_at(1), !none, colf);
+    if (e) break;
+    // column pair on the transposed grid, then back to (H, W)
+    e = pair(uT, dT, zT, bT, bT + bcp, bT + 2 * bcp, bT + 3 * bcp, colf, none ? colb : nullptr,
+             last_at(2), last_at(3), !none, colb);
+    if (e) break;
+    if (none) {
+      if ((e = armscan::transpose_hw(colf, out + 2 * plane, bd, (int)W, (int)H, false, st)))
+        break;
+      e = armscan::transpose_hw(colb, out + 3 * plane, bd, (int)W, (int)H, false, st);
+    } else {
+      if ((e = armscan::transpose_hw(colf, out, bd, (int)W, (int)H, true, st))) break;
+      if (merge == 2) e = armscan::scale_inplace(out, (long long)plane, 0.25f, st);
+    }
+  } while (false);
+  if (e != hipSuccess) rc = hip_fail(e, "ss2d launch");
+  hipError_t fe = hipFreeAsync(scratch, st);
+  if (rc == ARM_SCAN_OK && fe != hipSuccess) rc = hip_fail(fe, "ss2d scratch free");
+  return rc;
+}
+
+}  // extern "C"

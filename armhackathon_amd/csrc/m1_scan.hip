@@ -1,0 +1,682 @@
+// Mamba-1 selective scan on MI355X (gfx950).
+//
+// Semantics are the reference's scalar::scan (kernel/arm-scan-core/src/scalar.rs:11-89)
+// and scalar::scan_bidirectional (scalar.rs:114-201):
+//   h_n <- exp(dt*A_dn) h_n + dt*u*B_gn ;  y = sum_n C_gn h_n ; (y + D u) silu(z)
+// with dt = softplus(delta + bias) when asked, reverse as an index mode.
+//
+// Work decomposition (one workgroup = R channel rows x S time segments, one
+// wave per (row, segment)):
+//   * a lane owns I consecutive timesteps ("items") of one row; a wave covers
+//     64*I steps, a row-chunk CH = S*64*I steps; longer rows loop over chunks
+//     with the per-state carry kept in LDS;
+//   * per state n: each lane discretises its items (a = 2^(dt*A*log2e),
+//     b = dt*u*B), folds them into one affine map, the wave combines the maps
+//     with a DPP Hillis-Steele scan, segments combine through LDS, then each
+//     lane replays its items from the resulting h_in accumulating y += C*h.
+//     exp(dt*A) is evaluated exactly once per (item, state);
+//   * B/C rows of the current state are shared by the R rows of the
+//     workgroup (same batch and group): staged once into LDS, triple-buffered
+//     so one barrier per state suffices, and read back as 16-byte vectors with
+//     a 4-float pad per lane block (bank-conflict free);
+//   * u, delta, z, out move with 16-byte vector loads/stores straight between
+//     HBM and registers (each lane's block is one 128-B line at I = 32).
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+
+#include "scan_common.h"
+#include "scan_launch.h"
+
+namespace armscan {
+
+namespace {
+
+constexpr int kPad = 4;  // floats of padding per lane block in LDS
+
+struct M1Args {
+  const float* u;
+  const float* delta;
+  const float* A;
+  const float* B;   // forward-direction B (b, g, n, L)
+  const float* C;
+  const float* B2;  // backward-direction B/C (bidirectional kernel only)
+  const float* C2;
+  const float* D;
+  const float* z;
+  const float* bias;
+  const float* h0;
+  float* out;
+  float* last;
+  float* out2;   // backward output (bidirectional)
+  float* last2;
+  long long L;
+  int dim, N, groups, group_size, S;
+  int softplus, reverse, vec, merge;  // merge: bidir writes out = f + b (no out2)
+};
+
+// Scan-order item loads: item i of a lane whose first scan index is `sb`.
+// Forward: t = sb + i. Reverse: t = L - 1 - sb - i (a contiguous block read
+// backwards). Out-of-range items get `fill`.
+template <int I>
+__device__ __forceinline__ void load_items(const float* __restrict__ row, long long L,
+                                           long long sb, bool reverse, bool vec, float fill,
+                                           float (&v)[I]) {
+  if (!reverse) {
+    if (vec && sb + I <= L) {
+#pragma unroll
+      for (int q = 0; q < I / 4; ++q) {
+        const float4 x = *reinterpret_cast<const float4*>(row + sb + 4 * q);
+        v[4 * q] = x.x; v[4 * q + 1] = x.y; v[4 * q + 2] = x.z; v[4 * q + 3] = x.w;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < I; ++i) v[i] = (sb + i < L) ? row[sb + i] : fill;
+    }
+  } else {
+    const long long t0 = L - sb - I;  // memory start of the block
+    if (vec && t0 >= 0) {
+#pragma unroll
+      for (int q = 0; q < I / 4; ++q) {
+        const float4 x = *reinterpret_cast<const float4*>(row + t0 + 4 * q);
+        v[I - 1 - 4 * q] = x.x; v[I - 2 - 4 * q] = x.y;
+        v[I - 3 - 4 * q] = x.z; v[I - 4 - 4 * q] = x.w;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < I; ++i) {
+        const long long t = L - 1 - sb - i;
+        v[i] = (t >= 0) ? row[t] : fill;
+      }
+    }
+  }
+}
+
+template <int I>
+__device__ __forceinline__ void store_items(float* __restrict__ row, long long L, long long sb,
+                                            bool reverse, bool vec, const float (&v)[I]) {
+  if (!reverse) {
+    if (vec && sb + I <= L) {
+#pragma unroll
+      for (int q = 0; q < I / 4; ++q)
+        *reinterpret_cast<float4*>(row + sb + 4 * q) =
+            make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < I; ++i)
+        if (sb + i < L) row[sb + i] = v[i];
+    }
+  } else {
+    const long long t0 = L - sb - I;
+    if (vec && t0 >= 0) {
+#pragma unroll
+      for (int q = 0; q < I / 4; ++q)
+        *reinterpret_cast<float4*>(row + t0 + 4 * q) =
+            make_float4(v[I - 1 - 4 * q], v[I - 2 - 4 * q], v[I - 3 - 4 * q], v[I - 4 - 4 * q]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < I; ++i) {
+        const long long t = L - 1 - sb - i;
+        if (t >= 0) row[t] = v[i];
+      }
+    }
+  }
+}
+
+// Four consecutive memory positions t0..t0+3 of one B/C row, zero outside [0, L).
+__device__ __forceinline__ float4 load4(const float* __restrict__ p, long long t0, long long L,
+                                        bool vec) {
+  if (vec && t0 >= 0 && t0 + 4 <= L) return *reinterpret_cast<const float4*>(p + t0);
+  float4 r;
+  r.x = (t0 >= 0 && t0 < L) ? p[t0] : 0.0f;
+  r.y = (t0 + 1 >= 0 && t0 + 1 < L) ? p[t0 + 1] : 0.0f;
+  r.z = (t0 + 2 >= 0 && t0 + 2 < L) ? p[t0 + 2] : 0.0f;
+  r.w = (t0 + 3 >= 0 && t0 + 3 < L) ? p[t0 + 3] : 0.0f;
+  return r;
+}
+
+template <int I>
+__device__ __forceinline__ int lds_pos(int q) {
+  return (q / I) * (I + kPad) + (q % I);
+}
+
+// dt for each item: (delta + bias), softplus when asked; 0 for padding items
+// so that they act as the identity map (a = 1, b = 0).
+template <int I>
+__device__ __forceinline__ void discretize(const M1Args& p, const float* urow, const float* drow,
+                                           long long sb, bool reverse, float bias,
+                                           float (&dt)[I], float (&du)[I], float& sumdt) {
+  float uu[I];
+  load_items<I>(drow, p.L, sb, reverse, p.vec, 0.0f, dt);
+  load_items<I>(urow, p.L, sb, reverse, p.vec, 0.0f, uu);
+  sumdt = 0.0f;
+#pragma unroll
+  for (int i = 0; i < I; ++i) {
+    const long long si = sb + i;
+    float x = dt[i] + bias;
+    if (p.softplus) x = softplus(x);
+    x = (si < p.L) ? x : 0.0f;
+    dt[i] = x;
+    du[i] = x * uu[i];
+    sumdt += x;
+  }
+}
+
+// Epilogue (y + D u) * silu(z), applied per item (scalar.rs:75-80).
+template <int I>
+__device__ __forceinline__ void epilogue(const M1Args& p, const float* urow, const float* zrow,
+                                         long long sb, bool reverse, float dskip, float (&y)[I]) {
+  if (p.D) {
+    float uu[I];
+    load_items<I>(urow, p.L, sb, reverse, p.vec, 0.0f, uu);
+#pragma unroll
+    for (int i = 0; i < I; ++i) y[i] = fmaf(dskip, uu[i], y[i]);
+  }
+  if (zrow) {
+    float zz[I];
+    load_items<I>(zrow, p.L, sb, reverse, p.vec, 0.0f, zz);
+#pragma unroll
+    for (int i = 0; i < I; ++i) y[i] = y[i] * silu(zz[i]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Single-direction scan (forward or reverse index mode), any L.
+// LDS: B and C triple buffers [3][CHP] each, segment aggregates [2][R*S][2],
+// per-wave carries [R*S][N].
+template <int I, int MAXT>
+__global__ void __launch_bounds__(MAXT) m1_scan_kernel(M1Args p) {
+  constexpr int R = I / 4;
+  constexpr int LB = I + kPad;
+  extern __shared__ float smem[];
+  const int S = p.S;
+  const int CH = S * 64 * I;
+  const int CHP = S * 64 * LB;
+  float* sB = smem;
+  float* sC = smem + 3 * CHP;
+  float* sAgg = smem + 6 * CHP;
+  float* sCarry = sAgg + 4 * R * S;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = w / S, s = w - r * S;
+  const int wg_per_batch = p.dim / R;
+  const int bi = blockIdx.x / wg_per_batch;
+  const int d = (blockIdx.x - bi * wg_per_batch) * R + r;
+  const int g = ((blockIdx.x - bi * wg_per_batch) * R) / p.group_size;
+  const long long L = p.L;
+  const int N = p.N;
+  const bool rev = p.reverse != 0;
+  const long long row = (long long)bi * p.dim + d;
+  const float* urow = p.u + row * L;
+  const float* drow = p.delta + row * L;
+  const float* zrow = p.z ? p.z + row * L : nullptr;
+  float* orow = p.out + row * L;
+  const float* Bgrp = p.B + ((long long)bi * p.groups + g) * N * L;
+  const float* Cgrp = p.C + ((long long)bi * p.groups + g) * N * L;
+  const float* Arow = p.A + (long long)d * N;
+  const float bias = p.bias ? p.bias[d] : 0.0f;
+  const float dskip = p.D ? p.D[d] : 0.0f;
+
+  for (int n = lane; n < N; n += 64) sCarry[w * N + n] = p.h0 ? p.h0[row * N + n] : 0.0f;
+
+  const long long nchunks = (L + CH - 1) / CH;
+  // staging geometry: thread `tid` moves memory positions tbase + 4 tid .. +3
+  auto tbase_of = [&](long long c) { return rev ? (L - (c + 1) * CH) : c * CH; };
+  auto qpos = [&](void) { return rev ? (CH - 4 - 4 * tid) : 4 * tid; };
+  auto stage_store = [&](int buf, float4 vb, float4 vc) {
+    const int q0 = lds_pos<I>(qpos());
+    if (rev) {
+      vb = make_float4(vb.w, vb.z, vb.y, vb.x);
+      vc = make_float4(vc.w, vc.z, vc.y, vc.x);
+    }
+    *reinterpret_cast<float4*>(sB + buf * CHP + q0) = vb;
+    *reinterpret_cast<float4*>(sC + buf * CHP + q0) = vc;
+  };
+  {
+    const long long t0 = tbase_of(0) + 4 * tid;
+    stage_store(0, load4(Bgrp, t0, L, p.vec), load4(Cgrp, t0, L, p.vec));
+  }
+  __syncthreads();
+
+  int k = 0;  // (chunk, state) step counter: LDS buffer k % 3, aggregate slot k & 1
+  for (long long c = 0; c < nchunks; ++c) {
+    const long long sb = c * CH + (long long)(s * 64 + lane) * I;
+    float dt[I], du[I], y[I];
+    float sumdt;
+    discretize<I>(p, urow, drow, sb, rev, bias, dt, du, sumdt);
+#pragma unroll
+    for (int i = 0; i < I; ++i) y[i] = 0.0f;
+
+    for (int n = 0; n < N; ++n, ++k) {
+      // prefetch B/C of the next (chunk, state) step into registers
+      const bool has_next = (n + 1 < N) || (c + 1 < nchunks);
+      const int nn = (n + 1 < N) ? n + 1 : 0;
+      const long long cn = (n + 1 < N) ? c : c + 1;
+      float4 nb = make_float4(0.f, 0.f, 0.f, 0.f), nc = nb;
+      if (has_next) {
+        const long long t0 = tbase_of(cn) + 4 * tid;
+        nb = load4(Bgrp + (long long)nn * L, t0, L, p.vec);
+        nc = load4(Cgrp + (long long)nn * L, t0, L, p.vec);
+      }
+      const int buf = k % 3;
+      const float a2 = Arow[n] * kLog2e;
+      const float* lb = sB + buf * CHP + (s * 64 + lane) * LB;
+      float a[I], b[I];
+      float bt = 0.0f;
+#pragma unroll
+      for (int q = 0; q < I / 4; ++q) {
+        const float4 bv = *reinterpret_cast<const float4*>(lb + 4 * q);
+        const float bb[4] = {bv.x, bv.y, bv.z, bv.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int i = 4 * q + j;
+          a[i] = ex2(dt[i] * a2);
+          b[i] = du[i] * bb[j];
+          bt = fmaf(a[i], bt, b[i]);
+        }
+      }
+      float ai = ex2(a2 * sumdt), bi_ = bt;
+      wave_scan_up(ai, bi_);
+      const float ae = dpp<kWaveShr1, 0xF>(1.0f, ai);
+      const float be = dpp<kWaveShr1, 0xF>(0.0f, bi_);
+      const float aw = readlane(ai, 63), bw = readlane(bi_, 63);
+      if (S > 1 && lane == 0) {
+        sAgg[((k & 1) * R * S + w) * 2 + 0] = aw;
+        sAgg[((k & 1) * R * S + w) * 2 + 1] = bw;
+      }
+      if (has_next) stage_store((k + 1) % 3, nb, nc);
+      __syncthreads();
+      const float hc = sCarry[w * N + n];
+      float hseg = hc, hnew;
+      if (S > 1) {
+        const float* ag = sAgg + ((k & 1) * R * S + r * S) * 2;
+        float fa = 1.0f, fb = 0.0f;
+        for (int j = 0; j < S; ++j) {
+          if (j == s) hseg = fmaf(fa, hc, fb);
+          const float ja = ag[2 * j], jb = ag[2 * j + 1];
+          fb = fmaf(ja, fb, jb);
+          fa = fa * ja;
+        }
+        hnew = fmaf(fa, hc, fb);
+      } else {
+        hnew = fmaf(aw, hc, bw);
+      }
+      float h = fmaf(ae, hseg, be);
+      const float* lc = sC + buf * CHP + (s * 64 + lane) * LB;
+#pragma unroll
+      for (int q = 0; q < I / 4; ++q) {
+        const float4 cv = *reinterpret_cast<const float4*>(lc + 4 * q);
+        const float cc[4] = {cv.x, cv.y, cv.z, cv.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int i = 4 * q + j;
+          h = fmaf(a[i], h, b[i]);
+          y[i] = fmaf(cc[j], h, y[i]);
+        }
+      }
+      if (lane == 0) sCarry[w * N + n] = hnew;
+    }
+    epilogue<I>(p, urow, zrow, sb, rev, dskip, y);
+    store_items<I>(orow, L, sb, rev, p.vec, y);
+  }
+  if (p.last && s == 0) {
+    for (int n = lane; n < N; n += 64) p.last[row * N + n] = sCarry[w * N + n];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Fused bidirectional scan: one chunk covers the whole row (CH >= L). exp(dt*A)
+// is shared; each direction has its own B/C (identical for the reference's
+// bidirectional entry point, distinct for the four-direction 2D scan).
+// LDS: Bf, Cf, Bb, Cb triple buffers [3][CHP] each, aggregates [2][2][R*S][2].
+template <int I, int MAXT>
+__global__ void __launch_bounds__(MAXT) m1_bidir_kernel(M1Args p) {
+  constexpr int R = I / 4;
+  constexpr int LB = I + kPad;
+  extern __shared__ float smem[];
+  const int S = p.S;
+  const int CHP = S * 64 * LB;
+  const bool sep = (p.B2 != p.B) || (p.C2 != p.C);  // distinct backward B/C
+  float* sBf = smem;
+  float* sCf = smem + 3 * CHP;
+  float* sBb = smem + 6 * CHP;
+  float* sCb = smem + 9 * CHP;
+  float* sAgg = smem + (sep ? 12 : 6) * CHP;  // [2 slots][2 dirs][R*S][2]
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = w / S, s = w - r * S;
+  const int wg_per_batch = p.dim / R;
+  const int bi = blockIdx.x / wg_per_batch;
+  const int d = (blockIdx.x - bi * wg_per_batch) * R + r;
+  const int g = ((blockIdx.x - bi * wg_per_batch) * R) / p.group_size;
+  const long long L = p.L;
+  const int N = p.N;
+  const long long row = (long long)bi * p.dim + d;
+  const float* urow = p.u + row * L;
+  const float* drow = p.delta + row * L;
+  const float* zrow = p.z ? p.z + row * L : nullptr;
+  const long long goff = ((long long)bi * p.groups + g) * N * L;
+  const float* Arow = p.A + (long long)d * N;
+  const float bias = p.bias ? p.bias[d] : 0.0f;
+  const float dskip = p.D ? p.D[d] : 0.0f;
+  const int RS = R * S;
+
+  auto stage = [&](int buf, int n) {
+    const long long t0 = 4LL * tid;
+    const int q0 = lds_pos<I>(4 * tid);
+    const long long no = goff + (long long)n * L;
+    *reinterpret_cast<float4*>(sBf + buf * CHP + q0) = load4(p.B + no, t0, L, p.vec);
+    *reinterpret_cast<float4*>(sCf + buf * CHP + q0) = load4(p.C + no, t0, L, p.vec);
+    if (sep) {
+      *reinterpret_cast<float4*>(sBb + buf * CHP + q0) = load4(p.B2 + no, t0, L, p.vec);
+      *reinterpret_cast<float4*>(sCb + buf * CHP + q0) = load4(p.C2 + no, t0, L, p.vec);
+    }
+  };
+  stage(0, 0);
+  __syncthreads();
+
+  const long long sb = (long long)(s * 64 + lane) * I;
+  float dt[I], du[I], yf[I], yb[I];
+  float sumdt;
+  discretize<I>(p, urow, drow, sb, false, bias, dt, du, sumdt);
+#pragma unroll
+  for (int i = 0; i < I; ++i) { yf[i] = 0.0f; yb[i] = 0.0f; }
+
+  for (int n = 0; n < N; ++n) {
+    const int buf = n % 3;
+    const float a2 = Arow[n] * kLog2e;
+    const float* lbf = sBf + buf * CHP + (s * 64 + lane) * LB;
+    const float* lbb = (sep ? sBb : sBf) + buf * CHP + (s * 64 + lane) * LB;
+    float a[I], bf[I], bb[I];
+    float btf = 0.0f, btb = 0.0f;
+#pragma unroll
+    for (int q = 0; q < I / 4; ++q) {
+      const float4 v = *reinterpret_cast<const float4*>(lbf + 4 * q);
+      const float vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int i = 4 * q + j;
+        a[i] = ex2(dt[i] * a2);
+        bf[i] = du[i] * vv[j];
+        btf = fmaf(a[i], btf, bf[i]);
+      }
+    }
+    if (sep) {
+#pragma unroll
+      for (int q = 0; q < I / 4; ++q) {
+        const float4 v = *reinterpret_cast<const float4*>(lbb + 4 * q);
+        bb[4 * q] = du[4 * q] * v.x; bb[4 * q + 1] = du[4 * q + 1] * v.y;
+        bb[4 * q + 2] = du[4 * q + 2] * v.z; bb[4 * q + 3] = du[4 * q + 3] * v.w;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < I; ++i) bb[i] = bf[i];
+    }
+#pragma unroll
+    for (int i = I - 1; i >= 0; --i) btb = fmaf(a[i], btb, bb[i]);
+    const float P = ex2(a2 * sumdt);
+    float af = P, bfw = btf, ab = P, bbw = btb;
+    wave_scan_up(af, bfw);
+    wave_scan_down(ab, bbw, lane);
+    const float aef = dpp<kWaveShr1, 0xF>(1.0f, af);
+    const float bef = dpp<kWaveShr1, 0xF>(0.0f, bfw);
+    const float aeb = dpp<kWaveShl1, 0xF>(1.0f, ab);
+    const float beb = dpp<kWaveShl1, 0xF>(0.0f, bbw);
+    const float awf = readlane(af, 63), bwf = readlane(bfw, 63);
+    const float awb = readlane(ab, 0), bwb = readlane(bbw, 0);
+    const int slot = n & 1;
+    if (S > 1 && lane == 0) {
+      float* ag = sAgg + (slot * 2 * RS + w) * 2;
+      ag[0] = awf; ag[1] = bwf;
+      ag[2 * RS] = awb; ag[2 * RS + 1] = bwb;
+    }
+    if (n + 1 < N) stage((n + 1) % 3, n + 1);
+    __syncthreads();
+    float hsf = 0.0f, hsb = 0.0f, fin_f, fin_b;
+    if (S > 1) {
+      const float* agf = sAgg + (slot * 2 * RS + r * S) * 2;
+      const float* agb = agf + 2 * RS;
+      float fb = 0.0f;
+      for (int j = 0; j < S; ++j) {
+        if (j == s) hsf = fb;
+        fb = fmaf(agf[2 * j], fb, agf[2 * j + 1]);
+      }
+      fin_f = fb;
+      float gb = 0.0f;
+      for (int j = S - 1; j >= 0; --j) {
+        if (j == s) hsb = gb;
+        gb = fmaf(agb[2 * j], gb, agb[2 * j + 1]);
+      }
+      fin_b = gb;
+    } else {
+      fin_f = bwf;
+      fin_b = bwb;
+    }
+    float h = fmaf(aef, hsf, bef);
+    const float* lcf = sCf + buf * CHP + (s * 64 + lane) * LB;
+    const float* lcb = (sep ? sCb : sCf) + buf * CHP + (s * 64 + lane) * LB;
+#pragma unroll
+    for (int q = 0; q < I / 4; ++q) {
+      const float4 v = *reinterpret_cast<const float4*>(lcf + 4 * q);
+      const float cc[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int i = 4 * q + j;
+        h = fmaf(a[i], h, bf[i]);
+        yf[i] = fmaf(cc[j], h, yf[i]);
+      }
+    }
+    h = fmaf(aeb, hsb, beb);
+#pragma unroll
+    for (int q = I / 4 - 1; q >= 0; --q) {
+      const float4 v = *reinterpret_cast<const float4*>(lcb + 4 * q);
+      const float cc[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int j = 3; j >= 0; --j) {
+        const int i = 4 * q + j;
+        h = fmaf(a[i], h, bb[i]);
+        yb[i] = fmaf(cc[j], h, yb[i]);
+      }
+    }
+    if (p.last && s == 0 && lane == 0) {
+      p.last[row * N + n] = fin_f;
+      p.last2[row * N + n] = fin_b;
+    }
+  }
+  epilogue<I>(p, urow, zrow, sb, false, dskip, yf);
+  epilogue<I>(p, urow, zrow, sb, false, dskip, yb);
+  if (p.merge) {
+#pragma unroll
+    for (int i = 0; i < I; ++i) yf[i] += yb[i];
+    store_items<I>(p.out + row * L, L, sb, false, p.vec, yf);
+  } else {
+    store_items<I>(p.out + row * L, L, sb, false, p.vec, yf);
+    store_items<I>(p.out2 + row * L, L, sb, false, p.vec, yb);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Grid helpers for the 2D scan: (rows, H, W) <-> (rows, W, H) through LDS tiles.
+__global__ void __launch_bounds__(256) transpose_hw_kernel(const float* __restrict__ in,
+                                                           float* __restrict__ out, int H,
+                                                           int W, int accumulate) {
+  __shared__ float tile[32][33];
+  const long long plane = (long long)blockIdx.z * H * W;
+  const int i0 = blockIdx.y * 32, j0 = blockIdx.x * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8
+  for (int k = ty; k < 32; k += 8) {
+    const int i = i0 + k, j = j0 + tx;
+    if (i < H && j < W) tile[k][tx] = in[plane + (long long)i * W + j];
+  }
+  __syncthreads();
+  for (int k = ty; k < 32; k += 8) {
+    const int j = j0 + k, i = i0 + tx;  // out is (W, H)
+    if (i < H && j < W) {
+      float* o = out + plane + (long long)j * H + i;
+      const float v = tile[tx][k];
+      *o = accumulate ? (*o + v) : v;
+    }
+  }
+}
+
+__global__ void __launch_bounds__(256) scale_kernel(float* __restrict__ x, long long n,
+                                                    float scale) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) x[i] *= scale;
+}
+
+__global__ void __launch_bounds__(256) add_kernel(float* __restrict__ x,
+                                                  const float* __restrict__ y, long long n) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) x[i] += y[i];
+}
+
+struct Choice {
+  int I, S;
+};
+
+// Pick items per lane (I) and segments per row (S). More segments buy
+// parallelism for short batches; larger I amortises the per-state wave scan
+// (~6 item-equivalents) over more items. R = I/4 rows share B/C and must lie
+// in one group.
+Choice choose(long long rows, long long L, long long group_size, bool single_chunk) {
+  Choice best{4, 1};
+  double best_score = -1.0;
+  for (int I : {32, 16, 8, 4}) {
+    const int R = I / 4;
+    if (group_size % R) continue;
+    const int smax = (I == 32) ? 1 : 16 / R;
+    for (int S = 1; S <= smax; S *= 2) {
+      const long long CH = (long long)S * 64 * I;
+      const long long lds_floats = (long long)S * 64 * (I + kPad) * (single_chunk ? 12 : 6);
+      if (lds_floats * 4 > 96 * 1024) continue;
+      if (single_chunk && (CH < L || I > 16)) continue;
+      const long long nch = (L + CH - 1) / CH;
+      const double fill = (double)L / (double)(nch * CH);
+      const double par = std::min(1.0, (double)(rows * S) / 8192.0);
+      const double eff = (double)I / (I + 6.0);
+      const double score = fill * par * eff;
+      if (score > best_score + 1e-12) {
+        best_score = score;
+        best = {I, S};
+      }
+    }
+  }
+  if (best_score < 0) best = {0, 0};
+  return best;
+}
+
+template <int I, int MAXT>
+hipError_t launch_fwd(const M1Args& a, int S, long long rows, hipStream_t st) {
+  const int R = I / 4;
+  const int threads = 64 * R * S;
+  const size_t lds =
+      sizeof(float) * ((size_t)6 * S * 64 * (I + kPad) + 4 * R * S + (size_t)R * S * a.N);
+  const long long blocks = rows / R;
+  if (threads > MAXT) return hipErrorInvalidConfiguration;
+  hipLaunchKernelGGL((m1_scan_kernel<I, MAXT>), dim3((unsigned)blocks), dim3(threads), lds, st,
+                     a);
+  return hipGetLastError();
+}
+
+template <int I, int MAXT>
+hipError_t launch_bidir(const M1Args& a, int S, long long rows, hipStream_t st) {
+  const int R = I / 4;
+  const int threads = 64 * R * S;
+  const bool sep = (a.B2 != a.B) || (a.C2 != a.C);
+  const size_t lds =
+      sizeof(float) * ((size_t)(sep ? 12 : 6) * S * 64 * (I + kPad) + 8 * R * S);
+  const long long blocks = rows / R;
+  if (threads > MAXT) return hipErrorInvalidConfiguration;
+  hipLaunchKernelGGL((m1_bidir_kernel<I, MAXT>), dim3((unsigned)blocks), dim3(threads), lds, st,
+                     a);
+  return hipGetLastError();
+}
+
+bool aligned16(const void* p) { return p == nullptr || ((uintptr_t)p & 15u) == 0; }
+
+}  // namespace
+
+static void fill_args(M1Args& a, const M1Problem& pr) {
+  a.u = pr.u; a.delta = pr.delta; a.A = pr.A; a.B = pr.B; a.C = pr.C;
+  a.B2 = pr.B2 ? pr.B2 : pr.B; a.C2 = pr.C2 ? pr.C2 : pr.C;
+  a.D = pr.D; a.z = pr.z; a.bias = pr.bias; a.h0 = pr.h0;
+  a.out = pr.out; a.last = pr.last; a.out2 = pr.out2; a.last2 = pr.last2;
+  a.L = (long long)pr.len; a.dim = (int)pr.dim; a.N = (int)pr.state; a.groups = (int)pr.groups;
+  a.group_size = (int)(pr.dim / pr.groups);
+  a.softplus = pr.softplus; a.reverse = pr.reverse; a.merge = pr.merge;
+  const bool al = aligned16(pr.u) && aligned16(pr.delta) && aligned16(pr.B) && aligned16(pr.C) &&
+                  aligned16(pr.B2) && aligned16(pr.C2) && aligned16(pr.z) && aligned16(pr.out) &&
+                  aligned16(pr.out2);
+  a.vec = (pr.len % 4 == 0) && al;
+}
+
+hipError_t m1_scan(const M1Problem& pr, hipStream_t st) {
+  M1Args a{};
+  fill_args(a, pr);
+  const long long rows = (long long)pr.batch * pr.dim;
+  const Choice c = choose(rows, (long long)pr.len, (long long)(pr.dim / pr.groups), false);
+  a.S = c.S;
+  switch (c.I) {
+    case 32: return launch_fwd<32, 512>(a, c.S, rows, st);
+    case 16: return launch_fwd<16, 1024>(a, c.S, rows, st);
+    case 8: return launch_fwd<8, 1024>(a, c.S, rows, st);
+    case 4: return launch_fwd<4, 1024>(a, c.S, rows, st);
+    default: return hipErrorInvalidConfiguration;
+  }
+}
+
+bool m1_bidir_fusable(const M1Problem& pr) {
+  const long long rows = (long long)pr.batch * pr.dim;
+  return choose(rows, (long long)pr.len, (long long)(pr.dim / pr.groups), true).I != 0;
+}
+
+hipError_t m1_bidir(const M1Problem& pr, hipStream_t st) {
+  M1Args a{};
+  fill_args(a, pr);
+  const long long rows = (long long)pr.batch * pr.dim;
+  const Choice c = choose(rows, (long long)pr.len, (long long)(pr.dim / pr.groups), true);
+  a.S = c.S;
+  switch (c.I) {
+    case 16: return launch_bidir<16, 1024>(a, c.S, rows, st);
+    case 8: return launch_bidir<8, 1024>(a, c.S, rows, st);
+    case 4: return launch_bidir<4, 1024>(a, c.S, rows, st);
+    case 32: return launch_bidir<32, 512>(a, c.S, rows, st);
+    default: return hipErrorInvalidConfiguration;
+  }
+}
+
+hipError_t transpose_hw(const float* in, float* out, long long planes, int H, int W,
+                        bool accumulate, hipStream_t st) {
+  // gridDim.z is limited to 65535: walk the planes in slabs
+  for (long long p0 = 0; p0 < planes; p0 += 65535) {
+    const long long np = planes - p0 < 65535 ? planes - p0 : 65535;
+    const dim3 grid((unsigned)((W + 31) / 32), (unsigned)((H + 31) / 32), (unsigned)np);
+    const long long off = p0 * (long long)H * W;
+    hipLaunchKernelGGL(transpose_hw_kernel, grid, dim3(256), 0, st, in + off, out + off, H, W,
+                       accumulate ? 1 : 0);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+hipError_t add_inplace(float* x, const float* y, long long n, hipStream_t st) {
+  const long long blocks = (n + 255) / 256;
+  hipLaunchKernelGGL(add_kernel, dim3((unsigned)blocks), dim3(256), 0, st, x, y, n);
+  return hipGetLastError();
+}
+
+hipError_t scale_inplace(float* x, long long n, float scale, hipStream_t st) {
+  const long long blocks = (n + 255) / 256;
+  hipLaunchKernelGGL(scale_kernel, dim3((unsigned)blocks), dim3(256), 0, st, x, n, scale);
+  return hipGetLastError();
+}
+
+}  // namespace armscan

@@ -1,0 +1,44 @@
+// Host-side launchers behind the C ABI (internal to libarm_scan_hip.so).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+
+namespace armscan {
+
+// One Mamba-1 problem: the reference's layouts (lib.rs:9-16) on device memory.
+struct M1Problem {
+  size_t batch, dim, len, state, groups;
+  const float *u, *delta, *A, *B, *C;
+  const float *B2, *C2;  // backward-direction B/C for the bidirectional pass (null = B/C)
+  const float *D, *z, *bias, *h0;
+  float *out, *last;
+  float *out2, *last2;  // bidirectional outputs
+  int softplus, reverse;
+  int merge;  // bidirectional: write out = fwd + bwd instead of two outputs
+};
+
+hipError_t m1_scan(const M1Problem& p, hipStream_t st);
+// True when the fused bidirectional kernel can hold a whole row in one pass.
+bool m1_bidir_fusable(const M1Problem& p);
+hipError_t m1_bidir(const M1Problem& p, hipStream_t st);
+// (planes, H, W) -> (planes, W, H); accumulate adds into `out`.
+hipError_t transpose_hw(const float* in, float* out, long long planes, int H, int W,
+                        bool accumulate, hipStream_t st);
+hipError_t scale_inplace(float* x, long long n, float scale, hipStream_t st);
+hipError_t add_inplace(float* x, const float* y, long long n, hipStream_t st);
+
+// One Mamba-3 problem: mamba3/mod.rs:47-57 plus the groups axis on q/k.
+struct M3Problem {
+  size_t batch, heads, dv, dqk, len, rank, groups;
+  const float *q, *k, *v, *adt, *dt, *trap, *q_bias, *k_bias, *cos, *sin, *D, *z;
+  const float *psi, *zeta, *phi;  // all null = SISO
+  float *out, *last_state, *last_bx;
+  int reverse;
+};
+
+// Largest dv * dqk the Mamba-3 kernel holds on chip.
+size_t m3_max_state();
+hipError_t m3_scan(const M3Problem& p, hipStream_t st);
+
+}  // namespace armscan

@@ -1,0 +1,223 @@
+"""PyTorch front-end: `torch.library` custom ops over the HIP scan engine.
+
+Registered under the reference's names (python/arm_scan/op.py:23,103):
+`arm_scan::selective_scan` and `arm_scan::selective_scan_bidirectional`, each
+with a fake (meta) kernel so they trace under `torch.compile`.
+
+What changes from the reference is where the tensors live: inputs are
+PyTorch-ROCm device tensors, the kernels are enqueued on the current stream of
+the tensors' device, and the call returns without synchronising. A host tensor
+is an error, not a cue to fall back: this package has no CPU implementation.
+
+Inference-only, like the reference: no autograd formula is registered.
+"""
+
+from typing import Optional, Tuple
+
+import torch
+
+from . import _ffi
+
+_CALLS = {"n": 0}
+
+
+def _c(t: torch.Tensor) -> torch.Tensor:
+    return t.contiguous().float()
+
+
+def _ptr(t):
+    return 0 if t is None else t.data_ptr()
+
+
+def _device_of(*tensors):
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise ValueError(
+                "arm_scan on MI355X takes device tensors (got a tensor on "
+                f"{t.device}); move inputs with .to('cuda') first")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError(f"tensors on different devices: {dev} and {t.device}")
+    return dev
+
+
+def _stream(dev):
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _check_m1(u, delta, a, b, c, d_skip, z, delta_bias, h0):
+    """Shape checks for the Mamba-1 ops: the C side trusts element counts
+    (arm-scan-ffi/src/lib.rs:92-96), so shape safety is owned here."""
+    if u.dim() != 3:
+        raise ValueError(f"u must be (batch, dim, len), got {tuple(u.shape)}")
+    batch, dim, length = u.shape
+    if tuple(delta.shape) != (batch, dim, length):
+        raise ValueError(f"delta must be {(batch, dim, length)}, got {tuple(delta.shape)}")
+    if a.dim() != 2 or a.shape[0] != dim:
+        raise ValueError(f"A must be ({dim}, state), got {tuple(a.shape)}")
+    state = a.shape[1]
+    if b.dim() != 4 or c.dim() != 4:
+        raise ValueError("B/C must be (batch, groups, state, len)")
+    groups = b.shape[1]
+    for name, t in (("B", b), ("C", c)):
+        if tuple(t.shape) != (batch, groups, state, length):
+            raise ValueError(
+                f"{name} must be {(batch, groups, state, length)}, got {tuple(t.shape)}")
+    for name, t, want in (("D", d_skip, (dim,)), ("delta_bias", delta_bias, (dim,)),
+                          ("z", z, (batch, dim, length)),
+                          ("initial_state", h0, (batch, dim, state))):
+        if t is not None and tuple(t.shape) != want:
+            raise ValueError(f"{name} must be {want}, got {tuple(t.shape)}")
+    return batch, dim, length, state, groups
+
+
+@torch.library.custom_op("arm_scan::selective_scan", mutates_args=())
+def _selective_scan_op(
+    u: torch.Tensor,
+    delta: torch.Tensor,
+    a: torch.Tensor,
+    b: torch.Tensor,
+    c: torch.Tensor,
+    d_skip: Optional[torch.Tensor],
+    z: Optional[torch.Tensor],
+    delta_bias: Optional[torch.Tensor],
+    h0: Optional[torch.Tensor],
+    delta_softplus: bool,
+    reverse: bool,
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    dev = _device_of(u, delta, a, b, c, d_skip, z, delta_bias, h0)
+    batch, dim, length, state, groups = _check_m1(u, delta, a, b, c, d_skip, z, delta_bias, h0)
+    out = torch.empty_like(u)
+    last_state = u.new_empty((batch, dim, state))
+    dims = _ffi.ArmScanDims(batch, dim, length, state, groups)
+    with torch.cuda.device(dev):
+        _ffi.scan_raw(dims, u.data_ptr(), delta.data_ptr(), a.data_ptr(), b.data_ptr(),
+                      c.data_ptr(), _ptr(d_skip), _ptr(z), _ptr(delta_bias), delta_softplus,
+                      "auto", "auto", out.data_ptr(), last_state.data_ptr(), ptr_h0=_ptr(h0),
+                      reverse=reverse, stream=_stream(dev))
+    _CALLS["n"] += 1
+    return out, last_state
+
+
+@_selective_scan_op.register_fake
+def _(u, delta, a, b, c, d_skip, z, delta_bias, h0, delta_softplus, reverse):
+    return torch.empty_like(u), u.new_empty((u.shape[0], u.shape[1], a.shape[1]))
+
+
+def _bc4(t, batch, state, length):
+    return t.reshape(batch, 1, state, length) if t.dim() == 3 else t
+
+
+def selective_scan(u, delta, A, B, C, D=None, z=None, delta_bias=None,
+                   delta_softplus=False, return_last_state=False,
+                   initial_state=None, reverse=False):
+    """Mamba-1 selective scan on device float32 tensors
+    (the reference's `arm_scan.selective_scan`, python/arm_scan/op.py:63-100).
+
+    u, delta, z: (batch, dim, len); A: (dim, state);
+    B, C: (batch, state, len) or (batch, groups, state, len);
+    D, delta_bias: (dim,); initial_state: (batch, dim, state) to resume from.
+    Returns out (batch, dim, len) [, last_state (batch, dim, state)].
+
+    reverse walks the sequence backward in time with the output layout
+    unchanged (timestep t still lands at index t); under reverse, last_state
+    is the state after consuming t = 0.
+    """
+    batch, dim, length = u.shape
+    state = A.shape[1]
+    B = _bc4(B, batch, state, length)
+    C = _bc4(C, batch, state, length)
+    out, last_state = _selective_scan_op(
+        _c(u), _c(delta), _c(A), _c(B), _c(C),
+        None if D is None else _c(D),
+        None if z is None else _c(z),
+        None if delta_bias is None else _c(delta_bias),
+        None if initial_state is None else _c(initial_state),
+        bool(delta_softplus), bool(reverse))
+    return (out, last_state) if return_last_state else out
+
+
+@torch.library.custom_op("arm_scan::selective_scan_bidirectional", mutates_args=())
+def _selective_scan_bidir_op(
+    u: torch.Tensor,
+    delta: torch.Tensor,
+    a: torch.Tensor,
+    b: torch.Tensor,
+    c: torch.Tensor,
+    d_skip: Optional[torch.Tensor],
+    z: Optional[torch.Tensor],
+    delta_bias: Optional[torch.Tensor],
+    delta_softplus: bool,
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    dev = _device_of(u, delta, a, b, c, d_skip, z, delta_bias)
+    batch, dim, length, state, groups = _check_m1(u, delta, a, b, c, d_skip, z, delta_bias,
+                                                  None)
+    out_fwd = torch.empty_like(u)
+    out_bwd = torch.empty_like(u)
+    dims = _ffi.ArmScanDims(batch, dim, length, state, groups)
+    with torch.cuda.device(dev):
+        _ffi.scan_bidir_raw(dims, u.data_ptr(), delta.data_ptr(), a.data_ptr(), b.data_ptr(),
+                            c.data_ptr(), _ptr(d_skip), _ptr(z), _ptr(delta_bias),
+                            delta_softplus, "auto", "auto", out_fwd.data_ptr(),
+                            out_bwd.data_ptr(), stream=_stream(dev))
+    _CALLS["n"] += 1
+    return out_fwd, out_bwd
+
+
+@_selective_scan_bidir_op.register_fake
+def _(u, delta, a, b, c, d_skip, z, delta_bias, delta_softplus):
+    return torch.empty_like(u), torch.empty_like(u)
+
+
+def selective_scan_bidirectional(u, delta, A, B, C, D=None, z=None,
+                                 delta_bias=None, delta_softplus=False):
+    """Forward and reverse scans of the same inputs in one call
+    (python/arm_scan/op.py:138-160) -> (out_fwd, out_bwd). exp(delta*A) is
+    evaluated once and shared by both directions."""
+    batch, dim, length = u.shape
+    state = A.shape[1]
+    B = _bc4(B, batch, state, length)
+    C = _bc4(C, batch, state, length)
+    return _selective_scan_bidir_op(
+        _c(u), _c(delta), _c(A), _c(B), _c(C),
+        None if D is None else _c(D),
+        None if z is None else _c(z),
+        None if delta_bias is None else _c(delta_bias),
+        bool(delta_softplus))
+
+
+def selective_scan_bidirectional_with_state(u, delta, A, B, C, D=None, z=None,
+                                            delta_bias=None, delta_softplus=False):
+    """As `selective_scan_bidirectional`, also returning both final states:
+    (out_fwd, out_bwd, last_fwd, last_bwd). The reference's C ABI has these
+    outputs (arm-scan-ffi/src/lib.rs:235-252) but its torch op drops them."""
+    dev = _device_of(u, delta, A, B, C, D, z, delta_bias)
+    batch, dim, length = u.shape
+    state = A.shape[1]
+    u, delta, A = _c(u), _c(delta), _c(A)
+    B = _c(_bc4(B, batch, state, length))
+    C = _c(_bc4(C, batch, state, length))
+    D = None if D is None else _c(D)
+    z = None if z is None else _c(z)
+    delta_bias = None if delta_bias is None else _c(delta_bias)
+    _, _, _, _, groups = _check_m1(u, delta, A, B, C, D, z, delta_bias, None)
+    of, ob = torch.empty_like(u), torch.empty_like(u)
+    lf, lb = u.new_empty((batch, dim, state)), u.new_empty((batch, dim, state))
+    dims = _ffi.ArmScanDims(batch, dim, length, state, groups)
+    with torch.cuda.device(dev):
+        _ffi.scan_bidir_raw(dims, u.data_ptr(), delta.data_ptr(), A.data_ptr(), B.data_ptr(),
+                            C.data_ptr(), _ptr(D), _ptr(z), _ptr(delta_bias), delta_softplus,
+                            "auto", "auto", of.data_ptr(), ob.data_ptr(), lf.data_ptr(),
+                            lb.data_ptr(), stream=_stream(dev))
+    _CALLS["n"] += 1
+    return of, ob, lf, lb
+
+
+def kernel_calls() -> int:
+    """How many times the native library has been invoked (engagement check,
+    python/arm_scan/op.py:163-166)."""
+    return _CALLS["n"]

@@ -1,0 +1,94 @@
+"""Drop-in acceleration of Hugging Face transformers Mamba-1 on MI355X.
+
+`patch()` replaces the module-level `mamba_selective_scan` of
+transformers.models.mamba.modeling_mamba (the seam the reference patches on
+transformers >= 5.5, python/arm_scan/patch.py:119-180) with a wrapper that runs
+the scan in the HIP kernel. Projections, the causal conv, gating, weights and
+caches stay upstream's; only the recurrence moves.
+
+The wrapper takes the fast path for float32 device tensors with no gradient
+required; anything else (host tensors, other dtypes, autograd) goes to the
+original function unchanged, exactly as the reference's wrapper falls back on
+what its kernel cannot serve (python/arm_scan/patch.py:152-168). Decode steps
+use `mamba_selective_state_update`, which is not patched.
+
+`unpatch()` restores the original; `stats()` reports engagement.
+"""
+
+import torch
+
+from .op import kernel_calls, selective_scan
+
+_STATE = {"orig": None, "target": None, "fast_calls": 0, "fallback_calls": 0}
+
+
+def _patch_scan_fn(modeling_mamba):
+    orig = modeling_mamba.mamba_selective_scan
+
+    def mamba_selective_scan(hidden_states, dt, A, B, C, D=None, z=None,
+                             delta_bias=None, delta_softplus=False,
+                             return_last_state=False, use_mambapy=False,
+                             use_associative_scan=False, **kwargs):
+        tensors = (hidden_states, dt, A, B, C)
+        optional = tuple(t for t in (D, z, delta_bias) if t is not None)
+        needs_grad = torch.is_grad_enabled() and any(
+            t.requires_grad for t in (*tensors, *optional))
+        if (needs_grad
+                or any(t.device.type != "cuda" for t in (*tensors, *optional))
+                or any(t.dtype != torch.float32 for t in tensors)):
+            _STATE["fallback_calls"] += 1
+            return orig(hidden_states, dt, A, B, C, D=D, z=z, delta_bias=delta_bias,
+                        delta_softplus=delta_softplus, return_last_state=return_last_state,
+                        use_mambapy=use_mambapy, use_associative_scan=use_associative_scan,
+                        **kwargs)
+        _STATE["fast_calls"] += 1
+        return selective_scan(hidden_states, dt, A, B, C, D=D, z=z, delta_bias=delta_bias,
+                              delta_softplus=delta_softplus,
+                              return_last_state=return_last_state)
+
+    modeling_mamba.mamba_selective_scan = mamba_selective_scan
+    _STATE["orig"] = orig
+    _STATE["target"] = "mamba_selective_scan"
+    return ["transformers mamba_selective_scan (selective_scan_fn API)"]
+
+
+def patch():
+    """Route HF Mamba's selective scan on device tensors through the HIP kernel.
+
+    Returns the list of patched targets ([] if this transformers version has
+    no `mamba_selective_scan` seam). Idempotent.
+    """
+    if _STATE["orig"] is not None:
+        return ["transformers mamba_selective_scan (already patched)"]
+    from transformers.models.mamba import modeling_mamba
+
+    if not hasattr(modeling_mamba, "mamba_selective_scan"):
+        import warnings
+
+        warnings.warn("armhackathon_amd.patch(): this transformers version has no "
+                      "mamba_selective_scan; leaving it unpatched")
+        return []
+    return _patch_scan_fn(modeling_mamba)
+
+
+def unpatch():
+    """Restore the original implementation (for A/B benchmarking)."""
+    if _STATE["orig"] is None:
+        return False
+    from transformers.models.mamba import modeling_mamba
+
+    modeling_mamba.mamba_selective_scan = _STATE["orig"]
+    _STATE["orig"] = None
+    _STATE["target"] = None
+    return True
+
+
+def stats():
+    """Engagement counters: fast-path vs fallback calls, native invocations."""
+    return {
+        "fast_calls": _STATE["fast_calls"],
+        "fallback_calls": _STATE["fallback_calls"],
+        "kernel_calls": kernel_calls(),
+        "patched": _STATE["orig"] is not None,
+        "api": "selective_scan_fn" if _STATE["orig"] is not None else None,
+    }

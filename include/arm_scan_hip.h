@@ -1,0 +1,130 @@
+/*
+ * arm_scan_hip.h — C ABI of libarm_scan_hip.so, the MI355X (gfx950) selective-scan
+ * engine that replaces the scan path of AdityaP9116/ARMHackathon ("Arm Scan").
+ *
+ * The entry points keep the reference's names, argument order and return codes
+ * (kernel/arm-scan-ffi/src/lib.rs). What changes, as the reference's own versioning
+ * rule demands (arm-scan-ffi/src/lib.rs:24-36: "bump on any signature or semantic
+ * change"), is ABI 7 -> 8:
+ *
+ *   - every tensor pointer is a DEVICE pointer (HBM of the current HIP device);
+ *   - every entry point takes a trailing `void* stream` (a hipStream_t; NULL is the
+ *     null stream). The call enqueues the kernels on that stream and returns without
+ *     synchronising: outputs are ready when the stream reaches that point;
+ *   - ArmMamba3Dims gains `groups` (q/k carry a groups axis, head h reads group
+ *     h / (heads / groups); groups == 1 is the reference layout);
+ *   - Mamba-3 MIMO may write `last_state` (the reference rejects any MIMO carry);
+ *   - one new entry point, arm_scan_ss2d_f32, the fused four-direction 2D scan;
+ *   - code 6 reports a HIP launch / device error; arm_scan_last_error() explains
+ *     the most recent nonzero code on the calling thread.
+ *
+ * Layouts are the reference's (row-major, contiguous, fp32):
+ *   Mamba-1   u, delta, z, out (batch, dim, len); a (dim, state);
+ *             b, c (batch, groups, state, len); d_skip, delta_bias (dim);
+ *             last_state, h0 (batch, dim, state)
+ *   Mamba-3   q, k (batch, len, rank, groups, dqk); v, z (batch, len, heads, dv);
+ *             adt, dt, trap (batch, heads, len); cos, sin (batch, len, heads, dqk/2);
+ *             q_bias, k_bias (heads, rank, dqk); d_skip (heads);
+ *             psi, zeta, phi (heads, rank, dv); out HEAD-MAJOR (batch, heads, len, dv);
+ *             last_state (batch, heads, dv, dqk); last_bx (batch, heads, dqk)
+ */
+#ifndef ARM_SCAN_HIP_H
+#define ARM_SCAN_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ARM_SCAN_ABI_VERSION 8u
+
+/* Return codes: arm-scan-ffi/src/lib.rs:53-58, plus 6. */
+#define ARM_SCAN_OK 0
+#define ARM_SCAN_ERR_NULL_POINTER 1
+#define ARM_SCAN_ERR_INVALID_DIMS 2
+#define ARM_SCAN_ERR_BACKEND_UNAVAILABLE 3
+#define ARM_SCAN_ERR_BAD_ENUM 4
+#define ARM_SCAN_ERR_PANIC 5
+#define ARM_SCAN_ERR_DEVICE 6
+
+/* backend: 0 auto (= the HIP kernels); 1 scalar and 2 neon are CPU backends of the
+ * reference and return ARM_SCAN_ERR_BACKEND_UNAVAILABLE here.
+ * threading: 0 auto, 1 sequential, 2 rayon — accepted for compatibility and ignored
+ * (the GPU grid replaces Rayon); any other value is ARM_SCAN_ERR_BAD_ENUM. */
+
+/* arm-scan-ffi/src/lib.rs:43-50, unchanged. */
+typedef struct ArmScanDims {
+  size_t batch, dim, len, state, groups;
+} ArmScanDims;
+
+/* arm-scan-ffi/src/lib.rs:362-373 plus `groups` (ABI 8). */
+typedef struct ArmMamba3Dims {
+  size_t batch, heads, dv, dqk, len, rank, groups;
+} ArmMamba3Dims;
+
+/* New in ABI 8: the 2D cross-scan over a (height, width) token grid. */
+typedef struct ArmSS2DDims {
+  size_t batch, dim, height, width, state;
+} ArmSS2DDims;
+
+/* Replaces arm_scan_abi_version (arm-scan-ffi/src/lib.rs:37-40); returns 8. */
+uint32_t arm_scan_abi_version(void);
+
+/* Replaces arm_scan_selective_scan_f32 (arm-scan-ffi/src/lib.rs:99-216).
+ * Nullable: d_skip, z, delta_bias, last_state, h0. `reverse` walks the sequence
+ * backward (output t still lands at index t; last_state is then the state after
+ * consuming t == 0). h0 seeds the recurrence (orthogonal to reverse). */
+int arm_scan_selective_scan_f32(const ArmScanDims* dims, const float* u, const float* delta,
+                                const float* a, const float* b, const float* c,
+                                const float* d_skip, const float* z, const float* delta_bias,
+                                int delta_softplus, int reverse, int backend, int threading,
+                                float* out, float* last_state, const float* h0, void* stream);
+
+/* Replaces arm_scan_selective_scan_bidirectional_f32 (arm-scan-ffi/src/lib.rs:235-354):
+ * the forward and the reverse scan of the same inputs in one pass sharing exp(delta*A).
+ * last_fwd / last_bwd: both or neither (else ARM_SCAN_ERR_INVALID_DIMS). */
+int arm_scan_selective_scan_bidirectional_f32(
+    const ArmScanDims* dims, const float* u, const float* delta, const float* a,
+    const float* b, const float* c, const float* d_skip, const float* z,
+    const float* delta_bias, int delta_softplus, int backend, int threading, float* out_fwd,
+    float* out_bwd, float* last_fwd, float* last_bwd, void* stream);
+
+/* Replaces arm_scan_mamba3_scan_f32 (arm-scan-ffi/src/lib.rs:419-577).
+ * psi/zeta/phi: all three (MIMO) or none (SISO), else ARM_SCAN_ERR_NULL_POINTER.
+ * SISO: last_state/last_bx both or neither (else code 1). MIMO: last_state allowed,
+ * last_bx rejected (code 2). trap is pre-sigmoid; cos/sin come from the angle
+ * pre-pass; out is head-major. */
+int arm_scan_mamba3_scan_f32(const ArmMamba3Dims* dims, const float* q, const float* k,
+                             const float* v, const float* adt, const float* dt,
+                             const float* trap, const float* q_bias, const float* k_bias,
+                             const float* cos, const float* sin, const float* d_skip,
+                             const float* z, const float* mimo_psi, const float* mimo_zeta,
+                             const float* mimo_phi, int reverse, int backend, int threading,
+                             float* out, float* last_state, float* last_bx, void* stream);
+
+/* New in ABI 8 (no single reference symbol: it fuses python/arm_scan/ss2d.py:277-342,
+ * which composes two bidirectional calls). Four directions over a (H, W) grid:
+ * row_fwd, row_bwd over the row-major flattening t = i*W + j, col_fwd, col_bwd over the
+ * column-major one t = j*H + i; backward = reverse index mode.
+ *   u, delta, z, out-planes (batch, dim, H, W); a (dim, state); d_skip, delta_bias (dim);
+ *   b4, c4 (4, batch, state, H, W): one B and one C per direction, in grid layout
+ *   (the token at (i, j) uses b4[k][.., i, j] in direction k).
+ * merge: 0 none -> out is (4, batch, dim, H, W), the planes in the order above;
+ *        1 sum  -> out is (batch, dim, H, W) = sum of the planes; 2 mean -> sum / 4.
+ * D and z apply inside every direction (a sum carries 4*D*u), as in the reference.
+ * last_states (4, batch, dim, state) is nullable. */
+int arm_scan_ss2d_f32(const ArmSS2DDims* dims, const float* u, const float* delta,
+                      const float* a, const float* b4, const float* c4, const float* d_skip,
+                      const float* z, const float* delta_bias, int delta_softplus, int merge,
+                      float* out, float* last_states, void* stream);
+
+/* Human-readable reason for the last nonzero code returned on this thread. */
+const char* arm_scan_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ARM_SCAN_HIP_H */

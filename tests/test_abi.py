@@ -1,0 +1,117 @@
+"""The C ABI of libarm_scan_hip.so, host side only (no GPU needed).
+
+* every function declared in include/arm_scan_hip.h is exported by the library;
+* the ABI version is 8 and the loader checks it;
+* the reference's rejection codes (arm-scan-ffi/src/lib.rs:53-58, :117-158,
+  :461-487) come back before any launch: null pointers -> 1, bad dims -> 2,
+  CPU backends -> 3, bad enums -> 4. These calls never touch the device, so
+  the pointers they carry are never dereferenced.
+"""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from armhackathon_amd import _ffi
+
+ROOT = Path(__file__).resolve().parents[1]
+FAKE = 0x1000  # never dereferenced: every call below is rejected on the host
+
+
+def _declared():
+    text = (ROOT / "include" / "arm_scan_hip.h").read_text()
+    return sorted(set(re.findall(r"^\S.*?\b(arm_scan_\w+)\s*\(", text, re.M)))
+
+
+def test_header_symbols_exported():
+    lib = _ffi.load()
+    names = _declared()
+    assert "arm_scan_selective_scan_f32" in names and len(names) >= 6
+    for n in names:
+        assert hasattr(lib, n), n
+
+
+def test_abi_version():
+    assert _ffi.load().arm_scan_abi_version() == 8 == _ffi.ABI_VERSION
+
+
+def _m1(dims, u=FAKE, backend=0, threading=0, last=None, h0=None):
+    L = _ffi.load()
+    return L.arm_scan_selective_scan_f32(ctypes.byref(dims), u, FAKE, FAKE, FAKE, FAKE, None,
+                                         None, None, 0, 0, backend, threading, FAKE, last, h0,
+                                         None)
+
+
+def test_m1_rejections():
+    ok = _ffi.ArmScanDims(1, 2, 2, 2, 1)
+    assert _m1(ok, u=None) == 1
+    assert _m1(ok, backend=7) == 4 and _m1(ok, threading=-1) == 4
+    assert _m1(ok, backend=1) == 3 and _m1(ok, backend=2) == 3
+    assert _m1(_ffi.ArmScanDims(0, 2, 2, 2, 1)) == 2
+    assert _m1(_ffi.ArmScanDims(1, 3, 2, 2, 2)) == 2
+    assert _m1(_ffi.ArmScanDims(2 ** 40, 2 ** 40, 2, 2, 1)) == 2
+    msg = _ffi.load().arm_scan_last_error().decode()
+    assert "overflow" in msg
+    L = _ffi.load()
+    rc = L.arm_scan_selective_scan_bidirectional_f32(
+        ctypes.byref(ok), FAKE, FAKE, FAKE, FAKE, FAKE, None, None, None, 0, 0, 0, FAKE, FAKE,
+        FAKE, None, None)
+    assert rc == 2  # half of the last-state pair
+    rc = L.arm_scan_selective_scan_bidirectional_f32(
+        ctypes.byref(ok), FAKE, FAKE, FAKE, FAKE, FAKE, None, None, None, 0, 0, 0, FAKE, None,
+        None, None, None)
+    assert rc == 1
+
+
+def _m3(dims, psi=None, zeta=None, phi=None, ls=None, lb=None, backend=0, q=FAKE):
+    L = _ffi.load()
+    return L.arm_scan_mamba3_scan_f32(ctypes.byref(dims), q, FAKE, FAKE, FAKE, FAKE, FAKE,
+                                      FAKE, FAKE, FAKE, FAKE, None, None, psi, zeta, phi, 0,
+                                      backend, 0, FAKE, ls, lb, None)
+
+
+def test_m3_rejections():
+    D = _ffi.ArmMamba3Dims
+    ok = D(1, 2, 4, 4, 3, 1, 1)
+    assert _m3(ok, q=None) == 1
+    assert _m3(ok, ls=FAKE) == 1           # half a carry
+    assert _m3(ok, psi=FAKE) == 1          # partial projections
+    assert _m3(ok, backend=9) == 4
+    assert _m3(ok, backend=1) == 3
+    assert _m3(D(1, 2, 4, 5, 3, 1, 1)) == 2            # odd dqk
+    assert _m3(D(1, 2, 4, 4, 3, 0, 1)) == 2            # rank 0
+    assert _m3(D(1, 2, 4, 4, 3, 2, 1)) == 2            # rank > 1 without MIMO
+    assert _m3(D(1, 3, 4, 4, 3, 1, 2)) == 2            # groups must divide heads
+    assert _m3(ok, psi=FAKE, zeta=FAKE, phi=FAKE, ls=FAKE, lb=FAKE) == 2  # MIMO last_bx
+
+
+def test_ss2d_rejections():
+    L = _ffi.load()
+    d = _ffi.ArmSS2DDims(1, 2, 3, 3, 4)
+
+    def call(dims, u=FAKE, merge=1):
+        return L.arm_scan_ss2d_f32(ctypes.byref(dims), u, FAKE, FAKE, FAKE, FAKE, None, None,
+                                   None, 0, merge, FAKE, None, None)
+
+    assert call(d, u=None) == 1
+    assert call(d, merge=5) == 4
+    assert call(_ffi.ArmSS2DDims(1, 2, 0, 3, 4)) == 2
+
+
+def test_python_errors_carry_code():
+    with pytest.raises(_ffi.ArmScanError) as e:
+        _ffi.scan_raw(_ffi.ArmScanDims(1, 2, 2, 2, 1), FAKE, FAKE, FAKE, FAKE, FAKE, 0, 0, 0,
+                      False, "scalar", "auto", FAKE, 0)
+    assert e.value.code == 3 and "backend" in str(e.value)
+
+
+def test_host_tensor_is_an_error():
+    torch = pytest.importorskip("torch")
+    import armhackathon_amd as arm_scan
+
+    u = torch.zeros(1, 2, 8)
+    with pytest.raises(ValueError, match="device tensors"):
+        arm_scan.selective_scan(u, u, torch.zeros(2, 4), torch.zeros(1, 4, 8),
+                                torch.zeros(1, 4, 8))

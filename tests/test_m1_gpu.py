@@ -1,0 +1,176 @@
+"""Mamba-1 selective scan on the GPU vs the CPU oracle and the reference goldens.
+
+Gates (fp32): tensor-scale relative error <= 1e-4 on outputs and final states
+plus the reference's own golden gates
+(check_ffi.py:153-154,205-206: max_abs < 1e-4 vs out_f64, last_state rel < 1e-4).
+Cases follow the reference's test strategy: every golden, reverse, h0 streaming,
+grouped B/C, missing optional inputs, ragged lengths (L not a multiple of the
+kernel's chunking, L = 1), D = 1, N = 8 and 13, and the full benchmark shapes.
+"""
+
+import json
+
+import numpy as np
+import pytest
+
+import oracle
+from armhackathon_amd import workloads
+from util import case, dev, host, rel_err
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+
+
+def _scan(x, **kw):
+    import armhackathon_amd as arm_scan
+
+    t = dev(x)
+    return arm_scan.selective_scan(t["u"], t["delta"], t["A"], t["B"], t["C"], D=t.get("D"),
+                                   z=t.get("z"), delta_bias=t.get("delta_bias"),
+                                   return_last_state=True,
+                                   initial_state=t.get("h0"), **kw)
+
+
+def _ref(x, dtype=np.float64, **kw):
+    return oracle.selective_scan(x["u"], x["delta"], x["A"], x["B"], x["C"], D=x.get("D"),
+                                 z=x.get("z"), delta_bias=x.get("delta_bias"),
+                                 h0=x.get("h0"), dtype=dtype, **kw)
+
+
+def test_m1_goldens(golden_dir):
+    """Every reference Mamba-1 golden under the reference's gates."""
+    man = json.loads((golden_dir / "1d" / "manifest.json").read_text())
+    for m in man:
+        case(f"golden {m['name']}")
+        z = np.load(golden_dir / "1d" / f"{m['name']}.npz")
+        meta = json.loads(bytes(z["meta_json"]).decode())
+        x = {k: z[k].astype(np.float32) for k in ("u", "delta", "A", "B", "C")}
+        for k, name in (("D", "D_skip"), ("z", "z"), ("delta_bias", "delta_bias")):
+            if name in z.files:
+                x[k] = z[name].astype(np.float32)
+        out, last = _scan(x, delta_softplus=meta["delta_softplus"])
+        out, last = host(out), host(last)
+        err = np.abs(out - z["out_f64"]).max()
+        floor = float(m.get("f32_max_abs_err") or 0.0)
+        assert err < 1e-4, (m["name"], err)
+        if floor > 0:
+            assert err < 50 * max(floor, 1e-7), (m["name"], err, floor)
+        assert rel_err(last, z["last_state_f64"]) < 1e-4, m["name"]
+
+
+SHAPES = [
+    # (batch, dim, len, state, groups)
+    (1, 4, 1, 16, 1),
+    (2, 8, 7, 16, 1),
+    (1, 3, 129, 5, 1),
+    (2, 16, 1000, 16, 4),
+    (1, 12, 2049, 13, 3),
+    (3, 10, 4096, 16, 2),
+    (1, 8, 9000, 8, 1),
+    (2, 64, 333, 16, 64),
+]
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("reverse", [False, True])
+def test_m1_random_vs_oracle(shape, reverse):
+    b, d, L, n, g = shape
+    case(f"m1 random {shape} reverse={reverse}")
+    rng = np.random.default_rng(hash((shape, reverse)) & 0xFFFF)
+    f = np.float32
+    x = dict(u=rng.standard_normal((b, d, L)).astype(f),
+             delta=(rng.standard_normal((b, d, L)) * 0.5).astype(f),
+             A=(-np.exp(rng.uniform(-0.7, 2.7, (d, n)))).astype(f),
+             B=rng.standard_normal((b, g, n, L)).astype(f),
+             C=rng.standard_normal((b, g, n, L)).astype(f),
+             D=rng.standard_normal(d).astype(f), z=rng.standard_normal((b, d, L)).astype(f),
+             delta_bias=rng.uniform(-6, -3, d).astype(f),
+             h0=rng.standard_normal((b, d, n)).astype(f))
+    out, last = _scan(x, delta_softplus=True, reverse=reverse)
+    ref, ref_last = _ref(x, delta_softplus=True, reverse=reverse)
+    assert rel_err(host(out), ref) < TOL
+    assert rel_err(host(last), ref_last) < TOL
+
+
+def test_m1_optional_inputs_absent():
+    x = workloads.m1_op(batch=2, dim=24, length=777, state=16, seed=3, z=False, D=False)
+    case("m1 without D/z/bias, softplus off")
+    out, last = _scan(x)
+    ref, ref_last = _ref(x)
+    assert rel_err(host(out), ref) < TOL and rel_err(host(last), ref_last) < TOL
+
+
+def test_m1_reverse_is_flip_forward_flip():
+    """property.rs:138: reverse == flip -> forward -> flip."""
+    x = workloads.m1_op(batch=2, dim=32, length=3000, state=16, seed=4)
+    case("m1 reverse == flip-forward-flip")
+    rev, lr = _scan(x, reverse=True)
+    fl = {k: (np.ascontiguousarray(v[..., ::-1]) if k in ("u", "delta", "B", "C", "z") else v)
+          for k, v in x.items()}
+    fwd, lf = _scan(fl)
+    assert rel_err(host(rev), host(fwd)[..., ::-1]) < 1e-6
+    assert rel_err(host(lr), host(lf)) < 1e-6
+    assert rel_err(host(rev), host(_scan(x)[0])) > 1e-2
+
+
+def test_m1_streaming_equals_one_shot():
+    """property.rs:500 / check_ffi.py:174-194: prefix then suffix with h0."""
+    x = workloads.m1_op(batch=2, dim=16, length=2500, state=16, seed=5)
+    case("m1 h0 streaming")
+    full, lfull = _scan(x)
+    cut = 1111
+    a = {k: (np.ascontiguousarray(v[..., :cut]) if k in ("u", "delta", "B", "C", "z") else v)
+         for k, v in x.items()}
+    b = {k: (np.ascontiguousarray(v[..., cut:]) if k in ("u", "delta", "B", "C", "z") else v)
+         for k, v in x.items()}
+    o1, l1 = _scan(a)
+    b["h0"] = host(l1)
+    o2, l2 = _scan(b)
+    assert rel_err(np.concatenate([host(o1), host(o2)], -1), host(full)) < 1e-5
+    assert rel_err(host(l2), host(lfull)) < 1e-5
+
+
+def test_m1_deterministic():
+    """Two launches on the same inputs are bit-identical (property.rs:453-497)."""
+    x = workloads.m1_op(batch=1, dim=64, length=4096, state=16, seed=6)
+    case("m1 determinism")
+    o1, _ = _scan(x)
+    o2, _ = _scan(x)
+    assert np.array_equal(host(o1), host(o2))
+
+
+def test_m1_bidirectional_fused():
+    """Fused pair == forward scan + reverse scan (property.rs:240)."""
+    import armhackathon_amd as arm_scan
+    from armhackathon_amd.op import selective_scan_bidirectional_with_state
+
+    for (b, d, L) in ((2, 16, 700), (1, 8, 2048), (1, 4, 6000)):
+        case(f"m1 bidirectional {b}x{d}x{L}")
+        x = workloads.m1_op(batch=b, dim=d, length=L, state=16, seed=L)
+        x["delta_bias"] = np.full(d, -0.5, np.float32)
+        t = dev(x)
+        of, ob, lf, lb = selective_scan_bidirectional_with_state(
+            t["u"], t["delta"], t["A"], t["B"], t["C"], D=t["D"], z=t["z"],
+            delta_bias=t["delta_bias"], delta_softplus=True)
+        rf, rb, rlf, rlb = oracle.selective_scan_bidirectional(
+            x["u"], x["delta"], x["A"], x["B"], x["C"], D=x["D"], z=x["z"],
+            delta_bias=x["delta_bias"], delta_softplus=True, dtype=np.float64)
+        assert rel_err(host(of), rf) < TOL and rel_err(host(ob), rb) < TOL
+        assert rel_err(host(lf), rlf) < TOL and rel_err(host(lb), rlb) < TOL
+        s = arm_scan.bidirectional_scan(t["u"], t["delta"], t["A"], t["B"], t["C"], D=t["D"],
+                                        z=t["z"], delta_bias=t["delta_bias"],
+                                        delta_softplus=True, merge="sum")
+        assert rel_err(host(s), rf + rb) < TOL
+
+
+@pytest.mark.parametrize("batch", [1, 8])
+def test_m1_benchmark_shape(batch):
+    """BASELINE config 1 (batch 1) and the north-star shape (batch 8): D 1536,
+    L 2048, N 16, against the float64 oracle, outputs and final states."""
+    case(f"m1 benchmark shape batch={batch}")
+    x = workloads.m1_op(batch=batch, dim=1536, length=2048, state=16, seed=0)
+    out, last = _scan(x)
+    ref, ref_last = _ref(x)
+    assert rel_err(host(out), ref) < TOL
+    assert rel_err(host(last), ref_last) < TOL

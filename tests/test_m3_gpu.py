@@ -1,0 +1,168 @@
+"""Mamba-3 SISO and MIMO scans on the GPU vs the CPU oracle and the reference goldens.
+
+Gates: tensor-scale relative error <= 1e-4 (fp32) against the float64 oracle on
+outputs and final states; the captured official-kernel goldens under the
+reference's own bf16-ULP gates (verify_golden_mamba3.py:47-65: <= 8 ULP SISO;
+check_mamba3_mimo_op.py:66: <= 12 ULP MIMO).
+"""
+
+import numpy as np
+import pytest
+
+import oracle
+from armhackathon_amd import workloads
+from util import case, dev, host, rel_err
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+BF16_EPS = 2.0 ** -8
+
+
+def _bf16(x):
+    x = np.asarray(x, np.float32)
+    bits = x.view(np.uint32).astype(np.uint64)
+    rounded = ((bits + 0x7FFF + ((bits >> 16) & 1)) >> 16) << 16
+    return rounded.astype(np.uint32).view(np.float32)
+
+
+def _ulps(got, gold):
+    gold = np.asarray(gold, np.float64)
+    return np.abs(_bf16(got).astype(np.float64) - gold).max() / (
+        max(np.abs(gold).max(), 1e-30) * BF16_EPS)
+
+
+SISO_KEYS = ("q", "k", "v", "adt", "dt", "trap", "q_bias", "k_bias")
+
+
+def _siso_gpu(x, **kw):
+    import armhackathon_amd as arm_scan
+
+    t = dev(x)
+    return arm_scan.mamba3_scan(*[t[k] for k in SISO_KEYS], cos=t["cos"], sin=t["sin"],
+                                D=t.get("D"), z=t.get("z"), **kw)
+
+
+def _siso_ref(x, **kw):
+    return oracle.mamba3_scan(*[x[k] for k in SISO_KEYS], x["cos"], x["sin"], D=x.get("D"),
+                              z=x.get("z"), dtype=np.float64, **kw)
+
+
+def test_m3_siso_goldens(golden_dir):
+    import torch
+
+    import armhackathon_amd as arm_scan
+
+    files = sorted((golden_dir / "mamba3").glob("*.npz"))
+    assert files
+    for f in files:
+        case(f"siso golden {f.name}")
+        z = np.load(f)
+        kw = {k[3:]: z[k] for k in z.files if k.startswith("kw_")}
+        t = {k: torch.from_numpy(np.ascontiguousarray(v, np.float32)).cuda()
+             for k, v in kw.items()}
+        out = arm_scan.mamba3_scan(t["Q"], t["K"], t["V"], t["ADT"], t["DT"], t["Trap"],
+                                   t["Q_bias"], t["K_bias"], angles=t["Angles"],
+                                   D=t.get("D"), z=t.get("Z"))
+        assert _ulps(host(out), z["out"]) <= 8.0, f.name
+
+
+def test_m3_mimo_goldens(golden_dir):
+    import torch
+
+    import armhackathon_amd as arm_scan
+
+    files = sorted((golden_dir / "mamba3_mimo").glob("*.npz"))
+    assert files
+    for f in files:
+        case(f"mimo golden {f.name}")
+        z = np.load(f)
+        kw = {k[3:]: z[k] for k in z.files if k.startswith("kw_")}
+        t = {k: torch.from_numpy(np.ascontiguousarray(v, np.float32)).cuda()
+             for k, v in kw.items()}
+        out = arm_scan.mamba3_mimo_scan(t["Q"], t["K"], t["V"], t["ADT"], t["DT"], t["Trap"],
+                                        t["Q_bias"], t["K_bias"], t["MIMO_V"], t["MIMO_Z"],
+                                        t["MIMO_Out"], angles=t["Angles"], D=t.get("D"),
+                                        z=t.get("Z"))
+        assert _ulps(host(out), z["out"]) <= 12.0, f.name
+
+
+SISO_SHAPES = [
+    # (batch, len, heads, dv, dqk, groups)
+    (1, 1, 1, 8, 8, 1),
+    (2, 37, 4, 16, 32, 1),
+    (1, 300, 3, 64, 128, 3),
+    (2, 130, 4, 32, 64, 2),
+]
+
+
+@pytest.mark.parametrize("shape", SISO_SHAPES, ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("reverse", [False, True])
+def test_m3_siso_vs_oracle(shape, reverse):
+    b, L, h, dv, dqk, g = shape
+    case(f"siso {shape} reverse={reverse}")
+    x = workloads.m3_siso(batch=b, length=L, heads=h, dv=dv, dqk=dqk, seed=L + h)
+    if g != h:
+        x["q"] = np.ascontiguousarray(x["q"][:, :, :g])
+        x["k"] = np.ascontiguousarray(x["k"][:, :, :g])
+    rng = np.random.default_rng(7)
+    x["q_bias"] = (rng.standard_normal((h, dqk)) * 0.1).astype(np.float32)
+    x["k_bias"] = (rng.standard_normal((h, dqk)) * 0.1).astype(np.float32)
+    x["D"] = rng.standard_normal(h).astype(np.float32)
+    x["z"] = rng.standard_normal(x["v"].shape).astype(np.float32)
+    out, ls, lbx = _siso_gpu(x, reverse=reverse, return_last_state=True)
+    ref, rls, rlbx = _siso_ref(x, reverse=reverse, want_state=True)
+    assert rel_err(host(out), ref.transpose(0, 2, 1, 3)) < TOL
+    assert rel_err(host(ls), rls) < TOL
+    assert rel_err(host(lbx), rlbx) < TOL
+
+
+MIMO_SHAPES = [
+    # (batch, len, heads, dv, dqk, rank, groups)
+    (1, 20, 2, 16, 32, 4, 1),
+    (2, 65, 4, 32, 64, 2, 4),
+    (1, 150, 2, 64, 128, 4, 2),
+]
+
+
+@pytest.mark.parametrize("shape", MIMO_SHAPES, ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("reverse", [False, True])
+def test_m3_mimo_vs_oracle(shape, reverse):
+    import armhackathon_amd as arm_scan
+
+    b, L, h, dv, dqk, r, g = shape
+    case(f"mimo {shape} reverse={reverse}")
+    x = workloads.m3_mimo(batch=b, length=L, heads=h, dv=dv, dqk=dqk, rank=r, seed=L)
+    if g != h:
+        x["q"] = np.ascontiguousarray(x["q"][:, :, :, :g])
+        x["k"] = np.ascontiguousarray(x["k"][:, :, :, :g])
+    rng = np.random.default_rng(9)
+    x["zeta"] = rng.standard_normal((h, r, dv)).astype(np.float32)
+    x["D"] = rng.standard_normal(h).astype(np.float32)
+    x["z"] = rng.standard_normal(x["v"].shape).astype(np.float32)
+    t = dev(x)
+    out, ls = arm_scan.mamba3_mimo_scan(
+        *[t[k] for k in SISO_KEYS], t["psi"], t["zeta"], t["phi"], cos=t["cos"], sin=t["sin"],
+        D=t["D"], z=t["z"], reverse=reverse, return_last_state=True)
+    ref, rls, _ = oracle.mamba3_scan(*[x[k] for k in SISO_KEYS], x["cos"], x["sin"], D=x["D"],
+                                     z=x["z"], psi=x["psi"], zeta=x["zeta"], phi=x["phi"],
+                                     reverse=reverse, dtype=np.float64, want_state=True)
+    assert rel_err(host(out), ref.transpose(0, 2, 1, 3)) < TOL
+    assert rel_err(host(ls), rls) < TOL
+
+
+def test_m3_pair_and_reverse_is_flip():
+    """reverse == flip -> forward -> flip (check_mamba3_op.py:99-121)."""
+    import armhackathon_amd as arm_scan
+
+    x = workloads.m3_siso(batch=1, length=50, heads=2, dv=16, dqk=32, seed=11)
+    case("siso pair / reverse flip")
+    t = dev(x)
+    fwd, bwd = arm_scan.mamba3_scan_pair(*[t[k] for k in SISO_KEYS], cos=t["cos"],
+                                         sin=t["sin"])
+    fl = {k: (np.ascontiguousarray(v[:, ::-1]) if k in ("q", "k", "v", "cos", "sin")
+              else np.ascontiguousarray(v[..., ::-1]) if k in ("adt", "dt", "trap") else v)
+          for k, v in x.items()}
+    f2 = _siso_gpu(fl)
+    assert rel_err(host(bwd), host(f2)[:, ::-1]) < 1e-5
+    assert rel_err(host(fwd), _siso_ref(x).transpose(0, 2, 1, 3)) < TOL
