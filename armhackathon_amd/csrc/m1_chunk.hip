@@ -1,0 +1,535 @@
+// Mamba-1 selective scan, one direction (forward or reverse index mode), on gfx950.
+//
+// Semantics: the reference's scalar::scan (kernel/arm-scan-core/src/scalar.rs:11-89),
+// per (batch, channel) row and state n:
+//   dt = softplus(delta + bias) (when asked);  h_n <- exp(dt A_n) h_n + dt u B_n
+//   y = sum_n C_n h_n ;  out = (y + D u) silu(z) ;  last_state = h after the last step
+// with reverse walking t = L-1 .. 0 while out[t] stays at index t.
+//
+// Decomposition. A row is cut into chunks of CH = LPR * I consecutive steps (in
+// traversal order); one row is owned by LPR lanes of a wave (64 / LPR rows per
+// wave), and lane j of the row owns steps [j*I, j*I + I) of the current chunk.
+// The wave walks the chunks of its rows in order, carrying the per-state row
+// state from chunk to chunk in LDS (wave-private, no barriers). Per chunk and
+// state n:
+//   pass 1  every lane discretises its I steps, a_i = 2^(dt_i * A_n log2 e),
+//           b_i = dt_i u_i B_n,i, and folds them into one affine map (a_tot, b_tot),
+//           with a_tot = 2^(A_n log2 e * sum dt) (one exp, not a product of I);
+//           the row's first lane folds the carried state in;
+//   scan    an inclusive DPP scan of the affine maps across the row's lanes
+//           (Hillis-Steele, row_shr 1/2/4/8 and, for 64-lane rows, the two row
+//           broadcasts) gives every lane the absolute state at the end of its
+//           block; a row_shr/wave_shr by one turns that into each lane's entry state;
+//   pass 2  each lane replays its steps from the entry state with the stored
+//           (a_i, b_i), accumulating y_i += C_n,i h_i.
+// exp(dt A) is evaluated exactly once per (step, state). B and C rows (shared by
+// all channels of a batch/group) are read straight from memory through the
+// caches with 16-byte loads, one state ahead of their use.
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "scan_common.h"
+#include "scan_launch.h"
+
+namespace armscan {
+
+namespace {
+
+struct M1Kern {
+  const float *u, *delta, *A, *B, *C, *D, *z, *bias, *h0;
+  float *out, *last;
+  long long L;
+  int rows, dim, N, groups, group_size, softplus;
+};
+
+constexpr int kWavesPerBlock = 4;
+
+// Inclusive Hillis-Steele scan steps as single VOP2 DPP instructions:
+//   v_fmac_f32_dpp b, b[src], a   ->  b = a * b[src] + b
+//   v_mul_f32_dpp  a, a[src], a   ->  a = a * a[src]
+// Lanes without a source lane (row/wave edge, masked rows) are not written, so
+// they keep their map (the identity step). Each DPP read of a VGPR needs two
+// wait states after the VALU write of that VGPR; the s_nops provide them.
+#define ARMSCAN_DPP_STEP(CTRL, MASK)                                           \
+  "s_nop 0\n\t"                                                               \
+  "v_fmac_f32_dpp %0, %0, %1 " CTRL " row_mask:" MASK " bank_mask:0xf\n\t"    \
+  "s_nop 0\n\t"                                                               \
+  "v_mul_f32_dpp %1, %1, %1 " CTRL " row_mask:" MASK " bank_mask:0xf\n\t"
+#define ARMSCAN_DPP_LAST(CTRL, MASK) \
+  "s_nop 0\n\t"                      \
+  "v_fmac_f32_dpp %0, %0, %1 " CTRL " row_mask:" MASK " bank_mask:0xf\n\t"
+
+// Scan primitives over one row of LPR lanes.
+template <int LPR> struct Row;
+
+template <> struct Row<16> {
+  // inclusive scan of affine maps (a, b) over the 16 lanes of each DPP row;
+  // on return b is the inclusive composition (a is left partially combined).
+  static __device__ __forceinline__ void scan(float& a, float& b) {
+    asm volatile("s_nop 1\n\t"
+                 ARMSCAN_DPP_STEP("row_shr:1", "0xf")
+                 ARMSCAN_DPP_STEP("row_shr:2", "0xf")
+                 ARMSCAN_DPP_STEP("row_shr:4", "0xf")
+                 ARMSCAN_DPP_LAST("row_shr:8", "0xf")
+                 "s_nop 1"
+                 : "+v"(b), "+v"(a));
+  }
+  // value of the previous lane of the row; the row's first lane gets `first`
+  static __device__ __forceinline__ float prev(float v, float first) {
+    return dpp<kRowShr1, 0xF>(first, v);
+  }
+  // the row's last lane's value, delivered to the row's first lane
+  static __device__ __forceinline__ float last_to_first(float v) {
+    return dpp<kRowMirror, 0xF>(0.0f, v);
+  }
+};
+
+template <> struct Row<64> {
+  static __device__ __forceinline__ void scan(float& a, float& b) {
+    asm volatile("s_nop 1\n\t"
+                 ARMSCAN_DPP_STEP("row_shr:1", "0xf")
+                 ARMSCAN_DPP_STEP("row_shr:2", "0xf")
+                 ARMSCAN_DPP_STEP("row_shr:4", "0xf")
+                 ARMSCAN_DPP_STEP("row_shr:8", "0xf")
+                 ARMSCAN_DPP_STEP("row_bcast:15", "0xa")
+                 ARMSCAN_DPP_LAST("row_bcast:31", "0xc")
+                 "s_nop 1"
+                 : "+v"(b), "+v"(a));
+  }
+  static __device__ __forceinline__ float prev(float v, float first) {
+    return dpp<kWaveShr1, 0xF>(first, v);
+  }
+  static __device__ __forceinline__ float last_to_first(float v) {
+    return dpp<kWaveRor1, 0xF>(0.0f, v);
+  }
+};
+
+// Load the I steps of one lane block in traversal order: step i of the block
+// starting at traversal index sb is memory t = sb + i (forward) or L-1-sb-i
+// (reverse). Steps past the row's end read `fill`.
+// Lv bounds the valid traversal indices (s < Lv); L is the row length used for
+// the reverse mapping (a FULL chunk passes Lv = sb + I so the check folds away).
+template <int I, bool REV, bool VEC>
+__device__ __forceinline__ void load_block(const float* __restrict__ row, long long Lv,
+                                           long long sb, float fill, float (&v)[I],
+                                           long long L) {
+  if (VEC) {
+    const long long mb = REV ? L - sb - I : sb;
+    const float4* p = reinterpret_cast<const float4*>(row + mb);
+#pragma unroll
+    for (int q = 0; q < I / 4; ++q) {
+      const float4 x = p[q];
+      const float w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[REV ? I - 1 - (4 * q + e) : 4 * q + e] = w[e];
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < I; ++i) {
+      const long long s = sb + i;
+      v[i] = s < Lv ? row[REV ? L - 1 - s : s] : fill;
+    }
+  }
+}
+
+template <int I, bool REV, bool VEC>
+__device__ __forceinline__ void store_block(float* __restrict__ row, long long Lv, long long sb,
+                                            const float (&v)[I], long long L) {
+  if (VEC) {
+    const long long mb = REV ? L - sb - I : sb;
+    float4* p = reinterpret_cast<float4*>(row + mb);
+#pragma unroll
+    for (int q = 0; q < I / 4; ++q) {
+      float w[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) w[e] = v[REV ? I - 1 - (4 * q + e) : 4 * q + e];
+      p[q] = make_float4(w[0], w[1], w[2], w[3]);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < I; ++i) {
+      const long long s = sb + i;
+      if (s < Lv) row[REV ? L - 1 - s : s] = v[i];
+    }
+  }
+}
+
+// One state n of one chunk given this lane's B/C blocks (bb, cc): pass 1, the
+// row scan, pass 2, and the carry into the next chunk. a2 = A[d][n] log2(e).
+template <int LPR, int I>
+__device__ __forceinline__ void state_core(int n, int j, float a2, float* carry,
+                                           float* last_n, const float (&dt)[I],
+                                           const float (&du)[I], float sdt, float (&y)[I],
+                                           const float (&bb)[I], const float (&cc)[I]) {
+  float a[I], b[I];
+  float bt = 0.0f;
+#pragma unroll
+  for (int i = 0; i < I; ++i) {
+    a[i] = ex2(dt[i] * a2);
+    b[i] = du[i] * bb[i];
+    bt = fmaf(a[i], bt, b[i]);
+  }
+  float at = ex2(a2 * sdt);
+  const float hc_row = carry[n];
+  const float hc = (j == 0) ? hc_row : 0.0f;
+  bt = fmaf(at, hc, bt);  // the row's first lane starts from the carried state
+  Row<LPR>::scan(at, bt);
+  float h = Row<LPR>::prev(bt, hc);  // state entering this lane's block
+#pragma unroll
+  for (int i = 0; i < I; ++i) {
+    h = fmaf(a[i], h, b[i]);
+    y[i] = fmaf(cc[i], h, y[i]);
+  }
+  const float hend = Row<LPR>::last_to_first(h);
+  if (j == 0) carry[n] = hend;
+  if (last_n && j == LPR - 1) *last_n = h;
+}
+
+// One state of the global-load path: the next state's B/C blocks are fetched
+// into (b1, c1) while this one computes from (b0, c0).
+template <int LPR, int I, bool REV, bool V>
+__device__ __forceinline__ void state(const M1Kern& p, int n, long long sb, long long Lv, int j,
+                                      bool valid, bool last_chunk, long long row,
+                                      const float* Bg, const float* Cg, const float* a2s,
+                                      float* carry, const float (&dt)[I], const float (&du)[I],
+                                      float sdt, float (&y)[I], const float (&b0)[I],
+                                      const float (&c0)[I], float (&b1)[I], float (&c1)[I]) {
+  const long long L = p.L;
+  if (n + 1 < p.N) {
+    load_block<I, REV, V>(Bg + (long long)(n + 1) * L, Lv, sb, 0.0f, b1, L);
+    load_block<I, REV, V>(Cg + (long long)(n + 1) * L, Lv, sb, 0.0f, c1, L);
+  }
+  float* last_n = (last_chunk && p.last && valid) ? p.last + row * p.N + n : nullptr;
+  state_core<LPR, I>(n, j, a2s[n], carry, last_n, dt, du, sdt, y, b0, c0);
+}
+
+// One chunk of a wave's rows. FULL: every lane's block lies inside the row
+// (no bounds checks; 16-byte accesses when VEC); otherwise the row's tail.
+// (dn, un) carry the raw delta/u blocks of this chunk when `have` (fetched during
+// the previous chunk); when `pre_sb` >= 0 this chunk fetches the next chunk's
+// blocks (at traversal base pre_sb) into them half-way through its states.
+template <int LPR, int I, bool REV, bool VEC, bool FULL>
+__device__ __forceinline__ void chunk(const M1Kern& p, long long sb, int j, bool valid,
+                                      bool last_chunk, long long row, const float* urow,
+                                      const float* drow, const float* zrow, float* orow,
+                                      const float* Bg, const float* Cg, const float* a2s,
+                                      float bias, float dskip, float* carry, float (&dn)[I],
+                                      float (&un)[I], bool have, long long pre_sb) {
+  constexpr bool V = VEC && FULL;
+  const long long L = p.L;
+  const int N = p.N;
+  const long long Lv = FULL ? sb + I : L;  // FULL: the block is known to fit
+  float dt[I], du[I], y[I];
+  float sdt = 0.0f;
+  if (!have) {
+    load_block<I, REV, V>(drow, Lv, sb, 0.0f, dn, L);
+    load_block<I, REV, V>(urow, Lv, sb, 0.0f, un, L);
+  }
+#pragma unroll
+  for (int i = 0; i < I; ++i) {
+    float x = dn[i] + bias;
+    if (p.softplus) x = softplus_fast(x);
+    if (!FULL) x = (sb + i < L) ? x : 0.0f;  // padding steps are the identity map
+    dt[i] = x;
+    du[i] = x * un[i];
+    y[i] = dskip * un[i];
+    sdt += x;
+  }
+  if (!FULL) {
+    // the row's tail: bounds-checked loads, no prefetching (keeps registers low)
+    for (int n = 0; n < N; ++n) {
+      float bb[I], cc[I];
+      load_block<I, REV, false>(Bg + (long long)n * L, Lv, sb, 0.0f, bb, L);
+      load_block<I, REV, false>(Cg + (long long)n * L, Lv, sb, 0.0f, cc, L);
+      float* last_n = (last_chunk && p.last && valid) ? p.last + row * N + n : nullptr;
+      state_core<LPR, I>(n, j, a2s[n], carry, last_n, dt, du, sdt, y, bb, cc);
+    }
+    if (zrow) {
+      float zz[I];
+      load_block<I, REV, false>(zrow, Lv, sb, 0.0f, zz, L);
+#pragma unroll
+      for (int i = 0; i < I; ++i) y[i] *= silu_fast(zz[i]);
+    }
+    if (valid) store_block<I, REV, false>(orow, Lv, sb, y, L);
+    return;
+  }
+  float bv[I], cv[I], bn[I], cn[I], zz[I];
+  load_block<I, REV, V>(Bg, Lv, sb, 0.0f, bv, L);
+  load_block<I, REV, V>(Cg, Lv, sb, 0.0f, cv, L);
+  const int half = (N / 2) & ~1;
+  // states in pairs, ping-ponging the B/C registers: state n computes from
+  // (bv, cv) while the loads of state n+1 land in (bn, cn)
+  for (int n = 0; n < N; n += 2) {
+    if (n == half && pre_sb >= 0) {
+      load_block<I, REV, VEC>(drow, L, pre_sb, 0.0f, dn, L);
+      load_block<I, REV, VEC>(urow, L, pre_sb, 0.0f, un, L);
+    }
+    if (zrow && n + 2 >= N) load_block<I, REV, V>(zrow, Lv, sb, 0.0f, zz, L);
+    state<LPR, I, REV, V>(p, n, sb, Lv, j, valid, last_chunk, row, Bg, Cg, a2s, carry, dt, du,
+                          sdt, y, bv, cv, bn, cn);
+    if (n + 1 < N)
+      state<LPR, I, REV, V>(p, n + 1, sb, Lv, j, valid, last_chunk, row, Bg, Cg, a2s, carry,
+                            dt, du, sdt, y, bn, cn, bv, cv);
+  }
+  if (zrow) {
+#pragma unroll
+    for (int i = 0; i < I; ++i) y[i] *= silu_fast(zz[i]);
+  }
+  if (valid) store_block<I, REV, V>(orow, Lv, sb, y, L);
+}
+
+template <int LPR, int I, bool REV, bool VEC>
+__global__ void __launch_bounds__(64 * kWavesPerBlock, 2)
+m1_chunk_kernel(M1Kern p) {
+  constexpr int RPW = 64 / LPR;  // rows per wave
+  constexpr long long CH = (long long)LPR * I;
+  extern __shared__ float s_lds[];  // carry [wave][row][N], then A*log2e [wave][row][N]
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int j = lane % LPR;
+  const int rw = lane / LPR;
+  const long long row_raw = ((long long)blockIdx.x * kWavesPerBlock + wave) * RPW + rw;
+  const bool valid = row_raw < p.rows;
+  const long long row = valid ? row_raw : (long long)p.rows - 1;
+  const long long L = p.L;
+  const int N = p.N;
+  const int bi = (int)(row / p.dim), d = (int)(row - (long long)bi * p.dim);
+  const int g = d / p.group_size;
+  const float* urow = p.u + row * L;
+  const float* drow = p.delta + row * L;
+  const float* zrow = p.z ? p.z + row * L : nullptr;
+  float* orow = p.out + row * L;
+  const float* Bg = p.B + ((long long)bi * p.groups + g) * N * L;
+  const float* Cg = p.C + ((long long)bi * p.groups + g) * N * L;
+  const float* Arow = p.A + (long long)d * N;
+  const float bias = p.bias ? p.bias[d] : 0.0f;
+  const float dskip = p.D ? p.D[d] : 0.0f;
+  float* carry = s_lds + (wave * RPW + rw) * N;
+  float* a2s = s_lds + (kWavesPerBlock * RPW + wave * RPW + rw) * N;
+
+  if (j == 0)
+    for (int n = 0; n < N; ++n) {
+      carry[n] = p.h0 ? p.h0[row * N + n] : 0.0f;
+      a2s[n] = Arow[n] * kLog2e;
+    }
+
+  const long long nch = (L + CH - 1) / CH;
+  const long long nfull = L / CH;  // chunks that lie entirely inside the row
+  float dn[I], un[I];
+  for (long long c = 0; c < nfull; ++c) {
+    const long long pre = c + 1 < nfull ? (c + 1) * CH + (long long)j * I : -1;
+    chunk<LPR, I, REV, VEC, true>(p, c * CH + (long long)j * I, j, valid, c + 1 == nch, row,
+                                  urow, drow, zrow, orow, Bg, Cg, a2s, bias, dskip, carry, dn,
+                                  un, c > 0, pre);
+  }
+  if (nfull < nch)
+    chunk<LPR, I, REV, VEC, false>(p, nfull * CH + (long long)j * I, j, valid, true, row, urow,
+                                   drow, zrow, orow, Bg, Cg, a2s, bias, dskip, carry, dn, un,
+                                   false, -1);
+}
+
+// ---------------------------------------------------------------------------
+// LDS-tiled variant (16 lanes x 16 steps per row, 4 rows per wave, 16 rows per
+// block, all in one batch/group). B and C are the per-element operands that
+// dominate the on-chip traffic (two floats per step and state in every lane),
+// so instead of each wave pulling them through the L1 the block stages them
+// once per chunk in LDS, in tiles of kTileStates states x 256 steps (B rows then
+// C rows), double-buffered and filled by direct-to-LDS DMA
+// (global_load_lds_dwordx4): no VGPRs are spent on staging and the next tile
+// streams in while the current one is consumed. One barrier per tile.
+//
+// Tile row layout: a row of 256 floats is 64 pieces of 4 floats; lane j of a
+// DPP row reads pieces 4j'..4j'+3 (j' = j forward, 15-j reverse) with four
+// ds_read_b128, the q-th of which hits slot 16q + j': the 16 lanes of each
+// read touch 256 contiguous bytes (no bank conflicts). The DMA therefore writes
+// piece 4(s & 15) + (s >> 4) into slot s.
+constexpr int kTileStates = 8;
+constexpr int kTileRowFloats = 256;                       // 16 lanes x 16 steps
+constexpr int kTileFloats = 2 * kTileStates * kTileRowFloats;  // B rows then C rows
+
+template <bool REV>
+__device__ __forceinline__ void lds_block16(const float* __restrict__ trow, int j,
+                                            float (&v)[16]) {
+  const int jj = REV ? 15 - j : j;
+  const float4* t = reinterpret_cast<const float4*>(trow);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const float4 x = t[16 * q + jj];
+    const float w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[REV ? 15 - (4 * q + e) : 4 * q + e] = w[e];
+  }
+}
+
+// DMA one tile (states n0 .. n0+kTileStates-1 of the chunk whose memory range
+// starts at mem0) into `tile`; each wave moves kTileStates*2/kWavesPerBlock rows.
+__device__ __forceinline__ void issue_tile(float* tile, const float* Bg, const float* Cg,
+                                           long long L, long long mem0, int n0, int N,
+                                           int wave, int lane) {
+  const int piece = 4 * (lane & 15) + (lane >> 4);
+#pragma unroll
+  for (int r = 0; r < 2 * kTileStates / kWavesPerBlock; ++r) {
+    const int k = wave * (2 * kTileStates / kWavesPerBlock) + r;  // tile row, wave-uniform
+    const int n = n0 + (k % kTileStates);
+    if (n < N) {
+      const float* src = (k < kTileStates ? Bg : Cg) + (long long)n * L + mem0 + 4 * piece;
+      __builtin_amdgcn_global_load_lds(
+          (const void*)src,
+          (__attribute__((address_space(3))) void*)(tile + k * kTileRowFloats), 16, 0, 0);
+    }
+  }
+}
+
+__device__ __forceinline__ void tile_sync() {
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's DMA (and every other access) landed
+  __syncthreads();
+}
+
+template <bool REV>
+__global__ void __launch_bounds__(64 * kWavesPerBlock, 3)
+m1_tile_kernel(M1Kern p) {
+  constexpr int LPR = 16, I = 16, RPW = 4;
+  constexpr long long CH = LPR * I;
+  extern __shared__ __attribute__((aligned(16))) float s_lds[];
+  float* tiles = s_lds;                                  // [2][kTileFloats]
+  float* small = s_lds + 2 * kTileFloats;                // carry, then A*log2e
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int j = lane % LPR;
+  const int rw = lane / LPR;
+  const long long row = ((long long)blockIdx.x * kWavesPerBlock + wave) * RPW + rw;
+  const long long L = p.L;
+  const int N = p.N;
+  const int bi = (int)(row / p.dim), d = (int)(row - (long long)bi * p.dim);
+  const int g = d / p.group_size;
+  const float* urow = p.u + row * L;
+  const float* drow = p.delta + row * L;
+  const float* zrow = p.z ? p.z + row * L : nullptr;
+  float* orow = p.out + row * L;
+  const float* Bg = p.B + ((long long)bi * p.groups + g) * N * L;
+  const float* Cg = p.C + ((long long)bi * p.groups + g) * N * L;
+  const float* Arow = p.A + (long long)d * N;
+  const float bias = p.bias ? p.bias[d] : 0.0f;
+  const float dskip = p.D ? p.D[d] : 0.0f;
+  float* carry = small + (wave * RPW + rw) * N;
+  float* a2s = small + (kWavesPerBlock * RPW + wave * RPW + rw) * N;
+  if (j == 0)
+    for (int n = 0; n < N; ++n) {
+      carry[n] = p.h0 ? p.h0[row * N + n] : 0.0f;
+      a2s[n] = Arow[n] * kLog2e;
+    }
+
+  const long long nch = (L + CH - 1) / CH;
+  const long long nfull = L / CH;
+  const int ng = (N + kTileStates - 1) / kTileStates;  // tiles per chunk
+  const long long ntiles = nfull * ng;
+  auto mem0 = [&](long long c) { return REV ? L - (c + 1) * CH : c * CH; };
+  if (ntiles > 0) issue_tile(tiles, Bg, Cg, L, mem0(0), 0, N, wave, lane);
+  tile_sync();
+
+  long long k = 0;  // tile counter
+  for (long long c = 0; c < nfull; ++c) {
+    const long long sb = c * CH + (long long)j * I;
+    float dt[I], du[I], y[I], zz[I];
+    float sdt = 0.0f;
+    {
+      float dd[I], uu[I];
+      load_block<I, REV, true>(drow, L, sb, 0.0f, dd, L);
+      load_block<I, REV, true>(urow, L, sb, 0.0f, uu, L);
+#pragma unroll
+      for (int i = 0; i < I; ++i) {
+        float x = dd[i] + bias;
+        if (p.softplus) x = softplus_fast(x);
+        dt[i] = x;
+        du[i] = x * uu[i];
+        y[i] = dskip * uu[i];
+        sdt += x;
+      }
+    }
+    const bool last_chunk = c + 1 == nch;
+    for (int q = 0; q < ng; ++q, ++k) {
+      if (k + 1 < ntiles) {
+        const long long cn = (k + 1) / ng;
+        const int qn = (int)((k + 1) % ng);
+        issue_tile(tiles + ((k + 1) & 1) * kTileFloats, Bg, Cg, L, mem0(cn), qn * kTileStates,
+                   N, wave, lane);
+      }
+      if (zrow && q + 1 == ng) load_block<I, REV, true>(zrow, L, sb, 0.0f, zz, L);
+      const float* tile = tiles + (k & 1) * kTileFloats;
+      const int n0 = q * kTileStates;
+      const int n1 = n0 + kTileStates < N ? n0 + kTileStates : N;
+      for (int n = n0; n < n1; ++n) {
+        float bb[I], cc[I];
+        lds_block16<REV>(tile + (n - n0) * kTileRowFloats, j, bb);
+        lds_block16<REV>(tile + (kTileStates + n - n0) * kTileRowFloats, j, cc);
+        float* last_n = (last_chunk && p.last) ? p.last + row * N + n : nullptr;
+        state_core<LPR, I>(n, j, a2s[n], carry, last_n, dt, du, sdt, y, bb, cc);
+      }
+      tile_sync();
+    }
+    if (zrow) {
+#pragma unroll
+      for (int i = 0; i < I; ++i) y[i] *= silu_fast(zz[i]);
+    }
+    store_block<I, REV, true>(orow, L, sb, y, L);
+  }
+  if (nfull < nch) {
+    // the row's tail chunk goes through the bounds-checked global-load path
+    float dn[I], un[I];
+    chunk<LPR, I, REV, true, false>(p, nfull * CH + (long long)j * I, j, true, true, row, urow,
+                                    drow, zrow, orow, Bg, Cg, a2s, bias, dskip, carry, dn, un,
+                                    false, -1);
+  }
+}
+
+template <bool REV>
+hipError_t launch_tile(const M1Kern& k, hipStream_t st) {
+  constexpr int RPB = kWavesPerBlock * 4;
+  const long long blocks = (long long)k.rows / RPB;
+  const size_t lds = sizeof(float) * (2 * (size_t)kTileFloats + 2 * (size_t)RPB * k.N);
+  hipLaunchKernelGGL((m1_tile_kernel<REV>), dim3((unsigned)blocks), dim3(64 * kWavesPerBlock),
+                     lds, st, k);
+  return hipGetLastError();
+}
+
+template <int LPR, int I, bool REV, bool VEC>
+hipError_t launch(const M1Kern& k, hipStream_t st) {
+  constexpr int RPB = kWavesPerBlock * (64 / LPR);
+  const long long blocks = ((long long)k.rows + RPB - 1) / RPB;
+  const size_t lds = 2 * sizeof(float) * (size_t)kWavesPerBlock * (64 / LPR) * k.N;
+  hipLaunchKernelGGL((m1_chunk_kernel<LPR, I, REV, VEC>), dim3((unsigned)blocks),
+                     dim3(64 * kWavesPerBlock), lds, st, k);
+  return hipGetLastError();
+}
+
+template <int LPR, int I>
+hipError_t launch_dir(const M1Kern& k, bool rev, bool vec, hipStream_t st) {
+  if (rev) return vec ? launch<LPR, I, true, true>(k, st) : launch<LPR, I, true, false>(k, st);
+  return vec ? launch<LPR, I, false, true>(k, st) : launch<LPR, I, false, false>(k, st);
+}
+
+bool aligned16(const void* q) { return q == nullptr || ((uintptr_t)q & 15u) == 0; }
+
+}  // namespace
+
+hipError_t m1_scan_chunked(const M1Problem& pr, hipStream_t st) {
+  M1Kern k{};
+  k.u = pr.u; k.delta = pr.delta; k.A = pr.A; k.B = pr.B; k.C = pr.C; k.D = pr.D; k.z = pr.z;
+  k.bias = pr.bias; k.h0 = pr.h0; k.out = pr.out; k.last = pr.last;
+  k.L = (long long)pr.len; k.rows = (int)(pr.batch * pr.dim); k.dim = (int)pr.dim;
+  k.N = (int)pr.state; k.groups = (int)pr.groups; k.group_size = (int)(pr.dim / pr.groups);
+  k.softplus = pr.softplus;
+  const bool vec = pr.len % 4 == 0 && aligned16(pr.u) && aligned16(pr.delta) &&
+                   aligned16(pr.B) && aligned16(pr.C) && aligned16(pr.z) && aligned16(pr.out);
+  const bool rev = pr.reverse != 0;
+  // the tiled path needs every 16-row block inside one batch/group and 16-byte rows
+  const bool tiled = vec && pr.dim % 16 == 0 && (pr.dim / pr.groups) % 16 == 0;
+  if (tiled) return rev ? launch_tile<true>(k, st) : launch_tile<false>(k, st);
+  return launch_dir<16, 16>(k, rev, vec, st);
+}
+
+}  // namespace armscan

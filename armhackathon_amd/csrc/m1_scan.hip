@@ -618,6 +618,10 @@ static void fill_args(M1Args& a, const M1Problem& pr) {
 }
 
 hipError_t m1_scan(const M1Problem& pr, hipStream_t st) {
+  return m1_scan_chunked(pr, st);
+}
+
+hipError_t m1_scan_lds(const M1Problem& pr, hipStream_t st) {
   M1Args a{};
   fill_args(a, pr);
   const long long rows = (long long)pr.batch * pr.dim;

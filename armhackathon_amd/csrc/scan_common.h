@@ -31,6 +31,19 @@ __device__ __forceinline__ float softplus(float x) {
 }
 // silu(x) = x / (1 + e^-x) (float.rs:41-43).
 __device__ __forceinline__ float silu(float x) { return x / (1.0f + fexp(-x)); }
+// The same with the hardware reciprocal (v_rcp_f32, 1 ulp) in place of the
+// IEEE division: the hot-loop epilogues use this one.
+__device__ __forceinline__ float silu_fast(float x) {
+  return x * __builtin_amdgcn_rcpf(1.0f + fexp(-x));
+}
+// softplus as above with the division replaced by v_rcp_f32.
+__device__ __forceinline__ float softplus_fast(float x) {
+  if (x > 20.0f) return x;
+  const float e = fexp(x);
+  const float u = 1.0f + e;
+  const float d = u - 1.0f;
+  return d == 0.0f ? e : (lg2(u) * kLn2) * (e * __builtin_amdgcn_rcpf(d));
+}
 // sigmoid evaluated on the non-positive branch (float.rs:52-59).
 __device__ __forceinline__ float sigmoid(float x) {
   if (x >= 0.0f) return 1.0f / (1.0f + fexp(-x));
@@ -50,6 +63,8 @@ constexpr int kRowShl1 = 0x101, kRowShl2 = 0x102, kRowShl4 = 0x104, kRowShl8 = 0
 constexpr int kRowShr1 = 0x111, kRowShr2 = 0x112, kRowShr4 = 0x114, kRowShr8 = 0x118;
 constexpr int kWaveShl1 = 0x130, kWaveShr1 = 0x138;
 constexpr int kRowBcast15 = 0x142, kRowBcast31 = 0x143;
+constexpr int kRowRor1 = 0x121, kWaveRor1 = 0x13C;
+constexpr int kRowMirror = 0x140, kRowHalfMirror = 0x141;
 
 __device__ __forceinline__ float readlane(float v, int lane) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));

@@ -19,6 +19,8 @@ struct M1Problem {
 };
 
 hipError_t m1_scan(const M1Problem& p, hipStream_t st);
+// One direction through the chunked DPP-scan kernel (m1_chunk.hip).
+hipError_t m1_scan_chunked(const M1Problem& p, hipStream_t st);
 // True when the fused bidirectional kernel can hold a whole row in one pass.
 bool m1_bidir_fusable(const M1Problem& p);
 hipError_t m1_bidir(const M1Problem& p, hipStream_t st);

@@ -69,6 +69,12 @@ SHAPES = [
     (3, 10, 4096, 16, 2),
     (1, 8, 9000, 8, 1),
     (2, 64, 333, 16, 64),
+    # 16-row blocks inside one batch/group (the LDS-tiled kernel), with row tails
+    (2, 32, 1000, 16, 1),
+    (1, 16, 300, 16, 1),
+    (1, 32, 600, 13, 2),
+    (2, 48, 512, 8, 3),
+    (1, 16, 4096, 16, 1),
 ]
 
 
