@@ -45,6 +45,9 @@ struct M1Kern {
 };
 
 constexpr int kWavesPerBlock = 4;
+#ifndef M1_TILE_I
+#define M1_TILE_I 16
+#endif
 
 // Inclusive Hillis-Steele scan steps as single VOP2 DPP instructions:
 //   v_fmac_f32_dpp b, b[src], a   ->  b = a * b[src] + b
@@ -84,6 +87,11 @@ template <> struct Row<16> {
   static __device__ __forceinline__ float last_to_first(float v) {
     return dpp<kRowMirror, 0xF>(0.0f, v);
   }
+  // h = a0 * (b_incl of the previous lane) + h; the row's first lane keeps h
+  static __device__ __forceinline__ void step_from_prev(float& h, float b_incl, float a0) {
+    asm volatile("v_fmac_f32_dpp %0, %1, %2 row_shr:1 row_mask:0xf bank_mask:0xf"
+                 : "+v"(h) : "v"(b_incl), "v"(a0));
+  }
 };
 
 template <> struct Row<64> {
@@ -103,6 +111,10 @@ template <> struct Row<64> {
   }
   static __device__ __forceinline__ float last_to_first(float v) {
     return dpp<kWaveRor1, 0xF>(0.0f, v);
+  }
+  static __device__ __forceinline__ void step_from_prev(float& h, float b_incl, float a0) {
+    asm volatile("v_fmac_f32_dpp %0, %1, %2 wave_shr:1 row_mask:0xf bank_mask:0xf"
+                 : "+v"(h) : "v"(b_incl), "v"(a0));
   }
 };
 
@@ -332,53 +344,66 @@ m1_chunk_kernel(M1Kern p) {
 }
 
 // ---------------------------------------------------------------------------
-// LDS-tiled variant (16 lanes x 16 steps per row, 4 rows per wave, 16 rows per
+// LDS-tiled variant (16 lanes x I steps per row, 4 rows per wave, 16 rows per
 // block, all in one batch/group). B and C are the per-element operands that
 // dominate the on-chip traffic (two floats per step and state in every lane),
 // so instead of each wave pulling them through the L1 the block stages them
-// once per chunk in LDS, in tiles of kTileStates states x 256 steps (B rows then
-// C rows), double-buffered and filled by direct-to-LDS DMA
+// once per chunk in LDS, in tiles of kTileStates states x CH = 16*I steps (B
+// rows then C rows), double-buffered and filled by direct-to-LDS DMA
 // (global_load_lds_dwordx4): no VGPRs are spent on staging and the next tile
 // streams in while the current one is consumed. One barrier per tile.
 //
-// Tile row layout: a row of 256 floats is 64 pieces of 4 floats; lane j of a
-// DPP row reads pieces 4j'..4j'+3 (j' = j forward, 15-j reverse) with four
-// ds_read_b128, the q-th of which hits slot 16q + j': the 16 lanes of each
-// read touch 256 contiguous bytes (no bank conflicts). The DMA therefore writes
-// piece 4(s & 15) + (s >> 4) into slot s.
+// Tile row layout: a row of CH floats is 4I pieces of 4 floats; lane j of a
+// DPP row reads its I/4 pieces (j' = j forward, 15-j reverse) with I/4
+// ds_read_b128, the q-th of which hits slot 16q + j' of the row: the 16 lanes of
+// each read touch 256 contiguous bytes (no bank conflicts). Slot t of a row
+// therefore holds piece (I/4)(t mod 16) + t/16, and that is what the DMA writes.
 constexpr int kTileStates = 8;
-constexpr int kTileRowFloats = 256;                       // 16 lanes x 16 steps
-constexpr int kTileFloats = 2 * kTileStates * kTileRowFloats;  // B rows then C rows
 
-template <bool REV>
-__device__ __forceinline__ void lds_block16(const float* __restrict__ trow, int j,
-                                            float (&v)[16]) {
+template <int I> struct Tile {
+  static constexpr int CH = 16 * I;                    // steps per chunk (row floats)
+  static constexpr int QP = I / 4;                     // pieces per lane
+  static constexpr int FLOATS = 2 * kTileStates * CH;  // B rows then C rows
+  static constexpr int DMA = FLOATS / 256;             // wave-wide 16-byte DMA ops
+};
+
+template <int I, bool REV>
+__device__ __forceinline__ void lds_block(const float* __restrict__ trow, int j,
+                                          float (&v)[I]) {
   const int jj = REV ? 15 - j : j;
   const float4* t = reinterpret_cast<const float4*>(trow);
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
+  for (int q = 0; q < I / 4; ++q) {
     const float4 x = t[16 * q + jj];
     const float w[4] = {x.x, x.y, x.z, x.w};
 #pragma unroll
-    for (int e = 0; e < 4; ++e) v[REV ? 15 - (4 * q + e) : 4 * q + e] = w[e];
+    for (int e = 0; e < 4; ++e) v[REV ? I - 1 - (4 * q + e) : 4 * q + e] = w[e];
   }
 }
 
 // DMA one tile (states n0 .. n0+kTileStates-1 of the chunk whose memory range
-// starts at mem0) into `tile`; each wave moves kTileStates*2/kWavesPerBlock rows.
+// starts at mem0) into `tile`. Each DMA op fills 256 consecutive tile floats;
+// the block's waves take turns.
+template <int I>
 __device__ __forceinline__ void issue_tile(float* tile, const float* Bg, const float* Cg,
                                            long long L, long long mem0, int n0, int N,
                                            int wave, int lane) {
-  const int piece = 4 * (lane & 15) + (lane >> 4);
+  using G = Tile<I>;
+  constexpr int SPR = G::CH / 4;  // slots per tile row
+  const int t = lane % SPR;
+  const int piece = G::QP * (t & 15) + (t >> 4);
 #pragma unroll
-  for (int r = 0; r < 2 * kTileStates / kWavesPerBlock; ++r) {
-    const int k = wave * (2 * kTileStates / kWavesPerBlock) + r;  // tile row, wave-uniform
-    const int n = n0 + (k % kTileStates);
-    if (n < N) {
-      const float* src = (k < kTileStates ? Bg : Cg) + (long long)n * L + mem0 + 4 * piece;
-      __builtin_amdgcn_global_load_lds(
-          (const void*)src,
-          (__attribute__((address_space(3))) void*)(tile + k * kTileRowFloats), 16, 0, 0);
+  for (int m0 = 0; m0 < G::DMA; m0 += kWavesPerBlock) {
+    const int m = m0 + wave;  // wave-uniform
+    if (G::DMA % kWavesPerBlock == 0 || m < G::DMA) {
+      const int k = m * (256 / G::CH) + lane / SPR;  // tile row of this lane
+      const int n = n0 + (k % kTileStates);
+      if (n < N) {
+        const float* src = (k < kTileStates ? Bg : Cg) + (long long)n * L + mem0 + 4 * piece;
+        __builtin_amdgcn_global_load_lds(
+            (const void*)src, (__attribute__((address_space(3))) void*)(tile + m * 256), 16, 0,
+            0);
+      }
     }
   }
 }
@@ -388,14 +413,73 @@ __device__ __forceinline__ void tile_sync() {
   __syncthreads();
 }
 
-template <bool REV>
-__global__ void __launch_bounds__(64 * kWavesPerBlock, 3)
+// State core of the tiled path. hc is the carried row state in the row's first
+// lane and 0 in the others; it is folded into b_0 so that pass 1's aggregate
+// and pass 2's first step include it. The row's last lane returns the state at
+// the end of the chunk (the value in other lanes is meaningless).
+template <int I>
+__device__ __forceinline__ float tile_state(float a2, float hc, const float (&dt)[I],
+                                            const float (&du)[I], float sdt, float (&y)[I],
+                                            const float (&bb)[I], const float (&cc)[I]) {
+  float a[I], b[I];
+#pragma unroll
+  for (int i = 0; i < I; ++i) {
+    a[i] = ex2(dt[i] * a2);
+    b[i] = du[i] * bb[i];
+  }
+  b[0] = fmaf(a[0], hc, b[0]);
+  float bt = b[0];
+#pragma unroll
+  for (int i = 1; i < I; ++i) bt = fmaf(a[i], bt, b[i]);
+  float at = ex2(a2 * sdt);
+  Row<16>::scan(at, bt);
+  float h = b[0];
+  Row<16>::step_from_prev(h, bt, a[0]);  // state after this lane's first step
+  y[0] = fmaf(cc[0], h, y[0]);
+#pragma unroll
+  for (int i = 1; i < I; ++i) {
+    h = fmaf(a[i], h, b[i]);
+    y[i] = fmaf(cc[i], h, y[i]);
+  }
+  return h;
+}
+
+// The states n0 .. n0+kTileStates-1 of one chunk from one LDS tile, unrolled so
+// that the LDS offsets are immediates. cbase points at the row's carries for
+// the row's first lane and at zeros for the others.
+template <int I, bool REV>
+__device__ __forceinline__ void tile_states(const float* tile, int n0, int N, int j,
+                                            const float* a2s, const float* cbase,
+                                            float* carry, float* last_row,
+                                            const float (&dt)[I], const float (&du)[I],
+                                            float sdt, float (&y)[I]) {
+  constexpr int CH = Tile<I>::CH;
+#pragma unroll
+  for (int s = 0; s < kTileStates; ++s) {
+    if (n0 + s < N) {
+      float cc[I], bb[I];
+      lds_block<I, REV>(tile + s * CH, j, bb);
+      lds_block<I, REV>(tile + (kTileStates + s) * CH, j, cc);
+      const float a2 = a2s[n0 + s];
+      const float hc = cbase[n0 + s];
+      const float h = tile_state<I>(a2, hc, dt, du, sdt, y, bb, cc);
+      if (j == 15) {
+        carry[n0 + s] = h;
+        if (last_row) last_row[n0 + s] = h;
+      }
+    }
+  }
+}
+
+template <int I, bool REV>
+__global__ void __launch_bounds__(64 * kWavesPerBlock)
 m1_tile_kernel(M1Kern p) {
-  constexpr int LPR = 16, I = 16, RPW = 4;
-  constexpr long long CH = LPR * I;
+  constexpr int LPR = 16, RPW = 4;
+  using G = Tile<I>;
+  constexpr long long CH = G::CH;
   extern __shared__ __attribute__((aligned(16))) float s_lds[];
-  float* tiles = s_lds;                                  // [2][kTileFloats]
-  float* small = s_lds + 2 * kTileFloats;                // carry, then A*log2e
+  float* tiles = s_lds;                                  // [2][G::FLOATS]
+  float* small = s_lds + 2 * G::FLOATS;                  // carry, A*log2e, zeros
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -417,18 +501,21 @@ m1_tile_kernel(M1Kern p) {
   const float dskip = p.D ? p.D[d] : 0.0f;
   float* carry = small + (wave * RPW + rw) * N;
   float* a2s = small + (kWavesPerBlock * RPW + wave * RPW + rw) * N;
+  float* zeros = small + 2 * kWavesPerBlock * RPW * N;
+  const float* cbase = j == 0 ? carry : zeros;
   if (j == 0)
     for (int n = 0; n < N; ++n) {
       carry[n] = p.h0 ? p.h0[row * N + n] : 0.0f;
       a2s[n] = Arow[n] * kLog2e;
     }
+  for (int i = threadIdx.x; i < N; i += blockDim.x) zeros[i] = 0.0f;
 
   const long long nch = (L + CH - 1) / CH;
   const long long nfull = L / CH;
   const int ng = (N + kTileStates - 1) / kTileStates;  // tiles per chunk
   const long long ntiles = nfull * ng;
   auto mem0 = [&](long long c) { return REV ? L - (c + 1) * CH : c * CH; };
-  if (ntiles > 0) issue_tile(tiles, Bg, Cg, L, mem0(0), 0, N, wave, lane);
+  if (ntiles > 0) issue_tile<I>(tiles, Bg, Cg, L, mem0(0), 0, N, wave, lane);
   tile_sync();
 
   long long k = 0;  // tile counter
@@ -455,20 +542,13 @@ m1_tile_kernel(M1Kern p) {
       if (k + 1 < ntiles) {
         const long long cn = (k + 1) / ng;
         const int qn = (int)((k + 1) % ng);
-        issue_tile(tiles + ((k + 1) & 1) * kTileFloats, Bg, Cg, L, mem0(cn), qn * kTileStates,
-                   N, wave, lane);
+        issue_tile<I>(tiles + ((k + 1) & 1) * G::FLOATS, Bg, Cg, L, mem0(cn),
+                      qn * kTileStates, N, wave, lane);
       }
       if (zrow && q + 1 == ng) load_block<I, REV, true>(zrow, L, sb, 0.0f, zz, L);
-      const float* tile = tiles + (k & 1) * kTileFloats;
-      const int n0 = q * kTileStates;
-      const int n1 = n0 + kTileStates < N ? n0 + kTileStates : N;
-      for (int n = n0; n < n1; ++n) {
-        float bb[I], cc[I];
-        lds_block16<REV>(tile + (n - n0) * kTileRowFloats, j, bb);
-        lds_block16<REV>(tile + (kTileStates + n - n0) * kTileRowFloats, j, cc);
-        float* last_n = (last_chunk && p.last) ? p.last + row * N + n : nullptr;
-        state_core<LPR, I>(n, j, a2s[n], carry, last_n, dt, du, sdt, y, bb, cc);
-      }
+      tile_states<I, REV>(tiles + (k & 1) * G::FLOATS, q * kTileStates, N, j, a2s, cbase,
+                          carry, (last_chunk && p.last) ? p.last + row * N : nullptr, dt, du,
+                          sdt, y);
       tile_sync();
     }
     if (zrow) {
@@ -486,13 +566,14 @@ m1_tile_kernel(M1Kern p) {
   }
 }
 
-template <bool REV>
+template <int I, bool REV>
 hipError_t launch_tile(const M1Kern& k, hipStream_t st) {
   constexpr int RPB = kWavesPerBlock * 4;
   const long long blocks = (long long)k.rows / RPB;
-  const size_t lds = sizeof(float) * (2 * (size_t)kTileFloats + 2 * (size_t)RPB * k.N);
-  hipLaunchKernelGGL((m1_tile_kernel<REV>), dim3((unsigned)blocks), dim3(64 * kWavesPerBlock),
-                     lds, st, k);
+  const size_t lds =
+      sizeof(float) * (2 * (size_t)Tile<I>::FLOATS + (2 * (size_t)RPB + 1) * k.N);
+  hipLaunchKernelGGL((m1_tile_kernel<I, REV>), dim3((unsigned)blocks),
+                     dim3(64 * kWavesPerBlock), lds, st, k);
   return hipGetLastError();
 }
 
@@ -528,7 +609,7 @@ hipError_t m1_scan_chunked(const M1Problem& pr, hipStream_t st) {
   const bool rev = pr.reverse != 0;
   // the tiled path needs every 16-row block inside one batch/group and 16-byte rows
   const bool tiled = vec && pr.dim % 16 == 0 && (pr.dim / pr.groups) % 16 == 0;
-  if (tiled) return rev ? launch_tile<true>(k, st) : launch_tile<false>(k, st);
+  if (tiled) return rev ? launch_tile<M1_TILE_I, true>(k, st) : launch_tile<M1_TILE_I, false>(k, st);
   return launch_dir<16, 16>(k, rev, vec, st);
 }
 

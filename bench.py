@@ -43,6 +43,9 @@ def parse():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain device-to-device copy of 1 GiB (the reference "
+                         "kernel for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE counters)")
     return ap.parse_args()
 
 
@@ -184,9 +187,17 @@ def main():
 
     from armhackathon_amd import _ffi
 
-    _ffi.load()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.copy_calibration:
+        src = torch.ones(1 << 28, device=dev)  # 1 GiB of fp32
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": src.numel() * 4}), flush=True)
+        return
+    _ffi.load()
     r = bench_scan(args, dev)
     prefill = None if args.no_prefill else bench_prefill(args, dev)
     cpu = None if args.no_cpu else bench_cpu(args.cpu_seconds)
