@@ -24,6 +24,7 @@ __all__ = [
     "selective_scan_bidirectional",
     "bidirectional_scan",
     "ss2d_scan",
+    "use_arm_scan",
     "mamba3_scan",
     "mamba3_scan_pair",
     "mamba3_mimo_scan",
@@ -42,15 +43,16 @@ _LAZY = {
     "kernel_calls": ".op",
     "bidirectional_scan": ".bidirectional",
     "ss2d_scan": ".ss2d",
+    "use_arm_scan": ".ss2d",
     "mamba3_scan": ".mamba3",
     "mamba3_scan_pair": ".mamba3",
     "mamba3_mimo_scan": ".mamba3",
     "angles_to_cos_sin": ".mamba3",
     "ss2d_scan_mamba3": ".ss2d_mamba3",
     "selective_scan_numpy": ".numpy_api",
-    "patch": ".patch",
-    "unpatch": ".patch",
-    "stats": ".patch",
+    "patch": ".hf_patch",
+    "unpatch": ".hf_patch",
+    "stats": ".hf_patch",
 }
 
 

@@ -1,0 +1,39 @@
+"""The Hugging Face patch on the host: seam detection, idempotence, and the
+fallback for tensors the kernel does not serve (python/arm_scan/patch.py:152-168):
+host tensors go to upstream's function unchanged and are counted."""
+
+import pytest
+
+
+def test_patch_falls_back_on_host_tensors():
+    torch = pytest.importorskip("torch")
+    transformers = pytest.importorskip("transformers")
+    from transformers import MambaConfig, MambaForCausalLM
+    from transformers.models.mamba import modeling_mamba
+
+    import armhackathon_amd as arm_scan
+
+    orig = modeling_mamba.mamba_selective_scan
+    cfg = MambaConfig(vocab_size=64, hidden_size=16, state_size=4, num_hidden_layers=2,
+                      expand=2, conv_kernel=4, time_step_rank=2)
+    torch.manual_seed(0)
+    model = MambaForCausalLM(cfg).eval()
+    ids = torch.randint(0, 64, (1, 10))
+    with torch.no_grad():
+        ref = model(ids, use_cache=False).logits
+        targets = arm_scan.patch()
+        try:
+            assert targets and "mamba_selective_scan" in targets[0]
+            assert arm_scan.patch() == ["transformers mamba_selective_scan (already patched)"]
+            assert modeling_mamba.mamba_selective_scan is not orig
+            before = arm_scan.stats()
+            got = model(ids, use_cache=False).logits
+            after = arm_scan.stats()
+        finally:
+            assert arm_scan.unpatch()
+    assert modeling_mamba.mamba_selective_scan is orig
+    assert not arm_scan.unpatch()
+    assert after["fallback_calls"] - before["fallback_calls"] == 2
+    assert after["fast_calls"] == before["fast_calls"]
+    assert torch.equal(ref, got)
+    assert transformers is not None

@@ -1,0 +1,71 @@
+"""The Hugging Face Mamba-1 patch on the GPU (check_hf_patch.py's gates, on a
+random-init local MambaConfig: real checkpoints need the network).
+
+* logits patched vs unpatched (upstream's torch recurrence) within
+  1e-4 * max(1, scale) (check_hf_patch.py:34,67-69);
+* engagement: one fast call per layer per forward, no fallbacks;
+* cached prefill seeds the recurrent state, and greedy decoding continues
+  token-identically (check_hf_patch.py:76-101).
+"""
+
+import pytest
+
+from util import case
+
+pytestmark = pytest.mark.gpu
+
+
+def _model(layers=3, hidden=64, vocab=512, seed=0):
+    import torch
+    from transformers import MambaConfig, MambaForCausalLM
+
+    cfg = MambaConfig(vocab_size=vocab, hidden_size=hidden, state_size=16,
+                      num_hidden_layers=layers, expand=2, conv_kernel=4, time_step_rank=8)
+    torch.manual_seed(seed)
+    return MambaForCausalLM(cfg).cuda().float().eval()
+
+
+def test_patch_logits_and_engagement():
+    import torch
+
+    import armhackathon_amd as arm_scan
+
+    case("hf patch logits")
+    model = _model()
+    ids = torch.randint(0, 512, (2, 300), device="cuda",
+                        generator=torch.Generator(device="cuda").manual_seed(1))
+    with torch.no_grad():
+        ref = model(ids, use_cache=False).logits
+        arm_scan.patch()
+        try:
+            s0 = arm_scan.stats()
+            got = model(ids, use_cache=False).logits
+            s1 = arm_scan.stats()
+        finally:
+            arm_scan.unpatch()
+    assert s1["fast_calls"] - s0["fast_calls"] == 3
+    assert s1["fallback_calls"] == s0["fallback_calls"]
+    scale = max(1.0, ref.abs().max().item())
+    assert (got - ref).abs().max().item() < 1e-4 * scale
+    assert not arm_scan.stats()["patched"]
+
+
+def test_patch_cached_generation():
+    import torch
+
+    import armhackathon_amd as arm_scan
+
+    case("hf patch generate")
+    model = _model(seed=2)
+    ids = torch.randint(0, 512, (1, 64), device="cuda",
+                        generator=torch.Generator(device="cuda").manual_seed(3))
+    with torch.no_grad():
+        ref = model.generate(ids, max_new_tokens=12, do_sample=False)
+        arm_scan.patch()
+        try:
+            got = model.generate(ids, max_new_tokens=12, do_sample=False)
+            st = arm_scan.stats()
+        finally:
+            arm_scan.unpatch()
+    assert st["fast_calls"] >= 3  # the prefill went through the kernel
+    assert torch.equal(ref, got)
