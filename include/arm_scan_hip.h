@@ -4,7 +4,7 @@
  *
  * The entry points keep the reference's names, argument order and return codes
  * (kernel/arm-scan-ffi/src/lib.rs). What changes, as the reference's own versioning
- * rule demands (arm-scan-ffi/src/lib.rs:24-36: "bump on any signature or semantic
+ * rule demands (arm-scan-ffi/src/lib.rs:25-37: "bump on any signature or semantic
  * change"), is ABI 7 -> 8:
  *
  *   - every tensor pointer is a DEVICE pointer (HBM of the current HIP device);
