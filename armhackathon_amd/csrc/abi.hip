@@ -163,10 +163,6 @@ int arm_scan_mamba3_scan_f32(const ArmMamba3Dims* dims, const float* q, const fl
     return fail(ARM_SCAN_ERR_INVALID_DIMS, "MIMO has no last_bx carry (rank > 1 k per step)");
   if (d.len > (1u << 30) || d.batch * d.heads > (1u << 30))
     return fail(ARM_SCAN_ERR_INVALID_DIMS, "problem too large for this build");
-  const size_t need = d.dv * (d.dqk + 1) + 2 * d.rank * (d.dqk + d.dv) + d.rank * d.rank + 4;
-  if (need > armscan::m3_max_state())
-    return fail(ARM_SCAN_ERR_INVALID_DIMS, "state dv*dqk (%zu x %zu) exceeds on-chip capacity",
-                d.dv, d.dqk);
   armscan::M3Problem p{};
   p.batch = d.batch; p.heads = d.heads; p.dv = d.dv; p.dqk = d.dqk; p.len = d.len;
   p.rank = d.rank; p.groups = d.groups;
@@ -174,6 +170,12 @@ int arm_scan_mamba3_scan_f32(const ArmMamba3Dims* dims, const float* q, const fl
   p.k_bias = k_bias; p.cos = cos; p.sin = sin; p.D = d_skip; p.z = z;
   p.psi = mimo_psi; p.zeta = mimo_zeta; p.phi = mimo_phi;
   p.out = out; p.last_state = last_state; p.last_bx = last_bx; p.reverse = reverse != 0;
+  // the chunked MFMA kernel takes dv, dqk multiples of 16 (dqk <= 256) and rank 1/2/4;
+  // everything else runs the step-by-step kernel, whose state must fit in LDS
+  const size_t need = d.dv * (d.dqk + 1) + 2 * d.rank * (d.dqk + d.dv) + d.rank * d.rank + 4;
+  if (!armscan::m3_chunk_supported(p) && need > armscan::m3_max_state())
+    return fail(ARM_SCAN_ERR_INVALID_DIMS, "state dv*dqk (%zu x %zu) exceeds on-chip capacity",
+                d.dv, d.dqk);
   return run(armscan::m3_scan(p, (hipStream_t)stream), "mamba3 launch");
 }
 

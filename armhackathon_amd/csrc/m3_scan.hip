@@ -21,6 +21,8 @@
 #include <hip/hip_runtime.h>
 
 #include "scan_common.h"
+#include <cstdint>
+
 #include "scan_launch.h"
 
 namespace armscan {
@@ -168,7 +170,17 @@ size_t lds_floats(size_t dv, size_t dqk, size_t r) {
 
 size_t m3_max_state() { return kM3MaxLdsFloats; }
 
+static bool aligned16(const void* q) { return q == nullptr || ((uintptr_t)q & 15u) == 0; }
+
 hipError_t m3_scan(const M3Problem& pr, hipStream_t st) {
+  const bool aligned = aligned16(pr.q) && aligned16(pr.k) && aligned16(pr.q_bias) &&
+                       aligned16(pr.k_bias) && aligned16(pr.cos) && aligned16(pr.sin) &&
+                       aligned16(pr.last_state) && aligned16(pr.last_bx);
+  if (aligned && m3_chunk_supported(pr)) return m3_scan_chunked(pr, st);
+  return m3_scan_sequential(pr, st);
+}
+
+hipError_t m3_scan_sequential(const M3Problem& pr, hipStream_t st) {
   const size_t fl = lds_floats(pr.dv, pr.dqk, pr.rank);
   if (fl > kM3MaxLdsFloats) return hipErrorInvalidValue;
   M3Args a{};

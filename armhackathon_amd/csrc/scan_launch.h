@@ -42,5 +42,10 @@ struct M3Problem {
 // Largest dv * dqk the Mamba-3 kernel holds on chip.
 size_t m3_max_state();
 hipError_t m3_scan(const M3Problem& p, hipStream_t st);
+// One workgroup per (batch, head), step by step (any shape).
+hipError_t m3_scan_sequential(const M3Problem& p, hipStream_t st);
+// The chunked MFMA path (m3_chunk.hip): dv, dqk multiples of 16, rank 1/2/4.
+bool m3_chunk_supported(const M3Problem& p);
+hipError_t m3_scan_chunked(const M3Problem& p, hipStream_t st);
 
 }  // namespace armscan

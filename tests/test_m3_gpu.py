@@ -166,3 +166,33 @@ def test_m3_pair_and_reverse_is_flip():
     f2 = _siso_gpu(fl)
     assert rel_err(host(bwd), host(f2)[:, ::-1]) < 1e-5
     assert rel_err(host(fwd), _siso_ref(x).transpose(0, 2, 1, 3)) < TOL
+
+
+def test_m3_siso_benchmark_shape():
+    """BASELINE config 3 (per-head q/k, L 4096, 24 heads x 64, dqk 128), batch
+    reduced to 2 to bound the oracle's CPU time; outputs, final states, last_bx."""
+    case("siso config 3 (batch 2)")
+    x = workloads.m3_siso(batch=2, seed=3)
+    out, ls, lbx = _siso_gpu(x, return_last_state=True)
+    ref, rls, rlbx = _siso_ref(x, want_state=True)
+    assert rel_err(host(out), ref.transpose(0, 2, 1, 3)) < TOL
+    assert rel_err(host(ls), rls) < TOL
+    assert rel_err(host(lbx), rlbx) < TOL
+
+
+def test_m3_mimo_benchmark_shape():
+    """BASELINE config 4 (rank 4, per-head q/k), batch 1, L 2048 to bound the
+    oracle's CPU time; output and final state."""
+    import armhackathon_amd as arm_scan
+
+    case("mimo config 4 (batch 1, L 2048)")
+    x = workloads.m3_mimo(batch=1, length=2048, seed=4)
+    t = dev(x)
+    out, ls = arm_scan.mamba3_mimo_scan(
+        *[t[k] for k in SISO_KEYS], t["psi"], t["zeta"], t["phi"], cos=t["cos"], sin=t["sin"],
+        return_last_state=True)
+    ref, rls, _ = oracle.mamba3_scan(*[x[k] for k in SISO_KEYS], x["cos"], x["sin"],
+                                     psi=x["psi"], zeta=x["zeta"], phi=x["phi"],
+                                     dtype=np.float64, want_state=True)
+    assert rel_err(host(out), ref.transpose(0, 2, 1, 3)) < TOL
+    assert rel_err(host(ls), rls) < TOL
