@@ -12,17 +12,31 @@
 // 16/R steps. The output of a step is the rank sum phi_r silu(z zeta_r) Y_r (MIMO)
 // or Y silu(z) (SISO).
 //
-// Work decomposition: one block per (sequence, 16-row slice of dv) and one wave
-// per 16-wide slice of dqk. Each wave keeps its 16x16 piece of S in MFMA
-// registers and per chunk computes
-//   its partial G^T = K Q^T over its dqk slice (4 MFMA),
-//   its partial diag(e^c) Q S0^T (4 MFMA),
-//   the update of its S piece (4 MFMA, through a K transpose in LDS);
-// the partials meet in LDS and wave 0 adds the masked intra-chunk term (4 MFMA)
-// and the epilogue. Every MFMA operand is used in the register layout the
-// previous MFMA produced: the reduction index of each product is permuted so that
-// lane l (row l%16, group j = l/16) always supplies element (l%16, 4j + r).
-// The per-step gates come from a small pre-pass (m3_gates_kernel).
+// Two kernels:
+//  * m3_gates_kernel, one lane per (sequence, chunk, row): the chunk's gate record
+//    {M, e^c, w, e^{c_last}} (1168 bytes per chunk), so that the main kernel does
+//    no transcendental work for the decays.
+//  * m3_chunk_kernel: one block per (sequence, PT 16-column slices of dv), one
+//    wave per 16-column slice of dqk (an "n-tile"). A wave keeps the PT 16x16
+//    pieces S[slice][n-tile] in MFMA registers and per chunk computes
+//      its partial G^T = K Q^T over its n-tile (4 MFMA),
+//      per slice its partial Q S0^T (4 MFMA),
+//      per slice the update of its S piece (4 MFMA, K transposed through LDS).
+//    The partials meet in LDS; wave j < PT finishes slice j of a chunk while the
+//    partials of the next chunk are computed: masked intra-chunk term (4 MFMA),
+//    D x, gating, rank sum, store.
+//
+// Every input of a chunk (q, k, cos, sin, v and z rows and the gate record)
+// reaches LDS by direct-to-LDS DMA (global_load_lds_dwordx4) two chunks ahead,
+// through a ring of three stages: no VGPRs are spent on staging and HBM latency
+// stays off the chunk loop. Each wave waits with an explicit vmcnt for its own
+// share of a stage, and a workgroup barrier publishes the stage. Rows of the last
+// chunk past the end of the sequence are clamped to the last step on load (their
+// gates are zero, so they add nothing) and are not stored.
+//
+// Every MFMA operand is used in the register layout the previous MFMA produced:
+// the reduction index of each product is permuted so that lane l (row l%16,
+// group j = l/16) always supplies element (l%16, 4j + r).
 
 #include <hip/hip_runtime.h>
 
@@ -36,251 +50,481 @@ namespace armscan {
 namespace {
 
 typedef float f4 __attribute__((ext_vector_type(4)));
+typedef float f2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ f4 mfma(float a, float b, f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
-struct M3Gates {
-  // per (sequence, traversal step): {c, e^c, gamma, scale}; per step w; per chunk e^c_last
-  f4* step;
-  float* w;
-  float* etot;
-};
+// Gate record of one (sequence, chunk), in floats.
+constexpr int kRecM = 0;         // M[i][s], 16 x 16
+constexpr int kRecEc = 256;      // e^{c_i}
+constexpr int kRecW = 272;       // w_s
+constexpr int kRecEtot = 288;    // e^{c_last}
+constexpr int kRecFloats = 292;  // + 3 floats of padding: whole 16-byte pieces
+constexpr int kRecPieces = kRecFloats / 4;
+
+constexpr int kMaxWaves = 8;   // n-tiles per block: dqk <= 128
+constexpr int kKtStride = 20;  // floats per row of a wave's K transpose tile
+constexpr int kStages = 3;
+constexpr size_t kLdsBudget = 160 * 1024;
 
 struct M3K {
-  const float *q, *k, *v, *adt, *dt, *trap, *qb, *kb, *cos, *sin, *D, *z, *psi, *zeta, *phi;
-  float *out, *last_state, *last_bx;
-  M3Gates g;
-  int batch, heads, dv, dqk, len, rank, groups, nparts, nchunks, steps_per_chunk, nseq;
+  const float *q, *k, *v, *qb, *kb, *cos, *sin, *D, *z, *psi, *zeta, *phi;
+  const float *adt, *dt, *trap;
+  float *out, *last_state, *last_bx, *rec;
+  int heads, dv, dqk, len, groups, nparts, nchunks, steps_per_chunk, nseq;
+  int ptiles, nstages;
+  // DMA instructions (1 KB each) per stage: q and k take one per n-tile
+  int n_cs, n_v, n_z;  // cos (and again sin), v, z
+  int n_ins;           // all sections, + 2 for the gate record
+  int stage_floats;
 };
 
 // ---------------------------------------------------------------------------
-// Gate pre-pass: one thread per (sequence, chunk). Traversal step g maps to memory
-// t = g (forward) or L-1-g (reverse); the trapezoid's "next" step is traversal
-// step g+1 (mamba3/scalar.rs:95-115), absent at the end of the traversal.
+// Gate pre-pass: 16 lanes per (sequence, chunk), lane = row i. Traversal step g
+// maps to memory t = g (forward) or L-1-g (reverse); the trapezoid's "next" step
+// is traversal step g+1 (mamba3/scalar.rs:95-115), absent at the end.
+template <int R>
 __global__ void __launch_bounds__(256) m3_gates_kernel(M3K p, int reverse) {
-  const long long tid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-  const long long total = (long long)p.nseq * p.nchunks;
-  if (tid >= total) return;
-  const int seq = (int)(tid / p.nchunks);
-  const int ch = (int)(tid - (long long)seq * p.nchunks);
+  const int row = threadIdx.x & 15;
+  const long long cidx = (long long)blockIdx.x * 16 + (threadIdx.x >> 4);
+  const bool valid = cidx < (long long)p.nseq * p.nchunks;
   const int L = p.len, T = p.steps_per_chunk;
-  const long long base = (long long)seq * L;  // gates are (b, h, l): seq = b*heads + h
-  float c = 0.0f;
-  float cs[16], sc[16];
-  for (int i = 0; i < T; ++i) {
-    const long long g = (long long)ch * T + i;
-    float adt = 0.0f, gamma = 0.0f, scale = 0.0f;
-    if (g < L) {
-      const long long t = reverse ? L - 1 - g : g;
-      adt = p.adt[base + t];
-      const float lam = sigmoid(p.trap[base + t]);
-      gamma = p.dt[base + t] * lam;
-      scale = gamma;
-      if (g + 1 < L) {
-        const long long tn = reverse ? t - 1 : t + 1;
-        scale = gamma + p.dt[base + tn] * (1.0f - sigmoid(p.trap[base + tn]));
-      }
+  int seq = 0, ch = 0;
+  if (valid) {
+    seq = (int)(cidx / p.nchunks);
+    ch = (int)(cidx - (long long)seq * p.nchunks);
+  }
+  const int step = row / R;
+  const long long g = (long long)ch * T + step;
+  float a = 0.0f, gamma = 0.0f, scale = 0.0f;
+  if (valid && g < L) {
+    const long long base = (long long)seq * L;  // gates are (b, h, l): seq = b*heads + h
+    const long long t = reverse ? L - 1 - g : g;
+    a = p.adt[base + t];
+    gamma = p.dt[base + t] * sigmoid(p.trap[base + t]);
+    scale = gamma;
+    if (g + 1 < L) {
+      const long long tn = reverse ? t - 1 : t + 1;
+      scale = gamma + p.dt[base + tn] * (1.0f - sigmoid(p.trap[base + tn]));
     }
-    c += adt;
-    cs[i] = c;
-    sc[i] = scale;
-    const long long o = (long long)seq * ((long long)p.nchunks * T) + (long long)ch * T + i;
-    p.g.step[o] = f4{c, fexp(c), gamma, scale};
   }
-  for (int i = 0; i < T; ++i) {
-    const long long o = (long long)seq * ((long long)p.nchunks * T) + (long long)ch * T + i;
-    p.g.w[o] = fexp(c - cs[i]) * sc[i];
+  // c_i: inclusive sum over the rows up to i of one adt per step (its rank-0 row)
+  float c = row % R == 0 ? a : 0.0f;
+#pragma unroll
+  for (int d = 1; d < 16; d <<= 1) {
+    const float o = __shfl_up(c, d, 16);
+    if (row >= d) c += o;
   }
-  p.g.etot[tid] = fexp(c);
+  const float clast = __shfl(c, 15, 16);
+  float m[16];
+#pragma unroll
+  for (int s = 0; s < 16; ++s) {
+    const float cs = __shfl(c, s, 16);
+    const float ss = __shfl(scale, s, 16);
+    const int step_s = s / R;
+    m[s] = step_s < step ? fexp(c - cs) * ss : (step_s == step ? gamma : 0.0f);
+  }
+  if (!valid) return;
+  float* rec = p.rec + cidx * kRecFloats;
+  f4* mrow = reinterpret_cast<f4*>(rec + kRecM + row * 16);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) mrow[q] = f4{m[4 * q], m[4 * q + 1], m[4 * q + 2], m[4 * q + 3]};
+  rec[kRecEc + row] = fexp(c);
+  rec[kRecW + row] = fexp(clast - c) * scale;
+  if (row < 4) rec[kRecEtot + row] = row == 0 ? fexp(clast) : 0.0f;
 }
 
 // ---------------------------------------------------------------------------
-// Rotated q/k for lane (row i, group j): the 4 columns n0 .. n0+3 of row i.
-// SISO rotates interleaved pairs (2u, 2u+1) with angle u (mamba3/scalar.rs:40-48);
-// MIMO rotates split halves (u, u + dqk/2) with angle u (mimo.rs:83-96).
-template <bool MIMO>
-__device__ __forceinline__ f4 rotated(const float* __restrict__ src, const float* __restrict__ bias,
-                                      const float* __restrict__ cs, const float* __restrict__ sn,
-                                      int n0, int dqk) {
-  if (!MIMO) {
-    const f4 x = *reinterpret_cast<const f4*>(src + n0) + *reinterpret_cast<const f4*>(bias + n0);
-    const float2 c = *reinterpret_cast<const float2*>(cs + n0 / 2);
-    const float2 s = *reinterpret_cast<const float2*>(sn + n0 / 2);
-    return f4{x[0] * c.x - x[1] * s.x, x[0] * s.x + x[1] * c.x,
-              x[2] * c.y - x[3] * s.y, x[2] * s.y + x[3] * c.y};
+// Waits until at most N vector-memory operations of this wave are outstanding and
+// every LDS operation of this wave is done. Vector memory operations complete in
+// issue order on gfx9, so "at most N outstanding" means "all but the last N done".
+template <int N>
+__device__ __forceinline__ void waitcnt_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));  // lgkmcnt(0)
+}
+
+// The same for a run-time n, rounded down to a step of the ladder (waiting for
+// more operations than needed is always safe).
+__device__ __forceinline__ void wait_vm_at_most(int n) {
+  if (n >= 16) waitcnt_vm<16>();
+  else if (n >= 12) waitcnt_vm<12>();
+  else if (n >= 8) waitcnt_vm<8>();
+  else if (n >= 6) waitcnt_vm<6>();
+  else if (n >= 4) waitcnt_vm<4>();
+  else if (n >= 3) waitcnt_vm<3>();
+  else if (n >= 2) waitcnt_vm<2>();
+  else if (n >= 1) waitcnt_vm<1>();
+  else waitcnt_vm<0>();
+}
+
+// Workgroup barrier that orders LDS only: outstanding global loads and stores
+// stay in flight.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+__device__ __forceinline__ f4 ld4(const float* p) { return *reinterpret_cast<const f4*>(p); }
+__device__ __forceinline__ f2 ld2(const float* p) { return *reinterpret_cast<const f2*>(p); }
+
+// Base pointers of a block's sequence.
+struct SeqIn {
+  const float *q, *k, *cos, *sin, *v, *z, *rec;
+  int qstride, csstride, vstride;  // floats per step
+};
+
+// Issues DMA instruction `ins` of chunk ch into a stage (1 KB per instruction).
+// Stage layout in 16-byte pieces, each section padded to whole instructions:
+//   q, k: piece (nt, lj, li) = columns nt*16 + 4lj .. +3 of row li
+//   cos, sin: piece u4*T + step = angles 4u4 .. 4u4+3 of the step
+//   v, z: piece step*4PT + c4 = columns p0 + 4c4 .. +3 of the step
+//   gate record: its 73 pieces in order
+template <int R, bool REV>
+__device__ __forceinline__ void dma_ins(const M3K& p, const SeqIn& s, int ins, int ch,
+                                        float* stage, int lane) {
+  const int WN = p.dqk / 16, T = p.steps_per_chunk, L = p.len;
+  const float* src;
+  int step = 0;    // step of the chunk the lane's piece belongs to
+  int col;         // float offset of the piece within its step's row
+  int stride = 0;  // floats per step
+  bool on = true;
+  int rel = ins;
+  if (rel < 2 * WN) {
+    const int nt = rel < WN ? rel : rel - WN;
+    const int li = lane & 15, lj = lane >> 4;
+    src = rel < WN ? s.q : s.k;
+    step = li / R;
+    col = (li % R) * p.groups * p.dqk + nt * 16 + 4 * lj;
+    stride = s.qstride;
+  } else if ((rel -= 2 * WN) < 2 * p.n_cs) {
+    const bool sn = rel >= p.n_cs;
+    const int j = (sn ? rel - p.n_cs : rel) * 64 + lane;
+    on = j < T * (p.dqk / 8);
+    src = sn ? s.sin : s.cos;
+    step = j % T;
+    col = 4 * (j / T);
+    stride = s.csstride;
+  } else if ((rel -= 2 * p.n_cs) < p.n_v + p.n_z) {
+    const bool zz = rel >= p.n_v;
+    const int j = (zz ? rel - p.n_v : rel) * 64 + lane;
+    const int w4 = 4 * p.ptiles;
+    on = j < T * w4;
+    src = zz ? s.z : s.v;
+    step = j / w4;
+    col = 4 * (j % w4);
+    stride = s.vstride;
+  } else {
+    const int j = (rel - p.n_v - p.n_z) * 64 + lane;
+    on = j < kRecPieces;
+    src = s.rec + (long long)ch * kRecFloats;
+    col = 4 * j;
   }
-  const int half = dqk / 2;
-  const bool lo = n0 < half;
-  const int u0 = lo ? n0 : n0 - half;  // angle index of column n0
-  const int m0 = lo ? n0 + half : n0 - half;  // partner columns
-  const f4 x = *reinterpret_cast<const f4*>(src + n0) + *reinterpret_cast<const f4*>(bias + n0);
-  const f4 y = *reinterpret_cast<const f4*>(src + m0) + *reinterpret_cast<const f4*>(bias + m0);
-  const f4 c = *reinterpret_cast<const f4*>(cs + u0);
-  const f4 s = *reinterpret_cast<const f4*>(sn + u0);
-  // low half: a*c - b*s with (a, b) = (x, y); high half: a*s + b*c with (a, b) = (y, x)
+  if (on) {
+    int g = ch * T + step;
+    g = g < L - 1 ? g : L - 1;
+    const int t = REV ? L - 1 - g : g;
+    const float* a = src + (unsigned)(t * stride + col);
+    __builtin_amdgcn_global_load_lds((const void*)a,
+                                     (__attribute__((address_space(3))) void*)(stage + ins * 256),
+                                     16, 0, 0);
+  }
+}
+
+// This wave's share of a stage: instructions wave, wave + nwaves, ...
+template <int R, bool REV>
+__device__ __forceinline__ void dma_stage(const M3K& p, const SeqIn& s, int ch, float* stage,
+                                          int wave, int nwaves, int lane) {
+  for (int ins = wave; ins < p.n_ins; ins += nwaves) dma_ins<R, REV>(p, s, ins, ch, stage, lane);
+}
+
+// Rotated q/k from the raw columns: SISO rotates interleaved pairs (2u, 2u+1)
+// with angle u (mamba3/scalar.rs:40-48); MIMO rotates split halves (u, u + dqk/2)
+// with angle u (mimo.rs:83-96), the lane holding its 4 columns x and their
+// partners y.
+template <bool MIMO>
+__device__ __forceinline__ f4 rope(f4 x, f4 y, f4 bx, f4 by, f4 c, f4 s, bool lo) {
+  x += bx;
+  if (!MIMO)
+    return f4{x[0] * c[0] - x[1] * s[0], x[0] * s[0] + x[1] * c[0],
+              x[2] * c[1] - x[3] * s[1], x[2] * s[1] + x[3] * c[1]};
+  y += by;
   return lo ? f4{x[0] * c[0] - y[0] * s[0], x[1] * c[1] - y[1] * s[1],
                  x[2] * c[2] - y[2] * s[2], x[3] * c[3] - y[3] * s[3]}
             : f4{y[0] * s[0] + x[0] * c[0], y[1] * s[1] + x[1] * c[1],
                  y[2] * s[2] + x[2] * c[2], y[3] * s[3] + x[3] * c[3]};
 }
 
-constexpr int kKtStride = 20;  // floats per row of the per-wave K transpose tile
+// What a chunk's epilogue needs from its stage, kept in registers so that the
+// stage can be refilled before the epilogue runs.
+struct Stash {
+  f4 m;   // M[li][4lj + r]
+  f4 ec;  // e^{c} of rows 4lj + r
+  f4 x;   // x of rows 4lj + r, in the wave's slice
+  float z[4];
+};
 
-template <int R, bool MIMO, bool REV>
-__global__ void __launch_bounds__(1024) m3_chunk_kernel(M3K p) {
+template <int R, bool MIMO, bool REV, int PT>
+__global__ void __launch_bounds__(64 * kMaxWaves) m3_chunk_kernel(M3K p) {
   extern __shared__ __attribute__((aligned(16))) float sm[];
-  const int W = p.dqk / 16;  // waves per block
+  const int WN = p.dqk / 16;
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int nt = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave = n-tile
   const int li = lane & 15, lj = lane >> 4;
   // blocks of one sequence share an XCD (block id mod 8), and so its L2
   const int bx = blockIdx.x & 7, by = blockIdx.x >> 3;
-  const int seq = (by / p.nparts) * 8 + bx;
-  const int part = by - (by / p.nparts) * p.nparts;
+  const int nb = p.nparts / PT;  // blocks per sequence
+  const int seq = (by / nb) * 8 + bx;
+  const int p0 = (by % nb) * PT * 16;  // first dv column of the block
   if (seq >= p.nseq) return;  // whole block exits: no barrier is reached by anyone
-  const int bi = seq / p.heads, h = seq - bi * p.heads;
-  const int grp = h / (p.heads / p.groups);
-  const int L = p.len, dqk = p.dqk, dv = p.dv, H = p.heads;
-  const int T = p.steps_per_chunk;  // 16 / R
-  const int n0 = wave * 16 + 4 * lj;  // this lane's 4 columns of the wave's dqk slice
-  const int pcol = part * 16 + li;    // this lane's state row (output column)
+  const int H = p.heads;
+  const int bi = seq / H, h = seq - bi * H;
+  const int grp = h / (H / p.groups);
+  const int L = p.len, dqk = p.dqk, dv = p.dv, T = p.steps_per_chunk, NS = p.nstages;
+  const int half = dqk / 2;
+  const int n0 = nt * 16 + 4 * lj;  // this lane's 4 columns of dqk
+  const bool lo = !MIMO || n0 < half;
+  const int step_i = li / R;
   const float dskip = p.D ? p.D[h] : 0.0f;
+  const bool ewave = nt < PT;  // finishes slice nt
+  const int ej = ewave ? nt : 0;
 
-  float* part_buf = sm;                                   // [2][W][64][8]
-  float* kt = sm + 2 * W * 64 * 8 + wave * 16 * kKtStride;  // [16][kKtStride] per wave
+  float* stages = sm;
+  // partials of every n-tile slot; the slots of absent waves (WN < kMaxWaves) stay 0
+  float* gbuf = stages + NS * p.stage_floats;  // [2][kMaxWaves][64][4]
+  float* ybuf = gbuf + 2 * kMaxWaves * 256;     // [2][PT][kMaxWaves][64][4]
+  float* kt = ybuf + 2 * PT * kMaxWaves * 256 + nt * 16 * kKtStride;
+  const int off_k = WN * 256, off_cs = 2 * WN * 256;
+  const int off_sn = off_cs + p.n_cs * 256, off_v = off_cs + 2 * p.n_cs * 256;
+  const int off_z = off_v + p.n_v * 256, off_rec = off_z + p.n_z * 256;
 
-  // per-lane rank projections of the B-operand rows s = 4*lj + m (MIMO)
-  float psi_m[4], zeta_r[4], phi_r[4];
+  SeqIn in;
+  in.q = p.q + ((long long)bi * L * R * p.groups + grp) * dqk;
+  in.k = p.k + ((long long)bi * L * R * p.groups + grp) * dqk;
+  in.cos = p.cos + ((long long)bi * L * H + h) * half;
+  in.sin = p.sin + ((long long)bi * L * H + h) * half;
+  in.v = p.v + ((long long)bi * L * H + h) * dv + p0;
+  in.z = p.z ? p.z + ((long long)bi * L * H + h) * dv + p0 : nullptr;
+  in.rec = p.rec + (long long)seq * p.nchunks * kRecFloats;
+  in.qstride = R * p.groups * dqk;
+  in.csstride = H * half;
+  in.vstride = H * dv;
+
+  // biases of the lane's columns (row li has rank li % R) and the MIMO projections
+  f4 bq, bk, bqp = {0.0f, 0.0f, 0.0f, 0.0f}, bkp = bqp;
+  const int m0 = n0 < half ? n0 + half : n0 - half;  // MIMO partner columns
+  {
+    const long long bo = ((long long)h * R + (li % R)) * dqk;
+    bq = ld4(p.qb + bo + n0);
+    bk = ld4(p.kb + bo + n0);
+    if (MIMO) {
+      bqp = ld4(p.qb + bo + m0);
+      bkp = ld4(p.kb + bo + m0);
+    }
+  }
+  float psi[PT][4], zeta[4], phi[4];
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
     const int rk = (4 * lj + m) % R;
-    psi_m[m] = MIMO ? p.psi[((long long)h * R + rk) * dv + pcol] : 1.0f;
-    zeta_r[m] = (MIMO && p.z) ? p.zeta[((long long)h * R + rk) * dv + pcol] : 1.0f;
-    phi_r[m] = MIMO ? p.phi[((long long)h * R + rk) * dv + pcol] : 1.0f;
+#pragma unroll
+    for (int j = 0; j < PT; ++j)
+      psi[j][m] = MIMO ? p.psi[((long long)h * R + rk) * dv + p0 + j * 16 + li] : 1.0f;
+    const long long pj = ((long long)h * R + rk) * dv + p0 + ej * 16 + li;
+    zeta[m] = (MIMO && p.z) ? p.zeta[pj] : 1.0f;
+    phi[m] = MIMO ? p.phi[pj] : 1.0f;
   }
 
-  f4 S = {0.0f, 0.0f, 0.0f, 0.0f};  // S[pcol][n0 .. n0+3]
-  const long long gate_base = (long long)seq * p.nchunks * T;
-  for (int ch = 0; ch < p.nchunks; ++ch) {
-    // ---- this lane's row i = li: step, rank, gates, rotated q/k
-    const int step_i = li / R, rank_i = li % R;
-    const long long g_i = (long long)ch * T + step_i;
-    const bool valid_i = g_i < L;
-    const long long t_i = REV ? L - 1 - g_i : g_i;
-    const f4 gi = p.g.step[gate_base + (long long)ch * T + step_i];  // {c, e, gamma, scale}
-    f4 qr = {0.0f, 0.0f, 0.0f, 0.0f}, kr = qr;
-    if (valid_i) {
-      const long long row = (((long long)bi * L + t_i) * R + rank_i) * p.groups + grp;
-      const long long cso = (((long long)bi * L + t_i) * H + h) * (dqk / 2);
-      const long long bo = ((long long)h * R + rank_i) * dqk;
-      qr = rotated<MIMO>(p.q + row * dqk, p.qb + bo, p.cos + cso, p.sin + cso, n0, dqk);
-      kr = rotated<MIMO>(p.k + row * dqk, p.kb + bo, p.cos + cso, p.sin + cso, n0, dqk);
+  // This wave's DMA instructions per stage, and the stores its epilogue issues per
+  // chunk (a lower bound: more operations in flight only makes a wait stricter).
+  const int nwaves = WN;
+  const int dma_per_stage = (p.n_ins - nt + nwaves - 1) / nwaves;
+  const int stores_per_chunk = ewave ? 4 / R : 0;
+
+  for (int c = 0; c < NS - 1 && c < p.nchunks; ++c)
+    dma_stage<R, REV>(p, in, c, stages + c * p.stage_floats, nt, nwaves, lane);
+
+  if (WN < kMaxWaves) {
+    const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int e = nt * 64 + lane; e < 2 * (1 + PT) * kMaxWaves * 64; e += WN * 64) {
+      const int slot = (e >> 6) % kMaxWaves;
+      if (slot >= WN) *reinterpret_cast<f4*>(gbuf + e * 4) = zero;  // ybuf follows gbuf
     }
-    // ---- B-operand rows s = 4*lj + m: x (= psi v) and the update weight w
-    float xv[4], wv[4];
+  }
+
+  f4 S[PT];
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      const int s = 4 * lj + m;
-      const int step_s = s / R;
-      const long long g_s = (long long)ch * T + step_s;
-      float x = 0.0f, w = 0.0f;
-      if (g_s < L) {
-        const long long t_s = REV ? L - 1 - g_s : g_s;
-        x = p.v[(((long long)bi * L + t_s) * H + h) * dv + pcol] * psi_m[m];
-        w = p.g.w[gate_base + (long long)ch * T + step_s];
-      }
-      xv[m] = x;
-      wv[m] = w;
+  for (int j = 0; j < PT; ++j) S[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+  Stash st = {};
+
+  // epilogue of chunk ch for slice ej, from the partials in buffer ch & 1
+  auto epilogue = [&](int ch) {
+    const float* gb = gbuf + (ch & 1) * kMaxWaves * 256;
+    const float* yb = ybuf + ((ch & 1) * PT + ej) * kMaxWaves * 256;
+    f4 gs[kMaxWaves], ys[kMaxWaves];  // all reads in flight at once
+#pragma unroll
+    for (int w2 = 0; w2 < kMaxWaves; ++w2) {
+      gs[w2] = ld4(gb + (w2 * 64 + lane) * 4);
+      ys[w2] = ld4(yb + (w2 * 64 + lane) * 4);
     }
-    // ---- partial G^T = K Q^T and partial diag(e^c) Q S0^T over this wave's columns
-    f4 gp = {0.0f, 0.0f, 0.0f, 0.0f}, yp = gp;
-    const float ei = gi[1];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      gp = mfma(kr[r], qr[r], gp);
-      yp = mfma(ei * qr[r], S[r], yp);
-    }
-    float* pb = part_buf + ((ch & 1) * W + wave) * 64 * 8 + lane * 8;
-    *reinterpret_cast<f4*>(pb) = gp;
-    *reinterpret_cast<f4*>(pb + 4) = yp;
-    // ---- K transpose through LDS, then S = e^{c_last} S + K^T diag(w) X
-    *reinterpret_cast<f4*>(kt + li * kKtStride + 4 * lj) = kr;
-    const float etot = p.g.etot[(long long)seq * p.nchunks + ch];
-    f4 acc = S * etot;
+    for (int d = kMaxWaves / 2; d > 0; d /= 2)
 #pragma unroll
-    for (int m = 0; m < 4; ++m) acc = mfma(kt[(4 * lj + m) * kKtStride + li], wv[m] * xv[m], acc);
-    S = acc;
-    __syncthreads();
-    if (wave == 0) {
-      // ---- reduce the partials, mask G, add the intra-chunk term, epilogue
-      f4 G = {0.0f, 0.0f, 0.0f, 0.0f}, Y = G;
-      for (int w2 = 0; w2 < W; ++w2) {
-        const float* q2 = part_buf + ((ch & 1) * W + w2) * 64 * 8 + lane * 8;
-        G += *reinterpret_cast<const f4*>(q2);
-        Y += *reinterpret_cast<const f4*>(q2 + 4);
+      for (int w2 = 0; w2 < d; ++w2) {
+        gs[w2] += gs[w2 + d];
+        ys[w2] += ys[w2 + d];
       }
-      // lane holds G[i = li][s = 4*lj + r]
+    f4 G = gs[0], Y = ys[0];
+    G *= st.m;   // lane holds G[i = li][s = 4lj + r]
+    Y *= st.ec;  // lane holds Y[row = 4lj + r][p], the inter-chunk part
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int s = 4 * lj + r;
-        const int step_s = s / R;
-        const f4 gs = p.g.step[gate_base + (long long)ch * T + step_s];
-        float mval = 0.0f;
-        if (step_s < step_i) mval = fexp(gi[0] - gs[0]) * gs[3];
-        else if (step_s == step_i) mval = gi[2];
-        G[r] *= mval;
-      }
+    for (int m = 0; m < 4; ++m) Y = mfma(G[m], st.x[m], Y);
+    const int pcol = p0 + ej * 16 + li;
 #pragma unroll
-      for (int m = 0; m < 4; ++m) Y = mfma(G[m], xv[m], Y);
-      // lane holds Y[row = 4*lj + r][pcol]; add D x, gate, reduce ranks, store
-      float o[4];
+    for (int r = 0; r < 4; r += R) {
+      const int g = ch * T + (4 * lj + r) / R;
+      if (g < L) {
+        const int t = REV ? L - 1 - g : g;
+        float acc = 0.0f;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) o[r] = Y[r] + dskip * xv[r];
-#pragma unroll
-      for (int r = 0; r < 4; r += R) {
-        const int s = 4 * lj + r;
-        const long long g_s = (long long)ch * T + s / R;
-        if (g_s < L) {
-          const long long t_s = REV ? L - 1 - g_s : g_s;
-          const long long vo = (((long long)bi * L + t_s) * H + h) * dv + pcol;
-          const float zz = p.z ? p.z[vo] : 0.0f;
-          float acc_o = 0.0f;
-#pragma unroll
-          for (int rr = 0; rr < R; ++rr) {
-            float term = o[r + rr];
-            if (p.z) term *= silu_fast(zz * zeta_r[r + rr]);
-            acc_o = fmaf(phi_r[r + rr], term, acc_o);
-          }
-          p.out[(((long long)bi * H + h) * L + t_s) * dv + pcol] = acc_o;
+        for (int rr = 0; rr < R; ++rr) {
+          float term = Y[r + rr] + dskip * st.x[r + rr];
+          if (p.z) term *= silu_fast(st.z[r] * zeta[r + rr]);
+          acc = fmaf(phi[r + rr], term, acc);
         }
+        p.out[(((long long)bi * H + h) * L + t) * dv + pcol] = acc;
       }
     }
-    if (ch + 1 == p.nchunks) {
-      if (p.last_state)
-        *reinterpret_cast<f4*>(p.last_state + ((long long)seq * dv + pcol) * dqk + n0) = S;
-      if (p.last_bx && part == 0) {
-        const long long gl = L - 1;  // the traversal's final step
-        if (ch * (long long)T + step_i == gl && lj < 4)
-          *reinterpret_cast<f4*>(p.last_bx + (long long)seq * dqk + n0) = kr * gi[3];
+  };
+
+  f4 kr_last = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int ch = 0; ch < p.nchunks; ++ch) {
+    // Stage ch has landed once at most this many of the wave's operations are
+    // outstanding: the DMA stages issued after it and the epilogue stores
+    // issued after it (iterations ch-NS+2 .. ch-1, from the second on).
+    {
+      const int later = (ch + NS - 2 < p.nchunks - 1 ? ch + NS - 2 : p.nchunks - 1) - ch;
+      const int first_st = ch - NS + 2 > 1 ? ch - NS + 2 : 1;
+      const int st_groups = ch - first_st;
+      wait_vm_at_most(later * dma_per_stage + (st_groups > 0 ? st_groups * stores_per_chunk : 0));
+    }
+    lds_barrier();
+    if (ewave && ch > 0) epilogue(ch - 1);
+    if (ch + NS - 1 < p.nchunks)
+      dma_stage<R, REV>(p, in, ch + NS - 1, stages + ((ch + NS - 1) % NS) * p.stage_floats, nt,
+                        nwaves, lane);
+
+    const float* sg = stages + (ch % NS) * p.stage_floats;
+    // ---- rotated q/k rows of this n-tile
+    const f4 q = ld4(sg + (nt * 64 + lane) * 4);
+    const f4 k = ld4(sg + off_k + (nt * 64 + lane) * 4);
+    f4 qp = {0.0f, 0.0f, 0.0f, 0.0f}, kp = qp, cs, sn;
+    if (MIMO) {
+      const int pl = ((m0 >> 4) * 64 + ((m0 & 15) >> 2) * 16 + li) * 4;
+      qp = ld4(sg + pl);
+      kp = ld4(sg + off_k + pl);
+      const int u4 = (lo ? n0 : n0 - half) >> 2;
+      cs = ld4(sg + off_cs + (u4 * T + step_i) * 4);
+      sn = ld4(sg + off_sn + (u4 * T + step_i) * 4);
+    } else {
+      const int o = ((2 * nt + (lj >> 1)) * T + li) * 4 + 2 * (lj & 1);
+      const f2 c2 = ld2(sg + off_cs + o), s2 = ld2(sg + off_sn + o);
+      cs = f4{c2[0], c2[1], 0.0f, 0.0f};
+      sn = f4{s2[0], s2[1], 0.0f, 0.0f};
+    }
+    const f4 qr = rope<MIMO>(q, qp, bq, bqp, cs, sn, lo);
+    const f4 kr = rope<MIMO>(k, kp, bk, bkp, cs, sn, lo);
+    kr_last = kr;
+    // ---- partial G^T, and partial Q S0^T per slice
+    {
+      f4 gp = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int r = 0; r < 4; ++r) gp = mfma(kr[r], qr[r], gp);
+      *reinterpret_cast<f4*>(gbuf + (ch & 1) * kMaxWaves * 256 + (nt * 64 + lane) * 4) = gp;
+    }
+#pragma unroll
+    for (int j = 0; j < PT; ++j) {
+      f4 yp = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int r = 0; r < 4; ++r) yp = mfma(qr[r], S[j][r], yp);
+      *reinterpret_cast<f4*>(ybuf + (((ch & 1) * PT + j) * kMaxWaves + nt) * 256 + lane * 4) =
+          yp;
+    }
+    // ---- K transpose, then S = e^{c_last} S + K^T diag(w) X per slice
+    *reinterpret_cast<f4*>(kt + li * kKtStride + 4 * lj) = kr;
+    float kc[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) kc[m] = kt[(4 * lj + m) * kKtStride + li];
+    const f4 w = ld4(sg + off_rec + kRecW + 4 * lj);
+    const float etot = sg[off_rec + kRecEtot];
+#pragma unroll
+    for (int j = 0; j < PT; ++j) {
+      f4 x;
+#pragma unroll
+      for (int m = 0; m < 4; ++m)
+        x[m] = sg[off_v + ((4 * lj + m) / R) * 16 * PT + j * 16 + li] * psi[j][m];
+      f4 acc = S[j] * etot;
+#pragma unroll
+      for (int m = 0; m < 4; ++m) acc = mfma(kc[m], w[m] * x[m], acc);
+      S[j] = acc;
+      if (ewave && j == ej) st.x = x;
+    }
+    if (ewave) {
+      st.m = ld4(sg + off_rec + kRecM + li * 16 + 4 * lj);
+      st.ec = ld4(sg + off_rec + kRecEc + 4 * lj);
+      if (p.z) {
+#pragma unroll
+        for (int r = 0; r < 4; r += R)
+          st.z[r] = sg[off_z + ((4 * lj + r) / R) * 16 * PT + ej * 16 + li];
       }
+    }
+  }
+  lds_barrier();
+  if (ewave) epilogue(p.nchunks - 1);
+
+  if (p.last_state) {
+#pragma unroll
+    for (int j = 0; j < PT; ++j)
+      *reinterpret_cast<f4*>(p.last_state + ((long long)seq * dv + p0 + j * 16 + li) * dqk + n0) =
+          S[j];
+  }
+  if (p.last_bx && p0 == 0) {
+    // scale k at the final step = k times the w of its row (the chunk's last valid row)
+    const int last = p.nchunks - 1;
+    if (li % R == 0 && last * T + step_i == L - 1) {
+      const float* sg = stages + (last % NS) * p.stage_floats;
+      *reinterpret_cast<f4*>(p.last_bx + (long long)seq * dqk + n0) =
+          kr_last * sg[off_rec + kRecW + li];
     }
   }
 }
 
-template <int R, bool MIMO>
+size_t chunk_lds_bytes(const M3K& k, int pt, int ns) {
+  const int WN = k.dqk / 16;
+  return sizeof(float) * ((size_t)ns * k.stage_floats + (size_t)2 * kMaxWaves * 256 +
+                          (size_t)2 * pt * kMaxWaves * 256 + (size_t)WN * 16 * kKtStride);
+}
+
+template <int R, bool MIMO, int PT>
 hipError_t launch_chunk(const M3K& k, bool rev, hipStream_t st) {
-  const int W = k.dqk / 16;
-  const long long blocks = 8LL * k.nparts * ((k.nseq + 7) / 8);
-  const size_t lds = sizeof(float) * ((size_t)2 * W * 64 * 8 + (size_t)W * 16 * kKtStride);
+  const int WN = k.dqk / 16;
+  const long long blocks = 8LL * (k.nparts / PT) * ((k.nseq + 7) / 8);
+  const size_t lds = chunk_lds_bytes(k, PT, k.nstages);
   if (rev)
-    hipLaunchKernelGGL((m3_chunk_kernel<R, MIMO, true>), dim3((unsigned)blocks), dim3(64 * W),
-                       lds, st, k);
+    hipLaunchKernelGGL((m3_chunk_kernel<R, MIMO, true, PT>), dim3((unsigned)blocks),
+                       dim3(64 * WN), lds, st, k);
   else
-    hipLaunchKernelGGL((m3_chunk_kernel<R, MIMO, false>), dim3((unsigned)blocks), dim3(64 * W),
-                       lds, st, k);
+    hipLaunchKernelGGL((m3_chunk_kernel<R, MIMO, false, PT>), dim3((unsigned)blocks),
+                       dim3(64 * WN), lds, st, k);
   return hipGetLastError();
+}
+
+template <int R, bool MIMO>
+hipError_t launch_chunk_pt(const M3K& k, bool rev, hipStream_t st) {
+  return k.ptiles == 2 ? launch_chunk<R, MIMO, 2>(k, rev, st)
+                       : launch_chunk<R, MIMO, 1>(k, rev, st);
 }
 
 }  // namespace
@@ -288,8 +532,12 @@ hipError_t launch_chunk(const M3K& k, bool rev, hipStream_t st) {
 bool m3_chunk_supported(const M3Problem& pr) {
   const bool mimo = pr.psi != nullptr;
   const bool rank_ok = mimo ? (pr.rank == 1 || pr.rank == 2 || pr.rank == 4) : pr.rank == 1;
-  return rank_ok && pr.dv % 16 == 0 && pr.dqk % 16 == 0 && pr.dqk <= 256 && pr.dqk >= 16 &&
-         pr.len > 0;
+  // 32-bit offsets within a sequence: q/k, cos/sin and v/z/out spans below 2^30 floats
+  const size_t lim = (size_t)1 << 30;
+  const bool spans = pr.len * pr.rank * pr.groups * pr.dqk < lim &&
+                     pr.len * pr.heads * pr.dv < lim && pr.len * pr.heads * pr.dqk < lim;
+  return rank_ok && pr.dv % 16 == 0 && pr.dqk % 16 == 0 && pr.dqk >= 16 &&
+         pr.dqk <= 16 * (size_t)kMaxWaves && pr.len > 0 && spans;
 }
 
 hipError_t m3_scan_chunked(const M3Problem& pr, hipStream_t st) {
@@ -298,33 +546,50 @@ hipError_t m3_scan_chunked(const M3Problem& pr, hipStream_t st) {
   k.qb = pr.q_bias; k.kb = pr.k_bias; k.cos = pr.cos; k.sin = pr.sin; k.D = pr.D; k.z = pr.z;
   k.psi = pr.psi; k.zeta = pr.zeta; k.phi = pr.phi;
   k.out = pr.out; k.last_state = pr.last_state; k.last_bx = pr.last_bx;
-  k.batch = (int)pr.batch; k.heads = (int)pr.heads; k.dv = (int)pr.dv; k.dqk = (int)pr.dqk;
-  k.len = (int)pr.len; k.rank = (int)pr.rank; k.groups = (int)pr.groups;
+  k.heads = (int)pr.heads; k.dv = (int)pr.dv; k.dqk = (int)pr.dqk;
+  k.len = (int)pr.len; k.groups = (int)pr.groups;
+  const int R = (int)pr.rank;
   k.nparts = k.dv / 16;
-  k.steps_per_chunk = 16 / k.rank;
+  k.steps_per_chunk = 16 / R;
   k.nchunks = (k.len + k.steps_per_chunk - 1) / k.steps_per_chunk;
-  k.nseq = k.batch * k.heads;
-  const size_t nsteps = (size_t)k.nseq * k.nchunks * k.steps_per_chunk;
-  const size_t bytes = nsteps * (sizeof(f4) + sizeof(float)) + (size_t)k.nseq * k.nchunks * 4;
-  char* scratch = nullptr;
-  hipError_t e = hipMallocAsync((void**)&scratch, bytes, st);
+  k.nseq = (int)(pr.batch * pr.heads);
+  const int WN = k.dqk / 16;
+  // Two dv slices per block share the q/k/cos/sin rows and G when dv allows.
+  k.ptiles = (k.nparts % 2 == 0 && WN >= 2) ? 2 : 1;
+  auto plan = [&]() {
+    const int T = k.steps_per_chunk;
+    k.n_cs = (T * (k.dqk / 8) + 63) / 64;
+    k.n_v = (T * 4 * k.ptiles + 63) / 64;
+    k.n_z = pr.z ? k.n_v : 0;
+    k.n_ins = 2 * WN + 2 * k.n_cs + k.n_v + k.n_z + (kRecPieces + 63) / 64;
+    k.stage_floats = k.n_ins * 256;
+  };
+  plan();
+  k.nstages = kStages;
+  while (k.nstages > 2 && chunk_lds_bytes(k, k.ptiles, k.nstages) > kLdsBudget) --k.nstages;
+  if (chunk_lds_bytes(k, k.ptiles, k.nstages) > kLdsBudget && k.ptiles > 1) {
+    k.ptiles = 1;
+    plan();
+  }
+  if (chunk_lds_bytes(k, k.ptiles, k.nstages) > kLdsBudget) return hipErrorInvalidValue;
+
+  const size_t nrec = (size_t)k.nseq * k.nchunks;
+  hipError_t e = hipMallocAsync((void**)&k.rec, nrec * kRecFloats * sizeof(float), st);
   if (e != hipSuccess) return e;
-  k.g.step = reinterpret_cast<f4*>(scratch);
-  k.g.w = reinterpret_cast<float*>(scratch + nsteps * sizeof(f4));
-  k.g.etot = k.g.w + nsteps;
-  const long long gthreads = (long long)k.nseq * k.nchunks;
-  hipLaunchKernelGGL(m3_gates_kernel, dim3((unsigned)((gthreads + 255) / 256)), dim3(256), 0, st,
-                     k, pr.reverse ? 1 : 0);
+  const unsigned gblocks = (unsigned)((nrec + 15) / 16);
+  const int rev = pr.reverse ? 1 : 0;
+  if (R == 1) hipLaunchKernelGGL(m3_gates_kernel<1>, dim3(gblocks), dim3(256), 0, st, k, rev);
+  else if (R == 2) hipLaunchKernelGGL(m3_gates_kernel<2>, dim3(gblocks), dim3(256), 0, st, k, rev);
+  else hipLaunchKernelGGL(m3_gates_kernel<4>, dim3(gblocks), dim3(256), 0, st, k, rev);
   e = hipGetLastError();
   if (e == hipSuccess) {
-    const bool rev = pr.reverse != 0;
     const bool mimo = pr.psi != nullptr;
-    if (!mimo) e = launch_chunk<1, false>(k, rev, st);
-    else if (k.rank == 1) e = launch_chunk<1, true>(k, rev, st);
-    else if (k.rank == 2) e = launch_chunk<2, true>(k, rev, st);
-    else e = launch_chunk<4, true>(k, rev, st);
+    if (!mimo) e = launch_chunk_pt<1, false>(k, rev, st);
+    else if (R == 1) e = launch_chunk_pt<1, true>(k, rev, st);
+    else if (R == 2) e = launch_chunk_pt<2, true>(k, rev, st);
+    else e = launch_chunk_pt<4, true>(k, rev, st);
   }
-  const hipError_t fe = hipFreeAsync(scratch, st);
+  const hipError_t fe = hipFreeAsync(k.rec, st);
   return e != hipSuccess ? e : fe;
 }
 

@@ -175,7 +175,8 @@ static bool aligned16(const void* q) { return q == nullptr || ((uintptr_t)q & 15
 hipError_t m3_scan(const M3Problem& pr, hipStream_t st) {
   const bool aligned = aligned16(pr.q) && aligned16(pr.k) && aligned16(pr.q_bias) &&
                        aligned16(pr.k_bias) && aligned16(pr.cos) && aligned16(pr.sin) &&
-                       aligned16(pr.last_state) && aligned16(pr.last_bx);
+                       aligned16(pr.v) && aligned16(pr.z) && aligned16(pr.last_state) &&
+                       aligned16(pr.last_bx);
   if (aligned && m3_chunk_supported(pr)) return m3_scan_chunked(pr, st);
   return m3_scan_sequential(pr, st);
 }
