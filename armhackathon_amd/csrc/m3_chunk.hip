@@ -79,6 +79,7 @@ struct M3K {
   int n_cs, n_v, n_z;  // cos (and again sin), v, z
   int n_ins;           // all sections, + 2 for the gate record
   int stage_floats;
+  int dma_first;       // first wave that issues DMA
 };
 
 // ---------------------------------------------------------------------------
@@ -177,68 +178,146 @@ struct SeqIn {
   int qstride, csstride, vstride;  // floats per step
 };
 
-// Issues DMA instruction `ins` of chunk ch into a stage (1 KB per instruction).
-// Stage layout in 16-byte pieces, each section padded to whole instructions:
+// DMA instruction `ins` of a stage (1 KB, one 16-byte piece per lane). Stage
+// layout in pieces, each section padded to whole instructions:
 //   q, k: piece (nt, lj, li) = columns nt*16 + 4lj .. +3 of row li
 //   cos, sin: piece u4*T + step = angles 4u4 .. 4u4+3 of the step
 //   v, z: piece step*4PT + c4 = columns p0 + 4c4 .. +3 of the step
 //   gate record: its 73 pieces in order
-template <int R, bool REV>
-__device__ __forceinline__ void dma_ins(const M3K& p, const SeqIn& s, int ins, int ch,
-                                        float* stage, int lane) {
-  const int WN = p.dqk / 16, T = p.steps_per_chunk, L = p.len;
+// The lane's piece of chunk ch is src + t*stride + col with t the memory row of
+// step `step` of the chunk, or src + ch*kRecFloats + col for the gate record.
+struct DmaPiece {
   const float* src;
-  int step = 0;    // step of the chunk the lane's piece belongs to
-  int col;         // float offset of the piece within its step's row
-  int stride = 0;  // floats per step
-  bool on = true;
+  int step, col, stride;
+  bool on, rec;
+};
+
+template <int R>
+__device__ __forceinline__ DmaPiece dma_decode(const M3K& p, const SeqIn& s, int ins, int lane) {
+  const int WN = p.dqk / 16, T = p.steps_per_chunk;
+  DmaPiece d;
+  d.step = 0;
+  d.stride = 0;
+  d.on = true;
+  d.rec = false;
   int rel = ins;
   if (rel < 2 * WN) {
     const int nt = rel < WN ? rel : rel - WN;
     const int li = lane & 15, lj = lane >> 4;
-    src = rel < WN ? s.q : s.k;
-    step = li / R;
-    col = (li % R) * p.groups * p.dqk + nt * 16 + 4 * lj;
-    stride = s.qstride;
+    d.src = rel < WN ? s.q : s.k;
+    d.step = li / R;
+    d.col = (li % R) * p.groups * p.dqk + nt * 16 + 4 * lj;
+    d.stride = s.qstride;
   } else if ((rel -= 2 * WN) < 2 * p.n_cs) {
     const bool sn = rel >= p.n_cs;
     const int j = (sn ? rel - p.n_cs : rel) * 64 + lane;
-    on = j < T * (p.dqk / 8);
-    src = sn ? s.sin : s.cos;
-    step = j % T;
-    col = 4 * (j / T);
-    stride = s.csstride;
+    d.on = j < T * (p.dqk / 8);
+    d.src = sn ? s.sin : s.cos;
+    d.step = j % T;
+    d.col = 4 * (j / T);
+    d.stride = s.csstride;
   } else if ((rel -= 2 * p.n_cs) < p.n_v + p.n_z) {
     const bool zz = rel >= p.n_v;
     const int j = (zz ? rel - p.n_v : rel) * 64 + lane;
     const int w4 = 4 * p.ptiles;
-    on = j < T * w4;
-    src = zz ? s.z : s.v;
-    step = j / w4;
-    col = 4 * (j % w4);
-    stride = s.vstride;
+    d.on = j < T * w4;
+    d.src = zz ? s.z : s.v;
+    d.step = j / w4;
+    d.col = 4 * (j % w4);
+    d.stride = s.vstride;
   } else {
     const int j = (rel - p.n_v - p.n_z) * 64 + lane;
-    on = j < kRecPieces;
-    src = s.rec + (long long)ch * kRecFloats;
-    col = 4 * j;
+    d.on = j < kRecPieces;
+    d.src = s.rec;
+    d.col = 4 * j;
+    d.rec = true;
   }
-  if (on) {
-    int g = ch * T + step;
-    g = g < L - 1 ? g : L - 1;
-    const int t = REV ? L - 1 - g : g;
-    const float* a = src + (unsigned)(t * stride + col);
-    __builtin_amdgcn_global_load_lds((const void*)a,
-                                     (__attribute__((address_space(3))) void*)(stage + ins * 256),
-                                     16, 0, 0);
+  return d;
+}
+
+__device__ __forceinline__ void dma16(const float* src, float* lds) {
+  __builtin_amdgcn_global_load_lds((const void*)src,
+                                   (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+}
+
+// The DMA instructions of one wave, resolved once. For a chunk wholly inside the
+// sequence the lane's source is base[k] + ch * delta[k] + off[k] (floats; base and
+// delta are wave-uniform); the last, partial chunk goes through dma_clamped.
+constexpr int kMaxDma = 8;
+struct DmaPlan {
+  const float* base[kMaxDma];
+  int delta[kMaxDma];
+  int off[kMaxDma];
+  bool on[kMaxDma];
+  int ins[kMaxDma];
+  int count;
+};
+
+template <int R, bool REV>
+__device__ __forceinline__ void dma_plan(const M3K& p, const SeqIn& s, int first, int step_ins,
+                                         int lane, DmaPlan& d) {
+  const int T = p.steps_per_chunk, L = p.len;
+  d.count = 0;
+#pragma unroll
+  for (int k = 0; k < kMaxDma; ++k) {
+    const int ins = first + k * step_ins;
+    d.ins[k] = ins;
+    d.on[k] = false;
+    d.base[k] = s.rec;
+    d.delta[k] = 0;
+    d.off[k] = 0;
+    if (ins < p.n_ins) {
+      const DmaPiece pc = dma_decode<R>(p, s, ins, lane);
+      d.count = k + 1;
+      d.on[k] = pc.on;
+      if (pc.rec) {
+        d.base[k] = pc.src;
+        d.delta[k] = kRecFloats;
+        d.off[k] = pc.col;
+      } else if (!REV) {
+        d.base[k] = pc.src;
+        d.delta[k] = T * pc.stride;
+        d.off[k] = pc.step * pc.stride + pc.col;
+      } else {
+        d.base[k] = pc.src + (long long)(L - 1) * pc.stride;
+        d.delta[k] = -T * pc.stride;
+        d.off[k] = pc.col - pc.step * pc.stride;
+      }
+    }
   }
 }
 
-// This wave's share of a stage: instructions wave, wave + nwaves, ...
+__device__ __forceinline__ void dma_fast(const DmaPlan& d, int ch, float* stage) {
+#pragma unroll
+  for (int k = 0; k < kMaxDma; ++k)
+    if (k < d.count && d.on[k])
+      dma16(d.base[k] + ((long long)ch * d.delta[k] + d.off[k]), stage + d.ins[k] * 256);
+}
+
+// Any chunk, with the rows past the end clamped to the last step.
 template <int R, bool REV>
-__device__ __forceinline__ void dma_stage(const M3K& p, const SeqIn& s, int ch, float* stage,
-                                          int wave, int nwaves, int lane) {
-  for (int ins = wave; ins < p.n_ins; ins += nwaves) dma_ins<R, REV>(p, s, ins, ch, stage, lane);
+__device__ __forceinline__ void dma_clamped(const M3K& p, const SeqIn& s, const DmaPlan& d,
+                                            int ch, float* stage, int lane) {
+  const int T = p.steps_per_chunk, L = p.len;
+#pragma unroll
+  for (int k = 0; k < kMaxDma; ++k) {
+    if (k >= d.count) break;
+    const DmaPiece pc = dma_decode<R>(p, s, d.ins[k], lane);
+    if (!pc.on) continue;
+    int g = ch * T + pc.step;
+    g = g < L - 1 ? g : L - 1;
+    const int t = REV ? L - 1 - g : g;
+    const long long o = pc.rec ? (long long)ch * kRecFloats + pc.col
+                               : (long long)t * pc.stride + pc.col;
+    dma16(pc.src + o, stage + d.ins[k] * 256);
+  }
+}
+
+template <int R, bool REV>
+__device__ __forceinline__ void dma_stage(const M3K& p, const SeqIn& s, const DmaPlan& d, int ch,
+                                          float* stage, int lane) {
+  if ((ch + 1) * p.steps_per_chunk <= p.len) dma_fast(d, ch, stage);
+  else dma_clamped<R, REV>(p, s, d, ch, stage, lane);
 }
 
 // Rotated q/k from the raw columns: SISO rotates interleaved pairs (2u, 2u+1)
@@ -337,14 +416,19 @@ __global__ void __launch_bounds__(64 * kMaxWaves) m3_chunk_kernel(M3K p) {
     phi[m] = MIMO ? p.phi[pj] : 1.0f;
   }
 
-  // This wave's DMA instructions per stage, and the stores its epilogue issues per
-  // chunk (a lower bound: more operations in flight only makes a wait stricter).
-  const int nwaves = WN;
-  const int dma_per_stage = (p.n_ins - nt + nwaves - 1) / nwaves;
+  // DMA is issued by waves dma_first .. WN-1 (the epilogue waves are spared when
+  // the others can carry it). Per wave: its DMA instructions per stage, and the
+  // stores its epilogue issues per chunk (a lower bound: more operations in
+  // flight only makes a wait stricter).
+  const int dma_first = p.dma_first;
+  const bool dwave = nt >= dma_first;
+  DmaPlan dp;
+  dma_plan<R, REV>(p, in, dwave ? nt - dma_first : p.n_ins, WN - dma_first, lane, dp);
+  const int dma_per_stage = dp.count;
   const int stores_per_chunk = ewave ? 4 / R : 0;
 
   for (int c = 0; c < NS - 1 && c < p.nchunks; ++c)
-    dma_stage<R, REV>(p, in, c, stages + c * p.stage_floats, nt, nwaves, lane);
+    dma_stage<R, REV>(p, in, dp, c, stages + c * p.stage_floats, lane);
 
   if (WN < kMaxWaves) {
     const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -359,6 +443,9 @@ __global__ void __launch_bounds__(64 * kMaxWaves) m3_chunk_kernel(M3K p) {
   for (int j = 0; j < PT; ++j) S[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
   Stash st = {};
 
+  // output of the lane's first row in chunk 0 (the epilogue's column p0 + 16ej + li)
+  float* out_lane = p.out + (((long long)bi * H + h) * L + (REV ? L - 1 - lj * 4 / R : lj * 4 / R)) *
+                                dv + p0 + ej * 16 + li;
   // epilogue of chunk ch for slice ej, from the partials in buffer ch & 1
   auto epilogue = [&](int ch) {
     const float* gb = gbuf + (ch & 1) * kMaxWaves * 256;
@@ -381,12 +468,11 @@ __global__ void __launch_bounds__(64 * kMaxWaves) m3_chunk_kernel(M3K p) {
     Y *= st.ec;  // lane holds Y[row = 4lj + r][p], the inter-chunk part
 #pragma unroll
     for (int m = 0; m < 4; ++m) Y = mfma(G[m], st.x[m], Y);
-    const int pcol = p0 + ej * 16 + li;
+    float* orow = out_lane + (REV ? -(long long)ch : (long long)ch) * T * dv;
 #pragma unroll
     for (int r = 0; r < 4; r += R) {
       const int g = ch * T + (4 * lj + r) / R;
       if (g < L) {
-        const int t = REV ? L - 1 - g : g;
         float acc = 0.0f;
 #pragma unroll
         for (int rr = 0; rr < R; ++rr) {
@@ -394,7 +480,7 @@ __global__ void __launch_bounds__(64 * kMaxWaves) m3_chunk_kernel(M3K p) {
           if (p.z) term *= silu_fast(st.z[r] * zeta[r + rr]);
           acc = fmaf(phi[r + rr], term, acc);
         }
-        p.out[(((long long)bi * H + h) * L + t) * dv + pcol] = acc;
+        orow[(REV ? -(r / R) : r / R) * dv] = acc;
       }
     }
   };
@@ -408,13 +494,16 @@ __global__ void __launch_bounds__(64 * kMaxWaves) m3_chunk_kernel(M3K p) {
       const int later = (ch + NS - 2 < p.nchunks - 1 ? ch + NS - 2 : p.nchunks - 1) - ch;
       const int first_st = ch - NS + 2 > 1 ? ch - NS + 2 : 1;
       const int st_groups = ch - first_st;
-      wait_vm_at_most(later * dma_per_stage + (st_groups > 0 ? st_groups * stores_per_chunk : 0));
+      // a wave without DMA waits for nothing here (its stores need not land)
+      if (dwave)
+        wait_vm_at_most(later * dma_per_stage +
+                        (st_groups > 0 ? st_groups * stores_per_chunk : 0));
     }
     lds_barrier();
     if (ewave && ch > 0) epilogue(ch - 1);
     if (ch + NS - 1 < p.nchunks)
-      dma_stage<R, REV>(p, in, ch + NS - 1, stages + ((ch + NS - 1) % NS) * p.stage_floats, nt,
-                        nwaves, lane);
+      dma_stage<R, REV>(p, in, dp, ch + NS - 1, stages + ((ch + NS - 1) % NS) * p.stage_floats,
+                        lane);
 
     const float* sg = stages + (ch % NS) * p.stage_floats;
     // ---- rotated q/k rows of this n-tile
@@ -572,6 +661,9 @@ hipError_t m3_scan_chunked(const M3Problem& pr, hipStream_t st) {
     plan();
   }
   if (chunk_lds_bytes(k, k.ptiles, k.nstages) > kLdsBudget) return hipErrorInvalidValue;
+  // DMA by the waves that run no epilogue when they can carry it, else by all
+  k.dma_first = (WN > k.ptiles && k.n_ins <= kMaxDma * (WN - k.ptiles)) ? k.ptiles : 0;
+  if (k.n_ins > kMaxDma * (WN - k.dma_first)) return hipErrorInvalidValue;
 
   const size_t nrec = (size_t)k.nseq * k.nchunks;
   hipError_t e = hipMallocAsync((void**)&k.rec, nrec * kRecFloats * sizeof(float), st);
