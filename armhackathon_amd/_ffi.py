@@ -98,14 +98,14 @@ def _declare(lib):
                   _ci, _ci, _ci,         # delta_softplus backend threading
                   _vp, _vp, _vp, _vp,    # out_fwd out_bwd last_fwd last_bwd
                   _vp]                   # stream
-    f = lib.arm_scan_mamba3_scan_f32
-    f.restype = _ci
-    f.argtypes = [ctypes.POINTER(ArmMamba3Dims),
-                  *([_vp] * 15),         # q k v adt dt trap q_bias k_bias cos sin d_skip z
+    for f in (lib.arm_scan_mamba3_scan_f32, lib.arm_scan_mamba3_scan_time_major_f32):
+        f.restype = _ci
+        f.argtypes = [ctypes.POINTER(ArmMamba3Dims),
+                      *([_vp] * 15),     # q k v adt dt trap q_bias k_bias cos sin d_skip z
                                          # psi zeta phi
-                  _ci, _ci, _ci,         # reverse backend threading
-                  _vp, _vp, _vp,         # out last_state last_bx
-                  _vp]                   # stream
+                      _ci, _ci, _ci,     # reverse backend threading
+                      _vp, _vp, _vp,     # out last_state last_bx
+                      _vp]               # stream
     f = lib.arm_scan_ss2d_f32
     f.restype = _ci
     f.argtypes = [ctypes.POINTER(ArmSS2DDims),
@@ -183,16 +183,18 @@ def scan_bidir_raw(dims, ptr_u, ptr_delta, ptr_a, ptr_b, ptr_c, ptr_d_skip, ptr_
 
 
 def mamba3_raw(dims, ptrs, reverse, backend, threading, ptr_out, ptr_last_state,
-               ptr_last_bx, *, stream=0):
-    """Call arm_scan_mamba3_scan_f32 with the 15 input pointers in signature
+               ptr_last_bx, *, stream=0, time_major=False):
+    """Call arm_scan_mamba3_scan_f32 (out head-major (b, h, l, dv)), or with
+    time_major its (b, l, h, dv) twin, with the 15 input pointers in signature
     order: q, k, v, adt, dt, trap, q_bias, k_bias, cos, sin, d_skip, z, psi,
     zeta, phi (d_skip, z and the MIMO triple are nullable)."""
     if len(ptrs) != 15:
         raise ValueError(f"expected 15 input pointers, got {len(ptrs)}")
-    code = load().arm_scan_mamba3_scan_f32(
+    name = "arm_scan_mamba3_scan_time_major_f32" if time_major else "arm_scan_mamba3_scan_f32"
+    code = getattr(load(), name)(
         ctypes.byref(dims), *[_p(x) for x in ptrs], int(reverse), int(backend),
         int(threading), ptr_out, _p(ptr_last_state), _p(ptr_last_bx), _p(stream))
-    _check("arm_scan_mamba3_scan_f32", code)
+    _check(name, code)
 
 
 def ss2d_raw(dims, ptr_u, ptr_delta, ptr_a, ptr_b4, ptr_c4, ptr_d_skip, ptr_z,

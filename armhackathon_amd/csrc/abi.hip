@@ -8,7 +8,9 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdarg>
+#include <cstdint>
 #include <cstdio>
 #include <cstring>
 #include <string>
@@ -77,6 +79,27 @@ int run(hipError_t e, const char* where) {
 
 }  // namespace
 
+namespace armscan {
+
+hipError_t stream_alloc(void** p, size_t bytes, hipStream_t st) {
+  static std::atomic<unsigned long long> pools_set{0};  // one bit per device (< 64)
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  const unsigned long long bit = 1ull << (dev & 63);
+  if (!(pools_set.load() & bit)) {
+    hipMemPool_t pool;
+    if (hipDeviceGetDefaultMemPool(&pool, dev) == hipSuccess) {
+      uint64_t keep = UINT64_MAX;
+      hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep);
+    }
+    pools_set.fetch_or(bit);
+  }
+  return hipMallocAsync(p, bytes, st);
+}
+
+}  // namespace armscan
+
 extern "C" {
 
 uint32_t arm_scan_abi_version(void) { return ARM_SCAN_ABI_VERSION; }
@@ -129,13 +152,13 @@ int arm_scan_selective_scan_bidirectional_f32(
   return run(armscan::m1_scan(p, st), "bidirectional (reverse) launch");
 }
 
-int arm_scan_mamba3_scan_f32(const ArmMamba3Dims* dims, const float* q, const float* k,
-                             const float* v, const float* adt, const float* dt,
-                             const float* trap, const float* q_bias, const float* k_bias,
-                             const float* cos, const float* sin, const float* d_skip,
-                             const float* z, const float* mimo_psi, const float* mimo_zeta,
-                             const float* mimo_phi, int reverse, int backend, int threading,
-                             float* out, float* last_state, float* last_bx, void* stream) {
+static int mamba3_call(const ArmMamba3Dims* dims, const float* q, const float* k,
+                       const float* v, const float* adt, const float* dt, const float* trap,
+                       const float* q_bias, const float* k_bias, const float* cos,
+                       const float* sin, const float* d_skip, const float* z,
+                       const float* mimo_psi, const float* mimo_zeta, const float* mimo_phi,
+                       int reverse, int backend, int threading, float* out, float* last_state,
+                       float* last_bx, void* stream, bool time_major) {
   if (!dims || !q || !k || !v || !adt || !dt || !trap || !q_bias || !k_bias || !cos || !sin ||
       !out)
     return fail(ARM_SCAN_ERR_NULL_POINTER, "a required pointer is null");
@@ -170,6 +193,7 @@ int arm_scan_mamba3_scan_f32(const ArmMamba3Dims* dims, const float* q, const fl
   p.k_bias = k_bias; p.cos = cos; p.sin = sin; p.D = d_skip; p.z = z;
   p.psi = mimo_psi; p.zeta = mimo_zeta; p.phi = mimo_phi;
   p.out = out; p.last_state = last_state; p.last_bx = last_bx; p.reverse = reverse != 0;
+  p.out_time_major = time_major ? 1 : 0;
   // the chunked MFMA kernel takes dv, dqk multiples of 16 (dqk <= 256) and rank 1/2/4;
   // everything else runs the step-by-step kernel, whose state must fit in LDS
   const size_t need = d.dv * (d.dqk + 1) + 2 * d.rank * (d.dqk + d.dv) + d.rank * d.rank + 4;
@@ -177,6 +201,29 @@ int arm_scan_mamba3_scan_f32(const ArmMamba3Dims* dims, const float* q, const fl
     return fail(ARM_SCAN_ERR_INVALID_DIMS, "state dv*dqk (%zu x %zu) exceeds on-chip capacity",
                 d.dv, d.dqk);
   return run(armscan::m3_scan(p, (hipStream_t)stream), "mamba3 launch");
+}
+
+int arm_scan_mamba3_scan_f32(const ArmMamba3Dims* dims, const float* q, const float* k,
+                             const float* v, const float* adt, const float* dt,
+                             const float* trap, const float* q_bias, const float* k_bias,
+                             const float* cos, const float* sin, const float* d_skip,
+                             const float* z, const float* mimo_psi, const float* mimo_zeta,
+                             const float* mimo_phi, int reverse, int backend, int threading,
+                             float* out, float* last_state, float* last_bx, void* stream) {
+  return mamba3_call(dims, q, k, v, adt, dt, trap, q_bias, k_bias, cos, sin, d_skip, z,
+                     mimo_psi, mimo_zeta, mimo_phi, reverse, backend, threading, out, last_state,
+                     last_bx, stream, false);
+}
+
+int arm_scan_mamba3_scan_time_major_f32(
+    const ArmMamba3Dims* dims, const float* q, const float* k, const float* v, const float* adt,
+    const float* dt, const float* trap, const float* q_bias, const float* k_bias,
+    const float* cos, const float* sin, const float* d_skip, const float* z,
+    const float* mimo_psi, const float* mimo_zeta, const float* mimo_phi, int reverse,
+    int backend, int threading, float* out, float* last_state, float* last_bx, void* stream) {
+  return mamba3_call(dims, q, k, v, adt, dt, trap, q_bias, k_bias, cos, sin, d_skip, z,
+                     mimo_psi, mimo_zeta, mimo_phi, reverse, backend, threading, out, last_state,
+                     last_bx, stream, true);
 }
 
 int arm_scan_ss2d_f32(const ArmSS2DDims* dims, const float* u, const float* delta,
@@ -207,7 +254,7 @@ int arm_scan_ss2d_f32(const ArmSS2DDims* dims, const float* u, const float* delt
   // B/C, plus the column pair's outputs before they are transposed back.
   const size_t n_scratch = plane * (z ? 3 : 2) + 4 * bcp + 2 * plane;
   float* scratch = nullptr;
-  hipError_t e = hipMallocAsync((void**)&scratch, n_scratch * sizeof(float), st);
+  hipError_t e = armscan::stream_alloc((void**)&scratch, n_scratch * sizeof(float), st);
   if (e != hipSuccess) return hip_fail(e, "ss2d scratch allocation");
   float* uT = scratch;
   float* dT = uT + plane;

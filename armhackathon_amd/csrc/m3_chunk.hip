@@ -74,12 +74,12 @@ struct M3K {
   const float *adt, *dt, *trap;
   float *out, *last_state, *last_bx, *rec;
   int heads, dv, dqk, len, groups, nparts, nchunks, steps_per_chunk, nseq;
+  int out_tm;  // out (b, l, h, dv) instead of (b, h, l, dv)
   int ptiles, nstages;
   // DMA instructions (1 KB each) per stage: q and k take one per n-tile
   int n_cs, n_v, n_z;  // cos (and again sin), v, z
   int n_ins;           // all sections, + 2 for the gate record
   int stage_floats;
-  int dma_first;       // first wave that issues DMA
 };
 
 // ---------------------------------------------------------------------------
@@ -346,12 +346,18 @@ struct Stash {
   float z[4];
 };
 
+// Waves 0 .. WN-1 compute the partials of n-tile `wave` for every slice of the
+// block; waves WN .. WN+PT-1 finish slice wave-WN of the previous chunk. Both kinds
+// pass one barrier per chunk.
 template <int R, bool MIMO, bool REV, int PT>
-__global__ void __launch_bounds__(64 * kMaxWaves) m3_chunk_kernel(M3K p) {
+__global__ void __launch_bounds__(64 * (kMaxWaves + 2)) m3_chunk_kernel(M3K p) {
   extern __shared__ __attribute__((aligned(16))) float sm[];
   const int WN = p.dqk / 16;
   const int lane = threadIdx.x & 63;
-  const int nt = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave = n-tile
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const bool ewave = wave >= WN;                    // epilogue wave
+  const int nt = ewave ? 0 : wave;                  // n-tile of a partial wave
+  const int ej = ewave ? wave - WN : 0;             // slice of an epilogue wave
   const int li = lane & 15, lj = lane >> 4;
   // blocks of one sequence share an XCD (block id mod 8), and so its L2
   const int bx = blockIdx.x & 7, by = blockIdx.x >> 3;
@@ -364,15 +370,12 @@ __global__ void __launch_bounds__(64 * kMaxWaves) m3_chunk_kernel(M3K p) {
   const int grp = h / (H / p.groups);
   const int L = p.len, dqk = p.dqk, dv = p.dv, T = p.steps_per_chunk, NS = p.nstages;
   const int half = dqk / 2;
-  const int n0 = nt * 16 + 4 * lj;  // this lane's 4 columns of dqk
+  const int n0 = nt * 16 + 4 * lj;  // a partial wave's 4 columns of dqk
   const bool lo = !MIMO || n0 < half;
   const int step_i = li / R;
-  const float dskip = p.D ? p.D[h] : 0.0f;
-  const bool ewave = nt < PT;  // finishes slice nt
-  const int ej = ewave ? nt : 0;
 
+  // partials of every n-tile slot; the slots of absent n-tiles (WN < kMaxWaves) stay 0
   float* stages = sm;
-  // partials of every n-tile slot; the slots of absent waves (WN < kMaxWaves) stay 0
   float* gbuf = stages + NS * p.stage_floats;  // [2][kMaxWaves][64][4]
   float* ybuf = gbuf + 2 * kMaxWaves * 256;     // [2][PT][kMaxWaves][64][4]
   float* kt = ybuf + 2 * PT * kMaxWaves * 256 + nt * 16 * kKtStride;
@@ -380,6 +383,89 @@ __global__ void __launch_bounds__(64 * kMaxWaves) m3_chunk_kernel(M3K p) {
   const int off_sn = off_cs + p.n_cs * 256, off_v = off_cs + 2 * p.n_cs * 256;
   const int off_z = off_v + p.n_v * 256, off_rec = off_z + p.n_z * 256;
 
+  if (WN < kMaxWaves) {
+    const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int e = threadIdx.x; e < 2 * (1 + PT) * kMaxWaves * 64; e += blockDim.x) {
+      const int slot = (e >> 6) % kMaxWaves;
+      if (slot >= WN) *reinterpret_cast<f4*>(gbuf + e * 4) = zero;  // ybuf follows gbuf
+    }
+  }
+
+  if (ewave) {
+    // ================= epilogue wave: slice ej =================
+    const float dskip = p.D ? p.D[h] : 0.0f;
+    const int pcol = p0 + ej * 16 + li;
+    float psi[4], zeta[4], phi[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const long long pj = ((long long)h * R + (4 * lj + m) % R) * dv + pcol;
+      psi[m] = MIMO ? p.psi[pj] : 1.0f;
+      zeta[m] = (MIMO && p.z) ? p.zeta[pj] : 1.0f;
+      phi[m] = MIMO ? p.phi[pj] : 1.0f;
+    }
+    // output of the lane's first row in chunk 0; ostep floats per step
+    const int t0 = REV ? L - 1 - lj * 4 / R : lj * 4 / R;
+    const int ostep = p.out_tm ? H * dv : dv;
+    float* out_lane = p.out + pcol +
+                      (p.out_tm ? (((long long)bi * L + t0) * H + h) * dv
+                                : (((long long)bi * H + h) * L + t0) * dv);
+    Stash st = {};
+    auto epilogue = [&](int ch) {
+      const float* gb = gbuf + (ch & 1) * kMaxWaves * 256;
+      const float* yb = ybuf + ((ch & 1) * PT + ej) * kMaxWaves * 256;
+      f4 gs[kMaxWaves], ys[kMaxWaves];  // all reads in flight at once
+#pragma unroll
+      for (int w2 = 0; w2 < kMaxWaves; ++w2) {
+        gs[w2] = ld4(gb + (w2 * 64 + lane) * 4);
+        ys[w2] = ld4(yb + (w2 * 64 + lane) * 4);
+      }
+#pragma unroll
+      for (int d = kMaxWaves / 2; d > 0; d /= 2)
+#pragma unroll
+        for (int w2 = 0; w2 < d; ++w2) {
+          gs[w2] += gs[w2 + d];
+          ys[w2] += ys[w2 + d];
+        }
+      f4 G = gs[0] * st.m;   // lane holds G[i = li][s = 4lj + r], masked
+      f4 Y = ys[0] * st.ec;  // lane holds Y[row = 4lj + r][p], the inter-chunk part
+#pragma unroll
+      for (int m = 0; m < 4; ++m) Y = mfma(G[m], st.x[m], Y);
+      float* orow = out_lane + (REV ? -(long long)ch : (long long)ch) * T * ostep;
+#pragma unroll
+      for (int r = 0; r < 4; r += R) {
+        if (ch * T + (4 * lj + r) / R < L) {
+          float acc = 0.0f;
+#pragma unroll
+          for (int rr = 0; rr < R; ++rr) {
+            float term = Y[r + rr] + dskip * st.x[r + rr];
+            if (p.z) term *= silu_fast(st.z[r] * zeta[r + rr]);
+            acc = fmaf(phi[r + rr], term, acc);
+          }
+          orow[(REV ? -(r / R) : r / R) * ostep] = acc;
+        }
+      }
+    };
+    for (int ch = 0; ch < p.nchunks; ++ch) {
+      lds_barrier();  // stage ch landed, partials of chunk ch-1 written
+      if (ch > 0) epilogue(ch - 1);
+      const float* sg = stages + (ch % NS) * p.stage_floats;
+      st.m = ld4(sg + off_rec + kRecM + li * 16 + 4 * lj);
+      st.ec = ld4(sg + off_rec + kRecEc + 4 * lj);
+#pragma unroll
+      for (int m = 0; m < 4; ++m)
+        st.x[m] = sg[off_v + ((4 * lj + m) / R) * 16 * PT + ej * 16 + li] * psi[m];
+      if (p.z) {
+#pragma unroll
+        for (int r = 0; r < 4; r += R)
+          st.z[r] = sg[off_z + ((4 * lj + r) / R) * 16 * PT + ej * 16 + li];
+      }
+    }
+    lds_barrier();
+    epilogue(p.nchunks - 1);
+    return;
+  }
+
+  // ================= partial wave: n-tile nt =================
   SeqIn in;
   in.q = p.q + ((long long)bi * L * R * p.groups + grp) * dqk;
   in.k = p.k + ((long long)bi * L * R * p.groups + grp) * dqk;
@@ -392,7 +478,7 @@ __global__ void __launch_bounds__(64 * kMaxWaves) m3_chunk_kernel(M3K p) {
   in.csstride = H * half;
   in.vstride = H * dv;
 
-  // biases of the lane's columns (row li has rank li % R) and the MIMO projections
+  // biases of the lane's columns (row li has rank li % R)
   f4 bq, bk, bqp = {0.0f, 0.0f, 0.0f, 0.0f}, bkp = bqp;
   const int m0 = n0 < half ? n0 + half : n0 - half;  // MIMO partner columns
   {
@@ -404,103 +490,31 @@ __global__ void __launch_bounds__(64 * kMaxWaves) m3_chunk_kernel(M3K p) {
       bkp = ld4(p.kb + bo + m0);
     }
   }
-  float psi[PT][4], zeta[4], phi[4];
+  float psi[PT][4];
 #pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    const int rk = (4 * lj + m) % R;
+  for (int m = 0; m < 4; ++m)
 #pragma unroll
     for (int j = 0; j < PT; ++j)
-      psi[j][m] = MIMO ? p.psi[((long long)h * R + rk) * dv + p0 + j * 16 + li] : 1.0f;
-    const long long pj = ((long long)h * R + rk) * dv + p0 + ej * 16 + li;
-    zeta[m] = (MIMO && p.z) ? p.zeta[pj] : 1.0f;
-    phi[m] = MIMO ? p.phi[pj] : 1.0f;
-  }
+      psi[j][m] = MIMO ? p.psi[((long long)h * R + (4 * lj + m) % R) * dv + p0 + j * 16 + li]
+                       : 1.0f;
 
-  // DMA is issued by waves dma_first .. WN-1 (the epilogue waves are spared when
-  // the others can carry it). Per wave: its DMA instructions per stage, and the
-  // stores its epilogue issues per chunk (a lower bound: more operations in
-  // flight only makes a wait stricter).
-  const int dma_first = p.dma_first;
-  const bool dwave = nt >= dma_first;
+  // The DMA instructions of this wave; the partial waves issue no other vector
+  // memory operation inside the loop.
   DmaPlan dp;
-  dma_plan<R, REV>(p, in, dwave ? nt - dma_first : p.n_ins, WN - dma_first, lane, dp);
-  const int dma_per_stage = dp.count;
-  const int stores_per_chunk = ewave ? 4 / R : 0;
-
+  dma_plan<R, REV>(p, in, nt, WN, lane, dp);
   for (int c = 0; c < NS - 1 && c < p.nchunks; ++c)
     dma_stage<R, REV>(p, in, dp, c, stages + c * p.stage_floats, lane);
-
-  if (WN < kMaxWaves) {
-    const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int e = nt * 64 + lane; e < 2 * (1 + PT) * kMaxWaves * 64; e += WN * 64) {
-      const int slot = (e >> 6) % kMaxWaves;
-      if (slot >= WN) *reinterpret_cast<f4*>(gbuf + e * 4) = zero;  // ybuf follows gbuf
-    }
-  }
 
   f4 S[PT];
 #pragma unroll
   for (int j = 0; j < PT; ++j) S[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-  Stash st = {};
-
-  // output of the lane's first row in chunk 0 (the epilogue's column p0 + 16ej + li)
-  float* out_lane = p.out + (((long long)bi * H + h) * L + (REV ? L - 1 - lj * 4 / R : lj * 4 / R)) *
-                                dv + p0 + ej * 16 + li;
-  // epilogue of chunk ch for slice ej, from the partials in buffer ch & 1
-  auto epilogue = [&](int ch) {
-    const float* gb = gbuf + (ch & 1) * kMaxWaves * 256;
-    const float* yb = ybuf + ((ch & 1) * PT + ej) * kMaxWaves * 256;
-    f4 gs[kMaxWaves], ys[kMaxWaves];  // all reads in flight at once
-#pragma unroll
-    for (int w2 = 0; w2 < kMaxWaves; ++w2) {
-      gs[w2] = ld4(gb + (w2 * 64 + lane) * 4);
-      ys[w2] = ld4(yb + (w2 * 64 + lane) * 4);
-    }
-#pragma unroll
-    for (int d = kMaxWaves / 2; d > 0; d /= 2)
-#pragma unroll
-      for (int w2 = 0; w2 < d; ++w2) {
-        gs[w2] += gs[w2 + d];
-        ys[w2] += ys[w2 + d];
-      }
-    f4 G = gs[0], Y = ys[0];
-    G *= st.m;   // lane holds G[i = li][s = 4lj + r]
-    Y *= st.ec;  // lane holds Y[row = 4lj + r][p], the inter-chunk part
-#pragma unroll
-    for (int m = 0; m < 4; ++m) Y = mfma(G[m], st.x[m], Y);
-    float* orow = out_lane + (REV ? -(long long)ch : (long long)ch) * T * dv;
-#pragma unroll
-    for (int r = 0; r < 4; r += R) {
-      const int g = ch * T + (4 * lj + r) / R;
-      if (g < L) {
-        float acc = 0.0f;
-#pragma unroll
-        for (int rr = 0; rr < R; ++rr) {
-          float term = Y[r + rr] + dskip * st.x[r + rr];
-          if (p.z) term *= silu_fast(st.z[r] * zeta[r + rr]);
-          acc = fmaf(phi[r + rr], term, acc);
-        }
-        orow[(REV ? -(r / R) : r / R) * dv] = acc;
-      }
-    }
-  };
-
   f4 kr_last = {0.0f, 0.0f, 0.0f, 0.0f};
   for (int ch = 0; ch < p.nchunks; ++ch) {
-    // Stage ch has landed once at most this many of the wave's operations are
-    // outstanding: the DMA stages issued after it and the epilogue stores
-    // issued after it (iterations ch-NS+2 .. ch-1, from the second on).
-    {
-      const int later = (ch + NS - 2 < p.nchunks - 1 ? ch + NS - 2 : p.nchunks - 1) - ch;
-      const int first_st = ch - NS + 2 > 1 ? ch - NS + 2 : 1;
-      const int st_groups = ch - first_st;
-      // a wave without DMA waits for nothing here (its stores need not land)
-      if (dwave)
-        wait_vm_at_most(later * dma_per_stage +
-                        (st_groups > 0 ? st_groups * stores_per_chunk : 0));
-    }
+    // Stage ch has landed once no more of this wave's DMA is outstanding than the
+    // stages issued after it.
+    const int later = (ch + NS - 2 < p.nchunks - 1 ? ch + NS - 2 : p.nchunks - 1) - ch;
+    wait_vm_at_most(later * dp.count);
     lds_barrier();
-    if (ewave && ch > 0) epilogue(ch - 1);
     if (ch + NS - 1 < p.nchunks)
       dma_stage<R, REV>(p, in, dp, ch + NS - 1, stages + ((ch + NS - 1) % NS) * p.stage_floats,
                         lane);
@@ -550,28 +564,16 @@ __global__ void __launch_bounds__(64 * kMaxWaves) m3_chunk_kernel(M3K p) {
     const float etot = sg[off_rec + kRecEtot];
 #pragma unroll
     for (int j = 0; j < PT; ++j) {
-      f4 x;
-#pragma unroll
-      for (int m = 0; m < 4; ++m)
-        x[m] = sg[off_v + ((4 * lj + m) / R) * 16 * PT + j * 16 + li] * psi[j][m];
       f4 acc = S[j] * etot;
 #pragma unroll
-      for (int m = 0; m < 4; ++m) acc = mfma(kc[m], w[m] * x[m], acc);
-      S[j] = acc;
-      if (ewave && j == ej) st.x = x;
-    }
-    if (ewave) {
-      st.m = ld4(sg + off_rec + kRecM + li * 16 + 4 * lj);
-      st.ec = ld4(sg + off_rec + kRecEc + 4 * lj);
-      if (p.z) {
-#pragma unroll
-        for (int r = 0; r < 4; r += R)
-          st.z[r] = sg[off_z + ((4 * lj + r) / R) * 16 * PT + ej * 16 + li];
+      for (int m = 0; m < 4; ++m) {
+        const float x = sg[off_v + ((4 * lj + m) / R) * 16 * PT + j * 16 + li] * psi[j][m];
+        acc = mfma(kc[m], w[m] * x, acc);
       }
+      S[j] = acc;
     }
   }
   lds_barrier();
-  if (ewave) epilogue(p.nchunks - 1);
 
   if (p.last_state) {
 #pragma unroll
@@ -603,10 +605,10 @@ hipError_t launch_chunk(const M3K& k, bool rev, hipStream_t st) {
   const size_t lds = chunk_lds_bytes(k, PT, k.nstages);
   if (rev)
     hipLaunchKernelGGL((m3_chunk_kernel<R, MIMO, true, PT>), dim3((unsigned)blocks),
-                       dim3(64 * WN), lds, st, k);
+                       dim3(64 * (WN + PT)), lds, st, k);
   else
     hipLaunchKernelGGL((m3_chunk_kernel<R, MIMO, false, PT>), dim3((unsigned)blocks),
-                       dim3(64 * WN), lds, st, k);
+                       dim3(64 * (WN + PT)), lds, st, k);
   return hipGetLastError();
 }
 
@@ -635,6 +637,7 @@ hipError_t m3_scan_chunked(const M3Problem& pr, hipStream_t st) {
   k.qb = pr.q_bias; k.kb = pr.k_bias; k.cos = pr.cos; k.sin = pr.sin; k.D = pr.D; k.z = pr.z;
   k.psi = pr.psi; k.zeta = pr.zeta; k.phi = pr.phi;
   k.out = pr.out; k.last_state = pr.last_state; k.last_bx = pr.last_bx;
+  k.out_tm = pr.out_time_major;
   k.heads = (int)pr.heads; k.dv = (int)pr.dv; k.dqk = (int)pr.dqk;
   k.len = (int)pr.len; k.groups = (int)pr.groups;
   const int R = (int)pr.rank;
@@ -661,12 +664,10 @@ hipError_t m3_scan_chunked(const M3Problem& pr, hipStream_t st) {
     plan();
   }
   if (chunk_lds_bytes(k, k.ptiles, k.nstages) > kLdsBudget) return hipErrorInvalidValue;
-  // DMA by the waves that run no epilogue when they can carry it, else by all
-  k.dma_first = (WN > k.ptiles && k.n_ins <= kMaxDma * (WN - k.ptiles)) ? k.ptiles : 0;
-  if (k.n_ins > kMaxDma * (WN - k.dma_first)) return hipErrorInvalidValue;
+  if (k.n_ins > kMaxDma * WN) return hipErrorInvalidValue;  // DMA by the WN partial waves
 
   const size_t nrec = (size_t)k.nseq * k.nchunks;
-  hipError_t e = hipMallocAsync((void**)&k.rec, nrec * kRecFloats * sizeof(float), st);
+  hipError_t e = stream_alloc((void**)&k.rec, nrec * kRecFloats * sizeof(float), st);
   if (e != hipSuccess) return e;
   const unsigned gblocks = (unsigned)((nrec + 15) / 16);
   const int rev = pr.reverse ? 1 : 0;

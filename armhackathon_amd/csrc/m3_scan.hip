@@ -35,7 +35,7 @@ constexpr size_t kM3MaxLdsFloats = 15 * 1024;  // 60 KB
 struct M3Args {
   const float *q, *k, *v, *adt, *dt, *trap, *qb, *kb, *cos, *sin, *D, *z, *psi, *zeta, *phi;
   float *out, *last_state, *last_bx;
-  int heads, dv, dqk, len, rank, groups, reverse, mimo;
+  int heads, dv, dqk, len, rank, groups, reverse, mimo, out_tm;
 };
 
 __global__ void __launch_bounds__(kM3Threads) m3_seq_kernel(M3Args p) {
@@ -56,7 +56,10 @@ __global__ void __launch_bounds__(kM3Threads) m3_seq_kernel(M3Args p) {
   const int grp = h / (p.heads / p.groups);
   const long long gate_base = (long long)bh * L;
   const float dskip = p.D ? p.D[h] : 0.0f;
-  float* orow = p.out + (long long)bh * L * dv;  // head-major (b, h, l, dv)
+  // head-major (b, h, l, dv), or time-major (b, l, h, dv)
+  float* orow = p.out_tm ? p.out + ((long long)bi * L * p.heads + h) * dv
+                         : p.out + (long long)bh * L * dv;
+  const long long ostep = p.out_tm ? (long long)p.heads * dv : dv;
 
   for (int e = tid; e < dv * SP; e += kM3Threads) S[e] = 0.0f;
   __syncthreads();
@@ -126,7 +129,7 @@ __global__ void __launch_bounds__(kM3Threads) m3_seq_kernel(M3Args p) {
       float* sp = S + pp * SP + j;
       *sp = fmaf(alpha, *sp, scale * upd);
     }
-    float* dst = orow + (long long)t * dv;
+    float* dst = orow + (long long)t * ostep;
     for (int pp = tid; pp < dv; pp += kM3Threads) {
       float o;
       if (!p.mimo) {
@@ -192,6 +195,7 @@ hipError_t m3_scan_sequential(const M3Problem& pr, hipStream_t st) {
   a.heads = (int)pr.heads; a.dv = (int)pr.dv; a.dqk = (int)pr.dqk; a.len = (int)pr.len;
   a.rank = (int)pr.rank; a.groups = (int)pr.groups; a.reverse = pr.reverse;
   a.mimo = pr.psi != nullptr;
+  a.out_tm = pr.out_time_major;
   const unsigned blocks = (unsigned)(pr.batch * pr.heads);
   hipLaunchKernelGGL(m3_seq_kernel, dim3(blocks), dim3(kM3Threads), fl * sizeof(float), st, a);
   return hipGetLastError();

@@ -37,6 +37,7 @@ struct M3Problem {
   const float *psi, *zeta, *phi;  // all null = SISO
   float *out, *last_state, *last_bx;
   int reverse;
+  int out_time_major;  // out (b, l, h, dv) instead of head-major (b, h, l, dv)
 };
 
 // Largest dv * dqk the Mamba-3 kernel holds on chip.
@@ -47,5 +48,9 @@ hipError_t m3_scan_sequential(const M3Problem& p, hipStream_t st);
 // The chunked MFMA path (m3_chunk.hip): dv, dqk multiples of 16, rank 1/2/4.
 bool m3_chunk_supported(const M3Problem& p);
 hipError_t m3_scan_chunked(const M3Problem& p, hipStream_t st);
+
+// Stream-ordered scratch from the device's default pool, whose release threshold
+// is raised once per device so that freed blocks stay cached between calls.
+hipError_t stream_alloc(void** p, size_t bytes, hipStream_t st);
 
 }  // namespace armscan

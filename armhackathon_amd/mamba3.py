@@ -61,7 +61,9 @@ def _run(q, k, v, adt, dt, trap, q_bias, k_bias, cos, sin, d_skip, z, reverse, p
         rank = 1
     h, dv = v.shape[2], v.shape[3]
     dims = _ffi.ArmMamba3Dims(b, h, dv, dqk, length, rank, groups)
-    out_hm = torch.empty((b, h, length, dv), dtype=torch.float32, device=dev)
+    # written time-major by the kernel (python/arm_scan/mamba3.py:142 permutes the
+    # head-major result into this layout)
+    out = torch.empty((b, length, h, dv), dtype=torch.float32, device=dev)
     last_state = torch.empty((b, h, dv, dqk), dtype=torch.float32, device=dev) \
         if want_state else None
     last_bx = torch.empty((b, h, dqk), dtype=torch.float32, device=dev) \
@@ -73,9 +75,10 @@ def _run(q, k, v, adt, dt, trap, q_bias, k_bias, cos, sin, d_skip, z, reverse, p
              trap.data_ptr(), q_bias.data_ptr(), k_bias.data_ptr(), cos.data_ptr(),
              sin.data_ptr(), _ptr(d_skip), _ptr(z), _ptr(psi), _ptr(zeta), _ptr(phi)],
             1 if reverse else 0, _ffi.BACKENDS["auto"], _ffi.THREADING["auto"],
-            out_hm.data_ptr(), _ptr(last_state), _ptr(last_bx), stream=_stream(dev))
+            out.data_ptr(), _ptr(last_state), _ptr(last_bx), stream=_stream(dev),
+            time_major=True)
     _CALLS["n"] += 1
-    return out_hm, last_state, last_bx
+    return out, last_state, last_bx
 
 
 @torch.library.custom_op("arm_scan::mamba3_scan", mutates_args=())
@@ -97,10 +100,9 @@ def _mamba3_scan_op(
     zeta: Optional[torch.Tensor] = None,
     phi: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
-    out_hm, _, _ = _run(q, k, v, adt, dt, trap, q_bias, k_bias, cos, sin, d_skip, z, reverse,
-                        psi, zeta, phi, False)
-    # the kernel writes head-major (b, h, l, dv); the model's world is time-major
-    return out_hm.permute(0, 2, 1, 3).contiguous()
+    out, _, _ = _run(q, k, v, adt, dt, trap, q_bias, k_bias, cos, sin, d_skip, z, reverse,
+                     psi, zeta, phi, False)
+    return out
 
 
 @_mamba3_scan_op.register_fake
@@ -184,8 +186,7 @@ def mamba3_scan(q, k, v, adt, dt, trap, q_bias, k_bias, angles=None,
             _c(sin), None if D is None else _c(D), None if z is None else _c(z), bool(reverse))
     if not return_last_state:
         return _mamba3_scan_op(*args)
-    out_hm, ls, lbx = _run(*args, None, None, None, True)
-    return out_hm.permute(0, 2, 1, 3).contiguous(), ls, lbx
+    return _run(*args, None, None, None, True)
 
 
 def mamba3_scan_pair(q, k, v, adt, dt, trap, q_bias, k_bias, angles=None,
@@ -225,5 +226,5 @@ def mamba3_mimo_scan(q, k, v, adt, dt, trap, q_bias, k_bias, psi, zeta, phi,
             bool(reverse), _c(psi), _c(zeta), _c(phi))
     if not return_last_state:
         return _mamba3_scan_op(*args)
-    out_hm, ls, _ = _run(*args, True)
-    return out_hm.permute(0, 2, 1, 3).contiguous(), ls
+    out, ls, _ = _run(*args, True)
+    return out, ls

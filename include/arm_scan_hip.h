@@ -104,6 +104,17 @@ int arm_scan_mamba3_scan_f32(const ArmMamba3Dims* dims, const float* q, const fl
                              const float* mimo_phi, int reverse, int backend, int threading,
                              float* out, float* last_state, float* last_bx, void* stream);
 
+/* New in ABI 8 (no counterpart in the reference): arm_scan_mamba3_scan_f32 with out
+ * written time-major (batch, len, heads, dv), the layout python/arm_scan/mamba3.py:142
+ * produces from the head-major result with a permute and a copy. Same arguments,
+ * checks and codes. */
+int arm_scan_mamba3_scan_time_major_f32(
+    const ArmMamba3Dims* dims, const float* q, const float* k, const float* v, const float* adt,
+    const float* dt, const float* trap, const float* q_bias, const float* k_bias,
+    const float* cos, const float* sin, const float* d_skip, const float* z,
+    const float* mimo_psi, const float* mimo_zeta, const float* mimo_phi, int reverse,
+    int backend, int threading, float* out, float* last_state, float* last_bx, void* stream);
+
 /* New in ABI 8 (no single reference symbol: it fuses python/arm_scan/ss2d.py:277-342,
  * which composes two bidirectional calls). Four directions over a (H, W) grid:
  * row_fwd, row_bwd over the row-major flattening t = i*W + j, col_fwd, col_bwd over the

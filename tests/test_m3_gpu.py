@@ -196,3 +196,28 @@ def test_m3_mimo_benchmark_shape():
                                      dtype=np.float64, want_state=True)
     assert rel_err(host(out), ref.transpose(0, 2, 1, 3)) < TOL
     assert rel_err(host(ls), rls) < TOL
+
+
+def test_m3_head_major_entry_matches_time_major():
+    """arm_scan_mamba3_scan_f32 (the reference's head-major out) and its time-major
+    twin write the same values, for the chunked and the step-by-step kernels."""
+    import torch
+
+    from armhackathon_amd import _ffi
+
+    for dqk in (32, 8):  # 8: not a multiple of 16, the step-by-step kernel
+        case(f"head-major vs time-major entry, dqk={dqk}")
+        x = workloads.m3_siso(batch=2, length=45, heads=3, dv=16, dqk=dqk, seed=5)
+        t = dev(x)
+        b, length, h, dv = x["v"].shape
+        dims = _ffi.ArmMamba3Dims(b, h, dv, dqk, length, 1, h)  # per-head q/k
+        ptrs = [t[k].data_ptr() for k in SISO_KEYS] + [t["cos"].data_ptr(),
+                                                       t["sin"].data_ptr(), 0, 0, 0, 0, 0]
+        hm = torch.full((b, h, length, dv), float("nan"), device="cuda")
+        tm = torch.full((b, length, h, dv), float("nan"), device="cuda")
+        for out, major in ((hm, False), (tm, True)):
+            _ffi.mamba3_raw(dims, ptrs, 0, 0, 0, out.data_ptr(), 0, 0,
+                            stream=torch.cuda.current_stream().cuda_stream, time_major=major)
+        torch.cuda.synchronize()
+        assert torch.equal(hm.permute(0, 2, 1, 3), tm)
+        assert rel_err(host(tm), _siso_ref(x).transpose(0, 2, 1, 3)) < TOL
