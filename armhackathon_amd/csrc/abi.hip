@@ -250,7 +250,53 @@ int arm_scan_ss2d_f32(const ArmSS2DDims* dims, const float* u, const float* delt
   p.batch = d.batch; p.dim = d.dim; p.len = L; p.state = d.state; p.groups = 1;
   p.A = a; p.D = d_skip; p.bias = delta_bias; p.softplus = delta_softplus != 0;
 
-  // Scratch: the column-major views of u, delta, z and the column directions'
+  float* ls0 = last_states;
+  auto last_of = [&](int k) { return ls0 ? ls0 + (size_t)k * bdn : nullptr; };
+  {
+    armscan::M1Problem q = p;
+    q.u = u; q.delta = delta; q.z = z;
+    if (armscan::m1_jobs_supported(q, H, W) && plane % 4 == 0) {
+      // One launch for the four directions: u, delta, z stay in grid layout (the
+      // column directions read them in the column index mode); only the column
+      // directions' B/C are transposed into traversal order. Direction planes go
+      // to out (merge none), or direction 0 to out and 1-3 to scratch, summed after.
+      const bool none = merge == 0;
+      const size_t n_scratch = 4 * bcp + (none ? 0 : 3 * plane);
+      float* scratch = nullptr;
+      hipError_t e = armscan::stream_alloc((void**)&scratch, n_scratch * sizeof(float), st);
+      if (e != hipSuccess) return hip_fail(e, "ss2d scratch allocation");
+      float* bT = scratch;  // b4[2], b4[3], c4[2], c4[3] in column-major order
+      float* planes = scratch + 4 * bcp;
+      auto plane_of = [&](int k) {
+        return none ? out + (size_t)k * plane : (k == 0 ? out : planes + (size_t)(k - 1) * plane);
+      };
+      const long long bn = (long long)(d.batch * d.state);
+      for (int kk = 0; kk < 2 && e == hipSuccess; ++kk) {
+        e = armscan::transpose_hw(b4 + (2 + kk) * bcp, bT + kk * bcp, bn, (int)H, (int)W, false,
+                                  st);
+        if (e == hipSuccess)
+          e = armscan::transpose_hw(c4 + (2 + kk) * bcp, bT + (2 + kk) * bcp, bn, (int)H,
+                                    (int)W, false, st);
+      }
+      if (e == hipSuccess) {
+        const armscan::M1JobSpec jobs[4] = {
+            {b4, c4, plane_of(0), last_of(0), 0, 0},
+            {b4 + bcp, c4 + bcp, plane_of(1), last_of(1), 1, 0},
+            {bT, bT + 2 * bcp, plane_of(2), last_of(2), 0, 1},
+            {bT + bcp, bT + 3 * bcp, plane_of(3), last_of(3), 1, 1}};
+        e = armscan::m1_scan_jobs(q, H, W, jobs, 4, st);
+      }
+      if (e == hipSuccess && !none)
+        e = armscan::add3_inplace(out, planes, planes + plane, planes + 2 * plane,
+                                  (long long)plane, merge == 2 ? 0.25f : 1.0f, st);
+      int rc = e == hipSuccess ? ARM_SCAN_OK : hip_fail(e, "ss2d launch");
+      const hipError_t fe = hipFreeAsync(scratch, st);
+      if (rc == ARM_SCAN_OK && fe != hipSuccess) rc = hip_fail(fe, "ss2d scratch free");
+      return rc;
+    }
+  }
+
+  // Otherwise: the column-major views of u, delta, z and the column directions'
   // B/C, plus the column pair's outputs before they are transposed back.
   const size_t n_scratch = plane * (z ? 3 : 2) + 4 * bcp + 2 * plane;
   float* scratch = nullptr;

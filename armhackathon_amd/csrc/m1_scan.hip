@@ -531,6 +531,21 @@ __global__ void __launch_bounds__(256) scale_kernel(float* __restrict__ x, long 
   if (i < n) x[i] *= scale;
 }
 
+// x = (x + a + b + c) * scale over n floats, 4 per lane (n % 4 == 0, 16-byte
+// aligned): the merge of a 2D cross-scan's four direction planes.
+__global__ void __launch_bounds__(256) add3_kernel(float4* __restrict__ x,
+                                                   const float4* __restrict__ a,
+                                                   const float4* __restrict__ b,
+                                                   const float4* __restrict__ c, long long n4,
+                                                   float scale) {
+  for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n4;
+       i += (long long)gridDim.x * 256) {
+    const float4 p = x[i], q = a[i], r = b[i], t = c[i];
+    x[i] = make_float4((p.x + q.x + r.x + t.x) * scale, (p.y + q.y + r.y + t.y) * scale,
+                       (p.z + q.z + r.z + t.z) * scale, (p.w + q.w + r.w + t.w) * scale);
+  }
+}
+
 __global__ void __launch_bounds__(256) add_kernel(float* __restrict__ x,
                                                   const float* __restrict__ y, long long n) {
   const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
@@ -674,6 +689,17 @@ hipError_t transpose_hw(const float* in, float* out, long long planes, int H, in
 hipError_t add_inplace(float* x, const float* y, long long n, hipStream_t st) {
   const long long blocks = (n + 255) / 256;
   hipLaunchKernelGGL(add_kernel, dim3((unsigned)blocks), dim3(256), 0, st, x, y, n);
+  return hipGetLastError();
+}
+
+hipError_t add3_inplace(float* x, const float* a, const float* b, const float* c, long long n,
+                        float scale, hipStream_t st) {
+  const long long n4 = n / 4;
+  const long long blocks = (n4 + 255) / 256 < 8192 ? (n4 + 255) / 256 : 8192;
+  hipLaunchKernelGGL(add3_kernel, dim3((unsigned)blocks), dim3(256), 0, st,
+                     reinterpret_cast<float4*>(x), reinterpret_cast<const float4*>(a),
+                     reinterpret_cast<const float4*>(b), reinterpret_cast<const float4*>(c), n4,
+                     scale);
   return hipGetLastError();
 }
 

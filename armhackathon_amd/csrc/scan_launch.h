@@ -23,12 +23,26 @@ hipError_t m1_scan(const M1Problem& p, hipStream_t st);
 hipError_t m1_scan_chunked(const M1Problem& p, hipStream_t st);
 // True when the fused bidirectional kernel can hold a whole row in one pass.
 bool m1_bidir_fusable(const M1Problem& p);
+// Up to four traversals of the same u/delta/z rows in one launch (m1_chunk.hip):
+// each with its own B/C (in traversal order), output, final state, direction and
+// index mode (cols: column-major over the (H, W) grid, L = H * W).
+struct M1JobSpec {
+  const float *B, *C;
+  float *out, *last;
+  int rev, cols;
+};
+bool m1_jobs_supported(const M1Problem& p, size_t H, size_t W);
+hipError_t m1_scan_jobs(const M1Problem& p, size_t H, size_t W, const M1JobSpec* spec, int n,
+                        hipStream_t st);
 hipError_t m1_bidir(const M1Problem& p, hipStream_t st);
 // (planes, H, W) -> (planes, W, H); accumulate adds into `out`.
 hipError_t transpose_hw(const float* in, float* out, long long planes, int H, int W,
                         bool accumulate, hipStream_t st);
 hipError_t scale_inplace(float* x, long long n, float scale, hipStream_t st);
 hipError_t add_inplace(float* x, const float* y, long long n, hipStream_t st);
+// x = (x + a + b + c) * scale; n % 4 == 0 and 16-byte aligned pointers
+hipError_t add3_inplace(float* x, const float* a, const float* b, const float* c, long long n,
+                        float scale, hipStream_t st);
 
 // One Mamba-3 problem: mamba3/mod.rs:47-57 plus the groups axis on q/k.
 struct M3Problem {

@@ -46,7 +46,7 @@ def test_ss2d_goldens(golden_dir):
 
 
 @pytest.mark.parametrize("shape", [(2, 16, 12, 20, 16), (1, 8, 7, 5, 13), (3, 32, 64, 64, 16),
-                                   (1, 16, 1, 33, 8)],
+                                   (1, 16, 1, 33, 8), (2, 16, 32, 16, 16), (1, 32, 16, 48, 5)],
                          ids=lambda s: "x".join(map(str, s)))
 def test_ss2d_per_direction_vs_oracle(shape):
     import armhackathon_amd as arm_scan
