@@ -255,40 +255,50 @@ int arm_scan_ss2d_f32(const ArmSS2DDims* dims, const float* u, const float* delt
   {
     armscan::M1Problem q = p;
     q.u = u; q.delta = delta; q.z = z;
-    if (armscan::m1_jobs_supported(q, H, W) && plane % 4 == 0) {
-      // One launch for the four directions: u, delta, z stay in grid layout (the
-      // column directions read them in the column index mode); only the column
-      // directions' B/C are transposed into traversal order. Direction planes go
-      // to out (merge none), or direction 0 to out and 1-3 to scratch, summed after.
+    if (armscan::m1_jobs_supported(q)) {
+      // One launch for the four directions. The column directions scan column-major
+      // copies of u, delta, z and of their B/C (one batched transpose) and write
+      // their planes column-major; the merge (or, with merge none, a second batched
+      // transpose) brings them back onto the grid.
       const bool none = merge == 0;
-      const size_t n_scratch = 4 * bcp + (none ? 0 : 3 * plane);
+      const size_t n_scratch = (z ? 3 : 2) * plane + 4 * bcp + 2 * plane + (none ? 0 : plane);
       float* scratch = nullptr;
       hipError_t e = armscan::stream_alloc((void**)&scratch, n_scratch * sizeof(float), st);
       if (e != hipSuccess) return hip_fail(e, "ss2d scratch allocation");
-      float* bT = scratch;  // b4[2], b4[3], c4[2], c4[3] in column-major order
-      float* planes = scratch + 4 * bcp;
-      auto plane_of = [&](int k) {
-        return none ? out + (size_t)k * plane : (k == 0 ? out : planes + (size_t)(k - 1) * plane);
-      };
-      const long long bn = (long long)(d.batch * d.state);
-      for (int kk = 0; kk < 2 && e == hipSuccess; ++kk) {
-        e = armscan::transpose_hw(b4 + (2 + kk) * bcp, bT + kk * bcp, bn, (int)H, (int)W, false,
-                                  st);
-        if (e == hipSuccess)
-          e = armscan::transpose_hw(c4 + (2 + kk) * bcp, bT + (2 + kk) * bcp, bn, (int)H,
-                                    (int)W, false, st);
-      }
+      float* uT = scratch;
+      float* dT = uT + plane;
+      float* zT = z ? dT + plane : nullptr;
+      float* bT = (z ? zT : dT) + plane;  // b4[2], b4[3], c4[2], c4[3] column-major
+      float* q2 = bT + 4 * bcp;           // column-forward plane (column-major)
+      float* q3 = q2 + plane;             // column-backward plane
+      float* p1 = none ? out + plane : q3 + plane;
+      const long long bd = (long long)(d.batch * d.dim), bn = (long long)(d.batch * d.state);
+      armscan::TransposeSpec tin[7] = {{u, uT, bd},
+                                       {delta, dT, bd},
+                                       {b4 + 2 * bcp, bT, bn},
+                                       {b4 + 3 * bcp, bT + bcp, bn},
+                                       {c4 + 2 * bcp, bT + 2 * bcp, bn},
+                                       {c4 + 3 * bcp, bT + 3 * bcp, bn},
+                                       {z, zT, bd}};
+      e = armscan::transpose_batch(tin, z ? 7 : 6, (int)H, (int)W, st);
       if (e == hipSuccess) {
         const armscan::M1JobSpec jobs[4] = {
-            {b4, c4, plane_of(0), last_of(0), 0, 0},
-            {b4 + bcp, c4 + bcp, plane_of(1), last_of(1), 1, 0},
-            {bT, bT + 2 * bcp, plane_of(2), last_of(2), 0, 1},
-            {bT + bcp, bT + 3 * bcp, plane_of(3), last_of(3), 1, 1}};
-        e = armscan::m1_scan_jobs(q, H, W, jobs, 4, st);
+            {u, delta, z, b4, c4, out, last_of(0), 0},
+            {u, delta, z, b4 + bcp, c4 + bcp, p1, last_of(1), 1},
+            {uT, dT, zT, bT, bT + 2 * bcp, q2, last_of(2), 0},
+            {uT, dT, zT, bT + bcp, bT + 3 * bcp, q3, last_of(3), 1}};
+        e = armscan::m1_scan_jobs(q, jobs, 4, st);
       }
-      if (e == hipSuccess && !none)
-        e = armscan::add3_inplace(out, planes, planes + plane, planes + 2 * plane,
-                                  (long long)plane, merge == 2 ? 0.25f : 1.0f, st);
+      if (e == hipSuccess) {
+        if (none) {
+          const armscan::TransposeSpec tout[2] = {{q2, out + 2 * plane, bd},
+                                                  {q3, out + 3 * plane, bd}};
+          e = armscan::transpose_batch(tout, 2, (int)W, (int)H, st);
+        } else {
+          e = armscan::merge4_transposed(out, p1, q2, q3, bd, (int)H, (int)W,
+                                         merge == 2 ? 0.25f : 1.0f, st);
+        }
+      }
       int rc = e == hipSuccess ? ARM_SCAN_OK : hip_fail(e, "ss2d launch");
       const hipError_t fe = hipFreeAsync(scratch, st);
       if (rc == ARM_SCAN_OK && fe != hipSuccess) rc = hip_fail(fe, "ss2d scratch free");

@@ -42,16 +42,14 @@ struct M1Kern {
   float *out, *last;
   long long L;
   int rows, dim, N, groups, group_size, softplus;
-  int H, W;  // grid of the column index mode (L = H * W)
 };
 
-// One traversal of a multi-direction launch: its own B/C, outputs and index mode.
-// cols: traversal index t visits the (H, W) grid in column-major order, memory
-// position (t mod H) * W + t / H, instead of position t.
+// One traversal of a multi-traversal launch: its own inputs, B/C, outputs and
+// direction (u/delta/z rows in traversal order up to the direction).
 struct M1Job {
-  const float *B, *C;
+  const float *u, *delta, *z, *B, *C;
   float *out, *last;
-  int rev, cols;
+  int rev;
 };
 constexpr int kMaxJobs = 4;
 struct M1Jobs {
@@ -186,44 +184,6 @@ __device__ __forceinline__ void store_block(float* __restrict__ row, long long L
 // The same in the column index mode: the I steps of a lane block lie in one column
 // of the grid (H % I == 0, I-aligned blocks): step i of the block is grid row
 // r0 + i (forward) or r0 - i (reverse) of column c0.
-// Byte offset of the block's lowest grid row: the block starting at traversal
-// index sb covers rows r0 .. r0+I-1 (forward) or r0-I+1 .. r0 (reverse) of one column.
-template <int I, bool REV>
-__device__ __forceinline__ unsigned col_low(long long sb, int H, int W, long long L) {
-  const unsigned m = (unsigned)(REV ? L - 1 - sb : sb);  // column-major index of step 0
-  const unsigned c0 = m / (unsigned)H;
-  const unsigned r = m - c0 * (unsigned)H - (REV ? I - 1 : 0);
-  return 4u * (r * (unsigned)W + c0);
-}
-
-// Buffer resource over a whole tensor (raw, unswizzled; reads past `bytes` return 0).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t tensor_rsrc(const float* base,
-                                                              long long bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0, (int)bytes,
-                                           0x00020000);
-}
-
-// The I steps of a block from/to the grid: one VGPR offset (the lane's row start
-// plus col_low) and a wave-uniform SGPR offset per step (step i is row i of the
-// block forward, row I-1-i reverse, W floats apart).
-template <int I, bool REV>
-__device__ __forceinline__ void load_block_cols(__amdgpu_buffer_rsrc_t r, unsigned voff, int W,
-                                                float (&v)[I]) {
-#pragma unroll
-  for (int i = 0; i < I; ++i)
-    v[i] = __builtin_bit_cast(
-        float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, (REV ? I - 1 - i : i) * W * 4, 0));
-}
-
-template <int I, bool REV>
-__device__ __forceinline__ void store_block_cols(__amdgpu_buffer_rsrc_t r, unsigned voff, int W,
-                                                 const float (&v)[I]) {
-#pragma unroll
-  for (int i = 0; i < I; ++i)
-    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v[i]), r, voff,
-                                          (REV ? I - 1 - i : i) * W * 4, 0);
-}
-
 // One state n of one chunk given this lane's B/C blocks (bb, cc): pass 1, the
 // row scan, pass 2, and the carry into the next chunk. a2 = A[d][n] log2(e).
 template <int LPR, int I>
@@ -527,10 +487,8 @@ __device__ __forceinline__ void tile_states(const float* tile, int n0, int N, in
   }
 }
 
-// The rows of block `blk` (16 per block) through one traversal. COLS: the column
-// index mode for u, delta, z and out (B and C are always in traversal order;
-// the column mode needs H % I == 0 and no tail chunk).
-template <int I, bool REV, bool COLS>
+// The rows of block `blk` (16 per block) through one traversal.
+template <int I, bool REV>
 __device__ __forceinline__ void tile_rows(const M1Kern& p, long long blk) {
   constexpr int LPR = 16, RPW = 4;
   using G = Tile<I>;
@@ -583,14 +541,8 @@ __device__ __forceinline__ void tile_rows(const M1Kern& p, long long blk) {
     float sdt = 0.0f;
     {
       float dd[I], uu[I];
-      if (COLS) {
-        const unsigned off = (unsigned)(4 * row * L) + col_low<I, REV>(sb, p.H, p.W, L);
-        load_block_cols<I, REV>(tensor_rsrc(p.delta, 4LL * p.rows * L), off, p.W, dd);
-        load_block_cols<I, REV>(tensor_rsrc(p.u, 4LL * p.rows * L), off, p.W, uu);
-      } else {
-        load_block<I, REV, true>(drow, L, sb, 0.0f, dd, L);
-        load_block<I, REV, true>(urow, L, sb, 0.0f, uu, L);
-      }
+      load_block<I, REV, true>(drow, L, sb, 0.0f, dd, L);
+      load_block<I, REV, true>(urow, L, sb, 0.0f, uu, L);
 #pragma unroll
       for (int i = 0; i < I; ++i) {
         float x = dd[i] + bias;
@@ -609,13 +561,7 @@ __device__ __forceinline__ void tile_rows(const M1Kern& p, long long blk) {
         issue_tile<I>(tiles + ((k + 1) & 1) * G::FLOATS, Bg, Cg, L, mem0(cn),
                       qn * kTileStates, N, wave, lane);
       }
-      if (zrow && q + 1 == ng) {
-        if (COLS)
-          load_block_cols<I, REV>(tensor_rsrc(p.z, 4LL * p.rows * L),
-                                  (unsigned)(4 * row * L) + col_low<I, REV>(sb, p.H, p.W, L),
-                                  p.W, zz);
-        else load_block<I, REV, true>(zrow, L, sb, 0.0f, zz, L);
-      }
+      if (zrow && q + 1 == ng) load_block<I, REV, true>(zrow, L, sb, 0.0f, zz, L);
       tile_states<I, REV>(tiles + (k & 1) * G::FLOATS, q * kTileStates, N, j, a2s, cbase,
                           carry, (last_chunk && p.last) ? p.last + row * N : nullptr, dt, du,
                           sdt, y);
@@ -625,13 +571,9 @@ __device__ __forceinline__ void tile_rows(const M1Kern& p, long long blk) {
 #pragma unroll
       for (int i = 0; i < I; ++i) y[i] *= silu_fast(zz[i]);
     }
-    if (COLS)
-      store_block_cols<I, REV>(tensor_rsrc(p.out, 4LL * p.rows * L),
-                               (unsigned)(4 * row * L) + col_low<I, REV>(sb, p.H, p.W, L), p.W,
-                               y);
-    else store_block<I, REV, true>(orow, L, sb, y, L);
+    store_block<I, REV, true>(orow, L, sb, y, L);
   }
-  if (!COLS && nfull < nch) {
+  if (nfull < nch) {
     // the row's tail chunk goes through the bounds-checked global-load path
     float dn[I], un[I];
     chunk<LPR, I, REV, true, false>(p, nfull * CH + (long long)j * I, j, true, true, row, urow,
@@ -643,13 +585,12 @@ __device__ __forceinline__ void tile_rows(const M1Kern& p, long long blk) {
 template <int I, bool REV>
 __global__ void __launch_bounds__(64 * kWavesPerBlock)
 m1_tile_kernel(M1Kern p) {
-  tile_rows<I, REV, false>(p, blockIdx.x);
+  tile_rows<I, REV>(p, blockIdx.x);
 }
 
-// Several traversals of the same rows in one launch (the directions of a 2D
-// cross-scan): every job has p.rows / 16 blocks. The blocks of the jobs that share
-// a row block sit next to each other on one XCD (block id mod 8), so u, delta and
-// z are read from HBM about once and then from that XCD's L2.
+// Several traversals of rows of the same shape in one launch (the directions of
+// a 2D cross-scan): every job has p.rows / 16 blocks, and the blocks of the jobs
+// that share a row block sit next to each other on one XCD (block id mod 8).
 template <int I>
 __global__ void __launch_bounds__(64 * kWavesPerBlock, 3)
 m1_tile_jobs_kernel(M1Kern p, M1Jobs jobs) {
@@ -659,17 +600,15 @@ m1_tile_jobs_kernel(M1Kern p, M1Jobs jobs) {
   const long long blk = (long long)(k / jobs.njobs) * 8 + xcd;
   if (blk >= jobs.blocks_per_job) return;  // whole block: no barrier is reached
   const M1Job& jb = jobs.job[ji];
+  p.u = jb.u;
+  p.delta = jb.delta;
+  p.z = jb.z;
   p.B = jb.B;
   p.C = jb.C;
   p.out = jb.out;
   p.last = jb.last;
-  if (jb.cols) {
-    if (jb.rev) tile_rows<I, true, true>(p, blk);
-    else tile_rows<I, false, true>(p, blk);
-  } else {
-    if (jb.rev) tile_rows<I, true, false>(p, blk);
-    else tile_rows<I, false, false>(p, blk);
-  }
+  if (jb.rev) tile_rows<I, true>(p, blk);
+  else tile_rows<I, false>(p, blk);
 }
 
 template <int I, bool REV>
@@ -703,32 +642,26 @@ bool aligned16(const void* q) { return q == nullptr || ((uintptr_t)q & 15u) == 0
 
 }  // namespace
 
-bool m1_jobs_supported(const M1Problem& pr, size_t H, size_t W) {
-  constexpr long long CH = Tile<M1_TILE_I>::CH;
-  return pr.len == H * W && (long long)pr.len % CH == 0 && H % M1_TILE_I == 0 &&
-         pr.batch * pr.dim * pr.len < ((size_t)1 << 29) &&  // buffer byte offsets < 2^31
-         pr.dim % 16 == 0 && pr.groups == 1 && pr.h0 == nullptr && aligned16(pr.u) &&
-         aligned16(pr.delta) && aligned16(pr.z);
+bool m1_jobs_supported(const M1Problem& pr) {
+  return pr.len % 4 == 0 && pr.dim % 16 == 0 && pr.groups == 1 && pr.h0 == nullptr;
 }
 
-hipError_t m1_scan_jobs(const M1Problem& pr, size_t H, size_t W, const M1JobSpec* spec, int n,
-                        hipStream_t st) {
-  if (n < 1 || n > kMaxJobs || !m1_jobs_supported(pr, H, W)) return hipErrorInvalidValue;
+hipError_t m1_scan_jobs(const M1Problem& pr, const M1JobSpec* spec, int n, hipStream_t st) {
+  if (n < 1 || n > kMaxJobs || !m1_jobs_supported(pr)) return hipErrorInvalidValue;
   M1Kern k{};
-  k.u = pr.u; k.delta = pr.delta; k.A = pr.A; k.D = pr.D; k.z = pr.z;
-  k.bias = pr.bias; k.h0 = nullptr;
+  k.A = pr.A; k.D = pr.D; k.bias = pr.bias; k.h0 = nullptr;
   k.L = (long long)pr.len; k.rows = (int)(pr.batch * pr.dim); k.dim = (int)pr.dim;
   k.N = (int)pr.state; k.groups = 1; k.group_size = (int)pr.dim;
   k.softplus = pr.softplus;
-  k.H = (int)H; k.W = (int)W;
   M1Jobs jobs{};
   jobs.njobs = n;
   jobs.blocks_per_job = k.rows / 16;
   for (int i = 0; i < n; ++i) {
-    if (!aligned16(spec[i].B) || !aligned16(spec[i].C) || !aligned16(spec[i].out))
+    const M1JobSpec& j = spec[i];
+    if (!aligned16(j.u) || !aligned16(j.delta) || !aligned16(j.z) || !aligned16(j.B) ||
+        !aligned16(j.C) || !aligned16(j.out))
       return hipErrorInvalidValue;
-    jobs.job[i] = M1Job{spec[i].B, spec[i].C, spec[i].out, spec[i].last, spec[i].rev,
-                        spec[i].cols};
+    jobs.job[i] = M1Job{j.u, j.delta, j.z, j.B, j.C, j.out, j.last, j.rev};
   }
   const long long blocks = 8LL * n * ((jobs.blocks_per_job + 7) / 8);
   const size_t lds =

@@ -525,6 +525,70 @@ __global__ void __launch_bounds__(256) transpose_hw_kernel(const float* __restri
   }
 }
 
+struct TransposeBatch {
+  TransposeSpec t[8];
+  long long first[9];  // first global plane of each tensor; first[n] = total
+  int n;
+};
+
+// One 32 x 32 tile of one plane per block; blockIdx.y walks the planes of all the
+// tensors (a plane is found by a short search over first[]).
+__global__ void __launch_bounds__(256) transpose_batch_kernel(TransposeBatch b, int H, int W) {
+  __shared__ float tile[32][33];
+  const int tiles_w = (W + 31) / 32;
+  const int i0 = (blockIdx.x / tiles_w) * 32, j0 = (blockIdx.x % tiles_w) * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8
+  for (long long g = blockIdx.y; g < b.first[b.n]; g += gridDim.y) {
+    int k = 0;
+    while (g >= b.first[k + 1]) ++k;
+    const long long plane = (g - b.first[k]) * H * W;
+    const float* in = b.t[k].in + plane;
+    float* out = b.t[k].out + plane;
+    for (int r = ty; r < 32; r += 8) {
+      const int i = i0 + r, j = j0 + tx;
+      if (i < H && j < W) tile[r][tx] = in[(long long)i * W + j];
+    }
+    __syncthreads();
+    for (int r = ty; r < 32; r += 8) {
+      const int j = j0 + r, i = i0 + tx;  // out is (W, H)
+      if (i < H && j < W) out[(long long)j * H + i] = tile[tx][r];
+    }
+    __syncthreads();
+  }
+}
+
+// out = scale * (out + p1 + T(q2) + T(q3)); q2, q3 are (planes, W, H).
+__global__ void __launch_bounds__(256) merge4t_kernel(float* __restrict__ out,
+                                                      const float* __restrict__ p1,
+                                                      const float* __restrict__ q2,
+                                                      const float* __restrict__ q3,
+                                                      long long planes, int H, int W,
+                                                      float scale) {
+  __shared__ float t2[32][33], t3[32][33];
+  const int tiles_w = (W + 31) / 32;
+  const int i0 = (blockIdx.x / tiles_w) * 32, j0 = (blockIdx.x % tiles_w) * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+  for (long long g = blockIdx.y; g < planes; g += gridDim.y) {
+    const long long plane = g * H * W;
+    for (int r = ty; r < 32; r += 8) {
+      const int j = j0 + r, i = i0 + tx;  // q is (W, H): rows j, columns i
+      if (i < H && j < W) {
+        t2[r][tx] = q2[plane + (long long)j * H + i];
+        t3[r][tx] = q3[plane + (long long)j * H + i];
+      }
+    }
+    __syncthreads();
+    for (int r = ty; r < 32; r += 8) {
+      const int i = i0 + r, j = j0 + tx;
+      if (i < H && j < W) {
+        const long long o = plane + (long long)i * W + j;
+        out[o] = scale * (out[o] + p1[o] + t2[tx][r] + t3[tx][r]);
+      }
+    }
+    __syncthreads();
+  }
+}
+
 __global__ void __launch_bounds__(256) scale_kernel(float* __restrict__ x, long long n,
                                                     float scale) {
   const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
@@ -700,6 +764,30 @@ hipError_t add3_inplace(float* x, const float* a, const float* b, const float* c
                      reinterpret_cast<float4*>(x), reinterpret_cast<const float4*>(a),
                      reinterpret_cast<const float4*>(b), reinterpret_cast<const float4*>(c), n4,
                      scale);
+  return hipGetLastError();
+}
+
+hipError_t transpose_batch(const TransposeSpec* spec, int n, int H, int W, hipStream_t st) {
+  if (n < 1 || n > 8) return hipErrorInvalidValue;
+  TransposeBatch b{};
+  b.n = n;
+  for (int k = 0; k < n; ++k) {
+    b.t[k] = spec[k];
+    b.first[k + 1] = b.first[k] + spec[k].planes;
+  }
+  const long long tiles = (long long)((H + 31) / 32) * ((W + 31) / 32);
+  const long long ny = b.first[n] < 65535 ? b.first[n] : 65535;
+  hipLaunchKernelGGL(transpose_batch_kernel, dim3((unsigned)tiles, (unsigned)ny), dim3(256), 0,
+                     st, b, H, W);
+  return hipGetLastError();
+}
+
+hipError_t merge4_transposed(float* out, const float* p1, const float* q2, const float* q3,
+                             long long planes, int H, int W, float scale, hipStream_t st) {
+  const long long tiles = (long long)((H + 31) / 32) * ((W + 31) / 32);
+  const long long ny = planes < 65535 ? planes : 65535;
+  hipLaunchKernelGGL(merge4t_kernel, dim3((unsigned)tiles, (unsigned)ny), dim3(256), 0, st, out,
+                     p1, q2, q3, planes, H, W, scale);
   return hipGetLastError();
 }
 

@@ -23,17 +23,27 @@ hipError_t m1_scan(const M1Problem& p, hipStream_t st);
 hipError_t m1_scan_chunked(const M1Problem& p, hipStream_t st);
 // True when the fused bidirectional kernel can hold a whole row in one pass.
 bool m1_bidir_fusable(const M1Problem& p);
-// Up to four traversals of the same u/delta/z rows in one launch (m1_chunk.hip):
-// each with its own B/C (in traversal order), output, final state, direction and
-// index mode (cols: column-major over the (H, W) grid, L = H * W).
+// Up to four traversals of rows of one shape in one launch (m1_chunk.hip), each
+// with its own u/delta/z rows, B/C, output, final state and direction; rows of
+// 4k floats, 16-byte aligned, dim % 16 == 0, one B/C group, no h0.
 struct M1JobSpec {
-  const float *B, *C;
+  const float *u, *delta, *z, *B, *C;
   float *out, *last;
-  int rev, cols;
+  int rev;
 };
-bool m1_jobs_supported(const M1Problem& p, size_t H, size_t W);
-hipError_t m1_scan_jobs(const M1Problem& p, size_t H, size_t W, const M1JobSpec* spec, int n,
-                        hipStream_t st);
+bool m1_jobs_supported(const M1Problem& p);
+hipError_t m1_scan_jobs(const M1Problem& p, const M1JobSpec* spec, int n, hipStream_t st);
+// Batched (planes, H, W) -> (planes, W, H) transposes of up to 8 tensors.
+struct TransposeSpec {
+  const float* in;
+  float* out;
+  long long planes;
+};
+hipError_t transpose_batch(const TransposeSpec* spec, int n, int H, int W, hipStream_t st);
+// out = scale * (out + p1 + T(q2) + T(q3)) over (planes, H, W), with q2/q3 given as
+// (planes, W, H): the merge of a 2D cross-scan whose column planes are transposed.
+hipError_t merge4_transposed(float* out, const float* p1, const float* q2, const float* q3,
+                             long long planes, int H, int W, float scale, hipStream_t st);
 hipError_t m1_bidir(const M1Problem& p, hipStream_t st);
 // (planes, H, W) -> (planes, W, H); accumulate adds into `out`.
 hipError_t transpose_hw(const float* in, float* out, long long planes, int H, int W,
