@@ -531,27 +531,47 @@ struct TransposeBatch {
   int n;
 };
 
-// One 32 x 32 tile of one plane per block; blockIdx.y walks the planes of all the
-// tensors (a plane is found by a short search over first[]).
+// One 64 x 64 tile of one plane per block and iteration; blockIdx.y walks the
+// planes of all the tensors (a plane is found by a short search over first[]).
+// Rows move as float4 when W (reads) and H (writes) are multiples of 4.
 __global__ void __launch_bounds__(256) transpose_batch_kernel(TransposeBatch b, int H, int W) {
-  __shared__ float tile[32][33];
-  const int tiles_w = (W + 31) / 32;
-  const int i0 = (blockIdx.x / tiles_w) * 32, j0 = (blockIdx.x % tiles_w) * 32;
-  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8
+  __shared__ float tile[64][65];
+  const int tiles_w = (W + 63) / 64;
+  const int i0 = (blockIdx.x / tiles_w) * 64, j0 = (blockIdx.x % tiles_w) * 64;
+  const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;  // 16 x 16
+  const bool vec = (W % 4 == 0) && (H % 4 == 0);
   for (long long g = blockIdx.y; g < b.first[b.n]; g += gridDim.y) {
     int k = 0;
     while (g >= b.first[k + 1]) ++k;
     const long long plane = (g - b.first[k]) * H * W;
     const float* in = b.t[k].in + plane;
     float* out = b.t[k].out + plane;
-    for (int r = ty; r < 32; r += 8) {
-      const int i = i0 + r, j = j0 + tx;
-      if (i < H && j < W) tile[r][tx] = in[(long long)i * W + j];
+    for (int r = ty; r < 64; r += 16) {
+      const int i = i0 + r, j = j0 + 4 * tx;
+      if (i >= H) continue;
+      if (vec && j + 3 < W) {
+        const float4 v = *reinterpret_cast<const float4*>(in + (long long)i * W + j);
+        tile[r][4 * tx] = v.x;
+        tile[r][4 * tx + 1] = v.y;
+        tile[r][4 * tx + 2] = v.z;
+        tile[r][4 * tx + 3] = v.w;
+      } else {
+        for (int e = 0; e < 4; ++e)
+          if (j + e < W) tile[r][4 * tx + e] = in[(long long)i * W + j + e];
+      }
     }
     __syncthreads();
-    for (int r = ty; r < 32; r += 8) {
-      const int j = j0 + r, i = i0 + tx;  // out is (W, H)
-      if (i < H && j < W) out[(long long)j * H + i] = tile[tx][r];
+    for (int r = ty; r < 64; r += 16) {
+      const int j = j0 + r, i = i0 + 4 * tx;  // out is (W, H): row j, columns i
+      if (j >= W) continue;
+      if (vec && i + 3 < H) {
+        *reinterpret_cast<float4*>(out + (long long)j * H + i) =
+            make_float4(tile[4 * tx][r], tile[4 * tx + 1][r], tile[4 * tx + 2][r],
+                        tile[4 * tx + 3][r]);
+      } else {
+        for (int e = 0; e < 4; ++e)
+          if (i + e < H) out[(long long)j * H + i + e] = tile[4 * tx + e][r];
+      }
     }
     __syncthreads();
   }
@@ -775,7 +795,7 @@ hipError_t transpose_batch(const TransposeSpec* spec, int n, int H, int W, hipSt
     b.t[k] = spec[k];
     b.first[k + 1] = b.first[k] + spec[k].planes;
   }
-  const long long tiles = (long long)((H + 31) / 32) * ((W + 31) / 32);
+  const long long tiles = (long long)((H + 63) / 64) * ((W + 63) / 64);
   const long long ny = b.first[n] < 65535 ? b.first[n] : 65535;
   hipLaunchKernelGGL(transpose_batch_kernel, dim3((unsigned)tiles, (unsigned)ny), dim3(256), 0,
                      st, b, H, W);
