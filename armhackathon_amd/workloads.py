@@ -104,3 +104,30 @@ def m1_bytes(batch, dim, length, state, groups=1, z=True, D=True, bias=False,
              + dim * ((1 if D else 0) + (1 if bias else 0))    # D, delta_bias
              + (batch * dim * state if last_state else 0))     # last_state
     return n
+
+
+def m3_bytes(x, want_state=True):
+    """Algorithmic HBM bytes of one Mamba-3 scan over the inputs `x` (SISO or
+    MIMO, from m3_siso / m3_mimo): every input read once, the output (b, l, h, dv)
+    and the final states written once, fp32."""
+    b, length, h, dv = x["v"].shape
+    dqk = x["q"].shape[-1]
+    mimo = "psi" in x
+    n = sum(v.nbytes for v in x.values())
+    n += 4 * b * length * h * dv                       # out
+    if want_state:
+        n += 4 * b * h * dv * dqk                      # last_state
+        if not mimo:
+            n += 4 * b * h * dqk                       # last_bx
+    return n
+
+
+def ss2d_bytes(x, merge="sum", last_state=True):
+    """Algorithmic HBM bytes of one four-direction SS2D scan over the inputs `x`
+    (from ss2d): every input read once, the output and final states written once."""
+    b, d, hh, ww = x["u"].shape
+    n = sum(v.nbytes for v in x.values())
+    n += 4 * b * d * hh * ww * (4 if merge == "none" else 1)
+    if last_state:
+        n += 4 * 4 * b * d * x["A"].shape[1]
+    return n

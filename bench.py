@@ -15,8 +15,13 @@ The JSON line carries:
   prefill       BASELINE config 2 end to end: Hugging Face Mamba-130M
                 architecture, random init, fp32, batch 8 x 2048 tokens, scan in
                 the HIP kernel (patched), everything else in PyTorch-ROCm;
+  other_configs BASELINE configs 3-5 (Mamba-3 SISO, MIMO, SS2D) through the
+                public API, algorithmic GB/s of one call;
   cpu_baseline  the CPU oracle (a C++ restatement of the reference's x86
                 scalar scan path) on a bounded sample of the same workload.
+
+`--workload m3_siso|m3_mimo|ss2d` times one of configs 3-5 alone (the command
+behind their rocprofv3 summaries in profiles/).
 """
 
 import argparse
@@ -43,6 +48,11 @@ def parse():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--workload", choices=("m1", "m3_siso", "m3_mimo", "ss2d"), default="m1",
+                    help="m1 (default): the headline line below; the others time one of the "
+                         "configs 3-5 alone (for profiling) and print its own line")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip timing configs 3-5 in the headline line")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain device-to-device copy of 1 GiB (the reference "
                          "kernel for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE counters)")
@@ -98,6 +108,72 @@ def bench_scan(args, dev):
     nbytes = workloads.m1_bytes(b, d, L, n, z=True, D=True, bias=True, last_state=True)
     return dict(ms_per_step=ms, wall_ms_per_step=1e3 * wall / args.steps, bytes=nbytes,
                 gbs=nbytes / (ms * 1e-3) / 1e9)
+
+
+def config_inputs(name, dev):
+    """Seeded inputs of BASELINE config 3 (m3_siso), 4 (m3_mimo) or 5 (ss2d) on dev,
+    and the config's algorithmic bytes per call."""
+    import torch
+
+    from armhackathon_amd import workloads
+
+    if name == "m3_siso":
+        x = workloads.m3_siso(seed=3)
+        nbytes = workloads.m3_bytes(x)
+    elif name == "m3_mimo":
+        x = workloads.m3_mimo(seed=4)
+        nbytes = workloads.m3_bytes(x)
+    else:
+        x = workloads.ss2d(seed=5)
+        nbytes = workloads.ss2d_bytes(x, merge="sum")
+    return {k: torch.from_numpy(v).to(dev) for k, v in x.items()}, nbytes
+
+
+CONFIG_NAMES = {
+    "m3_siso": "config 3: Mamba-3 SISO B4 L4096 24 heads x 64, dqk 128 (final states too)",
+    "m3_mimo": "config 4: Mamba-3 MIMO rank 4, B4 L4096 24 heads x 64, dqk 128 (final state)",
+    "ss2d": "config 5: SS2D 4 directions, B16 D192 64x64 N16, D, z, merge sum (final states)",
+}
+
+
+def bench_config(name, dev, steps, warmup):
+    """One config through the public Python API (what a model calls), timed with
+    HIP events on the current stream: the whole call, pre-passes included."""
+    import torch
+
+    import armhackathon_amd as arm_scan
+
+    t, nbytes = config_inputs(name, dev)
+    K = ("q", "k", "v", "adt", "dt", "trap", "q_bias", "k_bias")
+    if name == "m3_siso":
+        def call():
+            return arm_scan.mamba3_scan(*[t[k] for k in K], cos=t["cos"], sin=t["sin"],
+                                        return_last_state=True)
+    elif name == "m3_mimo":
+        def call():
+            return arm_scan.mamba3_mimo_scan(*[t[k] for k in K], t["psi"], t["zeta"], t["phi"],
+                                             cos=t["cos"], sin=t["sin"], return_last_state=True)
+    else:
+        def call():
+            return arm_scan.ss2d_scan(t["u"], t["delta"], t["A"], t["B4"], t["C4"], D=t["D"],
+                                      z=t["z"], delta_softplus=False, merge="sum",
+                                      per_direction=True, return_last_state=True)
+    for _ in range(warmup):
+        call()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(steps):
+        call()
+    stop.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(stop) / steps
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    del t
+    torch.cuda.empty_cache()
+    return dict(workload=CONFIG_NAMES[name], ms_per_call=round(ms, 4), bytes_per_call=nbytes,
+                gbs=round(gbs, 2), frac_of_8tbs=round(gbs / HBM_PEAK_GBS, 4), steps=steps)
 
 
 def bench_prefill(args, dev):
@@ -198,8 +274,17 @@ def main():
         print(json.dumps({"copy_calibration_bytes": src.numel() * 4}), flush=True)
         return
     _ffi.load()
+    if args.workload != "m1":
+        r = bench_config(args.workload, dev, args.steps, args.warmup)
+        print(json.dumps({"metric": "algorithmic GB/s of one call", "value": r["gbs"],
+                          "unit": "GB/s", "n_gpus": 1, "dtype": "f32", "data": "synthetic",
+                          "config": {"workload": r["workload"]}, "detail": r}), flush=True)
+        return
     r = bench_scan(args, dev)
     prefill = None if args.no_prefill else bench_prefill(args, dev)
+    configs = None if args.no_configs else {
+        name: bench_config(name, dev, steps, 1)
+        for name, steps in (("m3_siso", 5), ("m3_mimo", 3), ("ss2d", 10))}
     cpu = None if args.no_cpu else bench_cpu(args.cpu_seconds)
     achieved = r["gbs"]
     line = {
@@ -223,6 +308,7 @@ def main():
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic_from_profiles()},
         "prefill": prefill,
+        "other_configs": configs,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
