@@ -287,10 +287,13 @@ __device__ __forceinline__ void dma_plan(const M3K& p, const SeqIn& s, int first
   }
 }
 
-__device__ __forceinline__ void dma_fast(const DmaPlan& d, int ch, float* stage) {
+// Instructions k0 .. k1-1 of the plan (a wave spreads a stage over its iteration so
+// that the block's DMA does not reach the address unit in one burst).
+__device__ __forceinline__ void dma_fast(const DmaPlan& d, int ch, float* stage, int k0 = 0,
+                                         int k1 = kMaxDma) {
 #pragma unroll
   for (int k = 0; k < kMaxDma; ++k)
-    if (k < d.count && d.on[k])
+    if (k >= k0 && k < k1 && k < d.count && d.on[k])
       dma16(d.base[k] + ((long long)ch * d.delta[k] + d.off[k]), stage + d.ins[k] * 256);
 }
 
@@ -318,6 +321,14 @@ __device__ __forceinline__ void dma_stage(const M3K& p, const SeqIn& s, const Dm
                                           float* stage, int lane) {
   if ((ch + 1) * p.steps_per_chunk <= p.len) dma_fast(d, ch, stage);
   else dma_clamped<R, REV>(p, s, d, ch, stage, lane);
+}
+
+// Part k0 .. k1-1 of dma_stage; the partial, last chunk goes whole with part 0.
+template <int R, bool REV>
+__device__ __forceinline__ void dma_stage_part(const M3K& p, const SeqIn& s, const DmaPlan& d,
+                                               int ch, float* stage, int lane, int k0, int k1) {
+  if ((ch + 1) * p.steps_per_chunk <= p.len) dma_fast(d, ch, stage, k0, k1);
+  else if (k0 == 0) dma_clamped<R, REV>(p, s, d, ch, stage, lane);
 }
 
 // Rotated q/k from the raw columns: SISO rotates interleaved pairs (2u, 2u+1)
@@ -515,9 +526,10 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 2)) m3_chunk_kernel(M3K p) {
     const int later = (ch + NS - 2 < p.nchunks - 1 ? ch + NS - 2 : p.nchunks - 1) - ch;
     wait_vm_at_most(later * dp.count);
     lds_barrier();
-    if (ch + NS - 1 < p.nchunks)
-      dma_stage<R, REV>(p, in, dp, ch + NS - 1, stages + ((ch + NS - 1) % NS) * p.stage_floats,
-                        lane);
+    // this iteration's DMA, one instruction per phase
+    const bool dma_now = ch + NS - 1 < p.nchunks;
+    float* dstage = stages + ((ch + NS - 1) % NS) * p.stage_floats;
+    if (dma_now) dma_stage_part<R, REV>(p, in, dp, ch + NS - 1, dstage, lane, 0, 1);
 
     const float* sg = stages + (ch % NS) * p.stage_floats;
     // ---- rotated q/k rows of this n-tile
@@ -540,6 +552,7 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 2)) m3_chunk_kernel(M3K p) {
     const f4 qr = rope<MIMO>(q, qp, bq, bqp, cs, sn, lo);
     const f4 kr = rope<MIMO>(k, kp, bk, bkp, cs, sn, lo);
     kr_last = kr;
+    if (dma_now) dma_stage_part<R, REV>(p, in, dp, ch + NS - 1, dstage, lane, 1, 2);
     // ---- partial G^T, and partial Q S0^T per slice
     {
       f4 gp = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -547,6 +560,7 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 2)) m3_chunk_kernel(M3K p) {
       for (int r = 0; r < 4; ++r) gp = mfma(kr[r], qr[r], gp);
       *reinterpret_cast<f4*>(gbuf + (ch & 1) * kMaxWaves * 256 + (nt * 64 + lane) * 4) = gp;
     }
+    if (dma_now) dma_stage_part<R, REV>(p, in, dp, ch + NS - 1, dstage, lane, 2, 3);
 #pragma unroll
     for (int j = 0; j < PT; ++j) {
       f4 yp = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -555,6 +569,7 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 2)) m3_chunk_kernel(M3K p) {
       *reinterpret_cast<f4*>(ybuf + (((ch & 1) * PT + j) * kMaxWaves + nt) * 256 + lane * 4) =
           yp;
     }
+    if (dma_now) dma_stage_part<R, REV>(p, in, dp, ch + NS - 1, dstage, lane, 3, 4);
     // ---- K transpose, then S = e^{c_last} S + K^T diag(w) X per slice
     *reinterpret_cast<f4*>(kt + li * kKtStride + 4 * lj) = kr;
     float kc[4];
@@ -572,6 +587,7 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 2)) m3_chunk_kernel(M3K p) {
       }
       S[j] = acc;
     }
+    if (dma_now) dma_stage_part<R, REV>(p, in, dp, ch + NS - 1, dstage, lane, 4, kMaxDma);
   }
   lds_barrier();
 
