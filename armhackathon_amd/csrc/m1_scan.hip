@@ -1,26 +1,27 @@
-// Mamba-1 selective scan on MI355X (gfx950).
+// Mamba-1 on MI355X (gfx950): the fused bidirectional scan for rows that fit one
+// on-chip pass, the grid helpers of the 2D cross-scan, and the dispatch of the
+// single-direction scan (whose kernels are in m1_chunk.hip).
 //
 // Semantics are the reference's scalar::scan (kernel/arm-scan-core/src/scalar.rs:11-89)
 // and scalar::scan_bidirectional (scalar.rs:114-201):
 //   h_n <- exp(dt*A_dn) h_n + dt*u*B_gn ;  y = sum_n C_gn h_n ; (y + D u) silu(z)
 // with dt = softplus(delta + bias) when asked, reverse as an index mode.
 //
-// Work decomposition (one workgroup = R channel rows x S time segments, one
-// wave per (row, segment)):
-//   * a lane owns I consecutive timesteps ("items") of one row; a wave covers
-//     64*I steps, a row-chunk CH = S*64*I steps; longer rows loop over chunks
-//     with the per-state carry kept in LDS;
-//   * per state n: each lane discretises its items (a = 2^(dt*A*log2e),
-//     b = dt*u*B), folds them into one affine map, the wave combines the maps
-//     with a DPP Hillis-Steele scan, segments combine through LDS, then each
-//     lane replays its items from the resulting h_in accumulating y += C*h.
-//     exp(dt*A) is evaluated exactly once per (item, state);
-//   * B/C rows of the current state are shared by the R rows of the
-//     workgroup (same batch and group): staged once into LDS, triple-buffered
-//     so one barrier per state suffices, and read back as 16-byte vectors with
-//     a 4-float pad per lane block (bank-conflict free);
-//   * u, delta, z, out move with 16-byte vector loads/stores straight between
-//     HBM and registers (each lane's block is one 128-B line at I = 32).
+// Fused bidirectional kernel (one workgroup = R channel rows x S time segments,
+// one wave per (row, segment), the whole row in one chunk):
+//   * a lane owns I consecutive timesteps ("items") of one row;
+//   * per state n: each lane discretises its items once (a = 2^(dt*A*log2e),
+//     b = dt*u*B) and the forward and the reverse pass share them: each folds
+//     the items into one affine map, the wave combines the maps with a DPP
+//     Hillis-Steele scan, segments combine through LDS, then each lane replays
+//     its items accumulating y += C*h. exp(dt*A) is evaluated once per (item,
+//     state) for both directions;
+//   * B/C rows of the current state are shared by the R rows of the workgroup
+//     (same batch and group): staged into LDS, triple-buffered so one barrier per
+//     state suffices, read back as 16-byte vectors with a 4-float pad per lane
+//     block (bank-conflict free);
+//   * u, delta, z, out move with 16-byte vector loads/stores between HBM and
+//     registers.
 
 #include <hip/hip_runtime.h>
 
@@ -179,152 +180,6 @@ __device__ __forceinline__ void epilogue(const M1Args& p, const float* urow, con
     load_items<I>(zrow, p.L, sb, reverse, p.vec, 0.0f, zz);
 #pragma unroll
     for (int i = 0; i < I; ++i) y[i] = y[i] * silu(zz[i]);
-  }
-}
-
-// ---------------------------------------------------------------------------
-// Single-direction scan (forward or reverse index mode), any L.
-// LDS: B and C triple buffers [3][CHP] each, segment aggregates [2][R*S][2],
-// per-wave carries [R*S][N].
-template <int I, int MAXT>
-__global__ void __launch_bounds__(MAXT) m1_scan_kernel(M1Args p) {
-  constexpr int R = I / 4;
-  constexpr int LB = I + kPad;
-  extern __shared__ float smem[];
-  const int S = p.S;
-  const int CH = S * 64 * I;
-  const int CHP = S * 64 * LB;
-  float* sB = smem;
-  float* sC = smem + 3 * CHP;
-  float* sAgg = smem + 6 * CHP;
-  float* sCarry = sAgg + 4 * R * S;
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int r = w / S, s = w - r * S;
-  const int wg_per_batch = p.dim / R;
-  const int bi = blockIdx.x / wg_per_batch;
-  const int d = (blockIdx.x - bi * wg_per_batch) * R + r;
-  const int g = ((blockIdx.x - bi * wg_per_batch) * R) / p.group_size;
-  const long long L = p.L;
-  const int N = p.N;
-  const bool rev = p.reverse != 0;
-  const long long row = (long long)bi * p.dim + d;
-  const float* urow = p.u + row * L;
-  const float* drow = p.delta + row * L;
-  const float* zrow = p.z ? p.z + row * L : nullptr;
-  float* orow = p.out + row * L;
-  const float* Bgrp = p.B + ((long long)bi * p.groups + g) * N * L;
-  const float* Cgrp = p.C + ((long long)bi * p.groups + g) * N * L;
-  const float* Arow = p.A + (long long)d * N;
-  const float bias = p.bias ? p.bias[d] : 0.0f;
-  const float dskip = p.D ? p.D[d] : 0.0f;
-
-  for (int n = lane; n < N; n += 64) sCarry[w * N + n] = p.h0 ? p.h0[row * N + n] : 0.0f;
-
-  const long long nchunks = (L + CH - 1) / CH;
-  // staging geometry: thread `tid` moves memory positions tbase + 4 tid .. +3
-  auto tbase_of = [&](long long c) { return rev ? (L - (c + 1) * CH) : c * CH; };
-  auto qpos = [&](void) { return rev ? (CH - 4 - 4 * tid) : 4 * tid; };
-  auto stage_store = [&](int buf, float4 vb, float4 vc) {
-    const int q0 = lds_pos<I>(qpos());
-    if (rev) {
-      vb = make_float4(vb.w, vb.z, vb.y, vb.x);
-      vc = make_float4(vc.w, vc.z, vc.y, vc.x);
-    }
-    *reinterpret_cast<float4*>(sB + buf * CHP + q0) = vb;
-    *reinterpret_cast<float4*>(sC + buf * CHP + q0) = vc;
-  };
-  {
-    const long long t0 = tbase_of(0) + 4 * tid;
-    stage_store(0, load4(Bgrp, t0, L, p.vec), load4(Cgrp, t0, L, p.vec));
-  }
-  __syncthreads();
-
-  int k = 0;  // (chunk, state) step counter: LDS buffer k % 3, aggregate slot k & 1
-  for (long long c = 0; c < nchunks; ++c) {
-    const long long sb = c * CH + (long long)(s * 64 + lane) * I;
-    float dt[I], du[I], y[I];
-    float sumdt;
-    discretize<I>(p, urow, drow, sb, rev, bias, dt, du, sumdt);
-#pragma unroll
-    for (int i = 0; i < I; ++i) y[i] = 0.0f;
-
-    for (int n = 0; n < N; ++n, ++k) {
-      // prefetch B/C of the next (chunk, state) step into registers
-      const bool has_next = (n + 1 < N) || (c + 1 < nchunks);
-      const int nn = (n + 1 < N) ? n + 1 : 0;
-      const long long cn = (n + 1 < N) ? c : c + 1;
-      float4 nb = make_float4(0.f, 0.f, 0.f, 0.f), nc = nb;
-      if (has_next) {
-        const long long t0 = tbase_of(cn) + 4 * tid;
-        nb = load4(Bgrp + (long long)nn * L, t0, L, p.vec);
-        nc = load4(Cgrp + (long long)nn * L, t0, L, p.vec);
-      }
-      const int buf = k % 3;
-      const float a2 = Arow[n] * kLog2e;
-      const float* lb = sB + buf * CHP + (s * 64 + lane) * LB;
-      float a[I], b[I];
-      float bt = 0.0f;
-#pragma unroll
-      for (int q = 0; q < I / 4; ++q) {
-        const float4 bv = *reinterpret_cast<const float4*>(lb + 4 * q);
-        const float bb[4] = {bv.x, bv.y, bv.z, bv.w};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int i = 4 * q + j;
-          a[i] = ex2(dt[i] * a2);
-          b[i] = du[i] * bb[j];
-          bt = fmaf(a[i], bt, b[i]);
-        }
-      }
-      float ai = ex2(a2 * sumdt), bi_ = bt;
-      wave_scan_up(ai, bi_);
-      const float ae = dpp<kWaveShr1, 0xF>(1.0f, ai);
-      const float be = dpp<kWaveShr1, 0xF>(0.0f, bi_);
-      const float aw = readlane(ai, 63), bw = readlane(bi_, 63);
-      if (S > 1 && lane == 0) {
-        sAgg[((k & 1) * R * S + w) * 2 + 0] = aw;
-        sAgg[((k & 1) * R * S + w) * 2 + 1] = bw;
-      }
-      if (has_next) stage_store((k + 1) % 3, nb, nc);
-      __syncthreads();
-      const float hc = sCarry[w * N + n];
-      float hseg = hc, hnew;
-      if (S > 1) {
-        const float* ag = sAgg + ((k & 1) * R * S + r * S) * 2;
-        float fa = 1.0f, fb = 0.0f;
-        for (int j = 0; j < S; ++j) {
-          if (j == s) hseg = fmaf(fa, hc, fb);
-          const float ja = ag[2 * j], jb = ag[2 * j + 1];
-          fb = fmaf(ja, fb, jb);
-          fa = fa * ja;
-        }
-        hnew = fmaf(fa, hc, fb);
-      } else {
-        hnew = fmaf(aw, hc, bw);
-      }
-      float h = fmaf(ae, hseg, be);
-      const float* lc = sC + buf * CHP + (s * 64 + lane) * LB;
-#pragma unroll
-      for (int q = 0; q < I / 4; ++q) {
-        const float4 cv = *reinterpret_cast<const float4*>(lc + 4 * q);
-        const float cc[4] = {cv.x, cv.y, cv.z, cv.w};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int i = 4 * q + j;
-          h = fmaf(a[i], h, b[i]);
-          y[i] = fmaf(cc[j], h, y[i]);
-        }
-      }
-      if (lane == 0) sCarry[w * N + n] = hnew;
-    }
-    epilogue<I>(p, urow, zrow, sb, rev, dskip, y);
-    store_items<I>(orow, L, sb, rev, p.vec, y);
-  }
-  if (p.last && s == 0) {
-    for (int n = lane; n < N; n += 64) p.last[row * N + n] = sCarry[w * N + n];
   }
 }
 
@@ -615,21 +470,6 @@ __global__ void __launch_bounds__(256) scale_kernel(float* __restrict__ x, long 
   if (i < n) x[i] *= scale;
 }
 
-// x = (x + a + b + c) * scale over n floats, 4 per lane (n % 4 == 0, 16-byte
-// aligned): the merge of a 2D cross-scan's four direction planes.
-__global__ void __launch_bounds__(256) add3_kernel(float4* __restrict__ x,
-                                                   const float4* __restrict__ a,
-                                                   const float4* __restrict__ b,
-                                                   const float4* __restrict__ c, long long n4,
-                                                   float scale) {
-  for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n4;
-       i += (long long)gridDim.x * 256) {
-    const float4 p = x[i], q = a[i], r = b[i], t = c[i];
-    x[i] = make_float4((p.x + q.x + r.x + t.x) * scale, (p.y + q.y + r.y + t.y) * scale,
-                       (p.z + q.z + r.z + t.z) * scale, (p.w + q.w + r.w + t.w) * scale);
-  }
-}
-
 __global__ void __launch_bounds__(256) add_kernel(float* __restrict__ x,
                                                   const float* __restrict__ y, long long n) {
   const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
@@ -672,19 +512,6 @@ Choice choose(long long rows, long long L, long long group_size, bool single_chu
 }
 
 template <int I, int MAXT>
-hipError_t launch_fwd(const M1Args& a, int S, long long rows, hipStream_t st) {
-  const int R = I / 4;
-  const int threads = 64 * R * S;
-  const size_t lds =
-      sizeof(float) * ((size_t)6 * S * 64 * (I + kPad) + 4 * R * S + (size_t)R * S * a.N);
-  const long long blocks = rows / R;
-  if (threads > MAXT) return hipErrorInvalidConfiguration;
-  hipLaunchKernelGGL((m1_scan_kernel<I, MAXT>), dim3((unsigned)blocks), dim3(threads), lds, st,
-                     a);
-  return hipGetLastError();
-}
-
-template <int I, int MAXT>
 hipError_t launch_bidir(const M1Args& a, int S, long long rows, hipStream_t st) {
   const int R = I / 4;
   const int threads = 64 * R * S;
@@ -718,21 +545,6 @@ static void fill_args(M1Args& a, const M1Problem& pr) {
 
 hipError_t m1_scan(const M1Problem& pr, hipStream_t st) {
   return m1_scan_chunked(pr, st);
-}
-
-hipError_t m1_scan_lds(const M1Problem& pr, hipStream_t st) {
-  M1Args a{};
-  fill_args(a, pr);
-  const long long rows = (long long)pr.batch * pr.dim;
-  const Choice c = choose(rows, (long long)pr.len, (long long)(pr.dim / pr.groups), false);
-  a.S = c.S;
-  switch (c.I) {
-    case 32: return launch_fwd<32, 512>(a, c.S, rows, st);
-    case 16: return launch_fwd<16, 1024>(a, c.S, rows, st);
-    case 8: return launch_fwd<8, 1024>(a, c.S, rows, st);
-    case 4: return launch_fwd<4, 1024>(a, c.S, rows, st);
-    default: return hipErrorInvalidConfiguration;
-  }
 }
 
 bool m1_bidir_fusable(const M1Problem& pr) {
@@ -773,17 +585,6 @@ hipError_t transpose_hw(const float* in, float* out, long long planes, int H, in
 hipError_t add_inplace(float* x, const float* y, long long n, hipStream_t st) {
   const long long blocks = (n + 255) / 256;
   hipLaunchKernelGGL(add_kernel, dim3((unsigned)blocks), dim3(256), 0, st, x, y, n);
-  return hipGetLastError();
-}
-
-hipError_t add3_inplace(float* x, const float* a, const float* b, const float* c, long long n,
-                        float scale, hipStream_t st) {
-  const long long n4 = n / 4;
-  const long long blocks = (n4 + 255) / 256 < 8192 ? (n4 + 255) / 256 : 8192;
-  hipLaunchKernelGGL(add3_kernel, dim3((unsigned)blocks), dim3(256), 0, st,
-                     reinterpret_cast<float4*>(x), reinterpret_cast<const float4*>(a),
-                     reinterpret_cast<const float4*>(b), reinterpret_cast<const float4*>(c), n4,
-                     scale);
   return hipGetLastError();
 }
 

@@ -50,9 +50,7 @@ hipError_t transpose_hw(const float* in, float* out, long long planes, int H, in
                         bool accumulate, hipStream_t st);
 hipError_t scale_inplace(float* x, long long n, float scale, hipStream_t st);
 hipError_t add_inplace(float* x, const float* y, long long n, hipStream_t st);
-// x = (x + a + b + c) * scale; n % 4 == 0 and 16-byte aligned pointers
-hipError_t add3_inplace(float* x, const float* a, const float* b, const float* c, long long n,
-                        float scale, hipStream_t st);
+
 
 // One Mamba-3 problem: mamba3/mod.rs:47-57 plus the groups axis on q/k.
 struct M3Problem {
