@@ -16,7 +16,8 @@ The JSON line carries:
                 architecture, random init, fp32, batch 8 x 2048 tokens, scan in
                 the HIP kernel (patched), everything else in PyTorch-ROCm;
   other_configs BASELINE configs 3-5 (Mamba-3 SISO, MIMO, SS2D) through the
-                public API, algorithmic GB/s of one call;
+                public API, algorithmic GB/s of one call, each with the CPU
+                oracle timed on a bounded sample of it;
   cpu_baseline  the CPU oracle (a C++ restatement of the reference's x86
                 scalar scan path) on a bounded sample of the same workload.
 
@@ -176,6 +177,50 @@ def bench_config(name, dev, steps, warmup):
                 gbs=round(gbs, 2), frac_of_8tbs=round(gbs / HBM_PEAK_GBS, 4), steps=steps)
 
 
+def bench_config_cpu(name, seconds):
+    """The C++ restatement of the reference's x86 path on host cores for one of
+    configs 3-5, over a bounded sample of the config (batch 1 of 4 for Mamba-3,
+    2 of 16 for SS2D), repeated until `seconds` of wall time have passed."""
+    import numpy as np
+
+    import oracle
+    from armhackathon_amd import workloads
+
+    threads = min(16, os.cpu_count() or 1)
+    oracle.set_threads(threads)
+    K = ("q", "k", "v", "adt", "dt", "trap", "q_bias", "k_bias")
+    if name == "m3_siso":
+        x = workloads.m3_siso(batch=1, seed=3)
+        nbytes, sample = workloads.m3_bytes(x), "batch 1 of config 3"
+
+        def call():
+            oracle.mamba3_scan(*[x[k] for k in K], x["cos"], x["sin"], want_state=True)
+    elif name == "m3_mimo":
+        x = workloads.m3_mimo(batch=1, seed=4)
+        nbytes, sample = workloads.m3_bytes(x), "batch 1 of config 4"
+
+        def call():
+            oracle.mamba3_scan(*[x[k] for k in K], x["cos"], x["sin"], psi=x["psi"],
+                               zeta=x["zeta"], phi=x["phi"], want_state=True)
+    else:
+        x = workloads.ss2d(batch=2, seed=5)
+        nbytes, sample = workloads.ss2d_bytes(x, merge="sum"), "batch 2 of config 5"
+
+        def call():
+            planes, _ = oracle.ss2d(x["u"], x["delta"], x["A"], x["B4"], x["C4"], D=x["D"],
+                                    z=x["z"], want_state=True)
+            planes.sum(axis=0)
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        call()
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or reps >= 50:
+            break
+    return dict(value=round(nbytes * reps / el / 1e9, 3), unit="GB/s", cores=threads,
+                kind="port", sample=f"{reps} passes of {sample} in {el:.1f} s, {threads} threads")
+
+
 def bench_prefill(args, dev):
     """random-init Mamba-130M architecture, batch 8 x 2048."""
     import torch
@@ -286,6 +331,9 @@ def main():
         name: bench_config(name, dev, steps, 1)
         for name, steps in (("m3_siso", 5), ("m3_mimo", 3), ("ss2d", 10))}
     cpu = None if args.no_cpu else bench_cpu(args.cpu_seconds)
+    if configs is not None and not args.no_cpu:
+        for name in configs:
+            configs[name]["cpu_baseline"] = bench_config_cpu(name, args.cpu_seconds / 4)
     achieved = r["gbs"]
     line = {
         "metric": METRIC,
