@@ -27,9 +27,9 @@
 //    D x, gating, rank sum, store.
 //
 // Every input of a chunk (q, k, cos, sin, v and z rows and the gate record)
-// reaches LDS by direct-to-LDS DMA (global_load_lds_dwordx4) two chunks ahead,
-// through a ring of three stages: no VGPRs are spent on staging and HBM latency
-// stays off the chunk loop. Each wave waits with an explicit vmcnt for its own
+// reaches LDS by direct-to-LDS DMA (global_load_lds_dwordx4) NS-1 chunks ahead,
+// through a ring of NS stages (as many as fit in LDS, at most kStages): no VGPRs
+// are spent on staging and HBM latency stays off the chunk loop. Each wave waits with an explicit vmcnt for its own
 // share of a stage, and a workgroup barrier publishes the stage. Rows of the last
 // chunk past the end of the sequence are clamped to the last step on load (their
 // gates are zero, so they add nothing) and are not stored.
@@ -66,7 +66,7 @@ constexpr int kRecPieces = kRecFloats / 4;
 
 constexpr int kMaxWaves = 8;   // n-tiles per block: dqk <= 128
 constexpr int kKtStride = 20;  // floats per row of a wave's K transpose tile
-constexpr int kStages = 3;
+constexpr int kStages = 4;   // deepest DMA ring
 constexpr size_t kLdsBudget = 160 * 1024;
 
 struct M3K {

@@ -43,8 +43,8 @@ SHAPE = dict(batch=8, dim=1536, length=2048, state=16)
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--prefill-steps", type=int, default=3)
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
@@ -328,8 +328,8 @@ def main():
     r = bench_scan(args, dev)
     prefill = None if args.no_prefill else bench_prefill(args, dev)
     configs = None if args.no_configs else {
-        name: bench_config(name, dev, steps, 1)
-        for name, steps in (("m3_siso", 5), ("m3_mimo", 3), ("ss2d", 10))}
+        name: bench_config(name, dev, steps, 10)
+        for name, steps in (("m3_siso", 100), ("m3_mimo", 40), ("ss2d", 100))}
     cpu = None if args.no_cpu else bench_cpu(args.cpu_seconds)
     if configs is not None and not args.no_cpu:
         for name in configs:
