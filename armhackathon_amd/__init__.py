@@ -22,6 +22,7 @@ __all__ = [
     "lib_path",
     "selective_scan",
     "selective_scan_bidirectional",
+    "selective_scan_time_major",
     "bidirectional_scan",
     "ss2d_scan",
     "use_arm_scan",
@@ -40,6 +41,7 @@ __all__ = [
 _LAZY = {
     "selective_scan": ".op",
     "selective_scan_bidirectional": ".op",
+    "selective_scan_time_major": ".op",
     "kernel_calls": ".op",
     "bidirectional_scan": ".bidirectional",
     "ss2d_scan": ".ss2d",

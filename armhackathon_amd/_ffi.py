@@ -91,6 +91,15 @@ def _declare(lib):
                   _ci, _ci, _ci, _ci,    # delta_softplus reverse backend threading
                   _vp, _vp, _vp,         # out last_state h0
                   _vp]                   # stream
+    f = lib.arm_scan_selective_scan_strided_f32
+    f.restype = _ci
+    f.argtypes = [ctypes.POINTER(ArmScanDims),
+                  *([_vp] * 7),          # u delta a b c d_skip z
+                  _vp, _vp,              # z_strides delta_bias
+                  _ci, _ci,              # delta_softplus reverse
+                  _vp, _vp,              # out out_strides
+                  _vp, _vp,              # last_state h0
+                  _vp]                   # stream
     f = lib.arm_scan_selective_scan_bidirectional_f32
     f.restype = _ci
     f.argtypes = [ctypes.POINTER(ArmScanDims),
@@ -168,6 +177,21 @@ def scan_raw(dims, ptr_u, ptr_delta, ptr_a, ptr_b, ptr_c, ptr_d_skip, ptr_z,
         BACKENDS[backend], THREADING[threading], ptr_out, _p(ptr_last), _p(ptr_h0),
         _p(stream))
     _check("arm_scan_selective_scan_f32", code)
+
+
+def scan_strided_raw(dims, ptr_u, ptr_delta, ptr_a, ptr_b, ptr_c, ptr_d_skip, ptr_z,
+                     z_strides, ptr_delta_bias, delta_softplus, ptr_out, out_strides,
+                     ptr_last=0, ptr_h0=0, *, reverse=False, stream=0):
+    """Call arm_scan_selective_scan_strided_f32: z and out given by element
+    strides (batch, dim, step); None = contiguous (batch, dim, len)."""
+    def arr(s):
+        return None if s is None else (ctypes.c_longlong * 3)(*[int(x) for x in s])
+    zs, os_ = arr(z_strides), arr(out_strides)
+    code = load().arm_scan_selective_scan_strided_f32(
+        ctypes.byref(dims), ptr_u, ptr_delta, ptr_a, ptr_b, ptr_c, _p(ptr_d_skip), _p(ptr_z),
+        zs, _p(ptr_delta_bias), int(bool(delta_softplus)), int(bool(reverse)), ptr_out, os_,
+        _p(ptr_last), _p(ptr_h0), _p(stream))
+    _check("arm_scan_selective_scan_strided_f32", code)
 
 
 def scan_bidir_raw(dims, ptr_u, ptr_delta, ptr_a, ptr_b, ptr_c, ptr_d_skip, ptr_z,

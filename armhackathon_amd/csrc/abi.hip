@@ -124,6 +124,32 @@ int arm_scan_selective_scan_f32(const ArmScanDims* dims, const float* u, const f
   return run(armscan::m1_scan(p, (hipStream_t)stream), "selective_scan launch");
 }
 
+int arm_scan_selective_scan_strided_f32(const ArmScanDims* dims, const float* u,
+                                        const float* delta, const float* a, const float* b,
+                                        const float* c, const float* d_skip, const float* z,
+                                        const long long* z_strides, const float* delta_bias,
+                                        int delta_softplus, int reverse, float* out,
+                                        const long long* out_strides, float* last_state,
+                                        const float* h0, void* stream) {
+  if (!dims || !u || !delta || !a || !b || !c || !out)
+    return fail(ARM_SCAN_ERR_NULL_POINTER, "a required pointer is null");
+  if (int rc = check_m1_dims(*dims)) return rc;
+  armscan::M1Problem p{};
+  p.batch = dims->batch; p.dim = dims->dim; p.len = dims->len; p.state = dims->state;
+  p.groups = dims->groups;
+  p.u = u; p.delta = delta; p.A = a; p.B = b; p.C = c; p.D = d_skip; p.z = z;
+  p.bias = delta_bias; p.h0 = h0; p.out = out; p.last = last_state;
+  p.softplus = delta_softplus != 0; p.reverse = reverse != 0;
+  for (int i = 0; i < 3; ++i) {
+    p.z_stride[i] = z_strides ? z_strides[i] : 0;
+    p.out_stride[i] = out_strides ? out_strides[i] : 0;
+  }
+  const char* why = nullptr;
+  if (armscan::m1_strided_io(p) && !armscan::m1_strided_supported(p, &why))
+    return fail(ARM_SCAN_ERR_INVALID_DIMS, "%s", why);
+  return run(armscan::m1_scan(p, (hipStream_t)stream), "selective_scan (strided) launch");
+}
+
 int arm_scan_selective_scan_bidirectional_f32(
     const ArmScanDims* dims, const float* u, const float* delta, const float* a,
     const float* b, const float* c, const float* d_skip, const float* z,

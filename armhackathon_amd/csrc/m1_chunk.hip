@@ -42,6 +42,11 @@ struct M1Kern {
   float *out, *last;
   long long L;
   int rows, dim, N, groups, group_size, softplus;
+  // strided z/out (m1_tile_kernel<.., true>): element strides per batch, channel and
+  // step, and the bytes of one batch's slab (every offset inside it fits 32 bits)
+  long long zs_b, zs_d, zs_t, os_b, os_d, os_t;
+  unsigned z_bytes, o_bytes;
+  int z_dma;  // strided z and out staged through LDS (m1_tile_kernel<.., 2>)
 };
 
 // One traversal of a multi-traversal launch: its own inputs, B/C, outputs and
@@ -139,7 +144,7 @@ template <> struct Row<64> {
 template <int I, bool REV, bool VEC>
 __device__ __forceinline__ void load_block(const float* __restrict__ row, long long Lv,
                                            long long sb, float fill, float (&v)[I],
-                                           long long L) {
+                                           long long L, long long ts = 1) {
   if (VEC) {
     const long long mb = REV ? L - sb - I : sb;
     const float4* p = reinterpret_cast<const float4*>(row + mb);
@@ -154,14 +159,14 @@ __device__ __forceinline__ void load_block(const float* __restrict__ row, long l
 #pragma unroll
     for (int i = 0; i < I; ++i) {
       const long long s = sb + i;
-      v[i] = s < Lv ? row[REV ? L - 1 - s : s] : fill;
+      v[i] = s < Lv ? row[(REV ? L - 1 - s : s) * ts] : fill;
     }
   }
 }
 
 template <int I, bool REV, bool VEC>
 __device__ __forceinline__ void store_block(float* __restrict__ row, long long Lv, long long sb,
-                                            const float (&v)[I], long long L) {
+                                            const float (&v)[I], long long L, long long ts = 1) {
   if (VEC) {
     const long long mb = REV ? L - sb - I : sb;
     float4* p = reinterpret_cast<float4*>(row + mb);
@@ -176,14 +181,40 @@ __device__ __forceinline__ void store_block(float* __restrict__ row, long long L
 #pragma unroll
     for (int i = 0; i < I; ++i) {
       const long long s = sb + i;
-      if (s < Lv) row[REV ? L - 1 - s : s] = v[i];
+      if (s < Lv) row[(REV ? L - 1 - s : s) * ts] = v[i];
     }
   }
 }
 
-// The same in the column index mode: the I steps of a lane block lie in one column
-// of the grid (H % I == 0, I-aligned blocks): step i of the block is grid row
-// r0 + i (forward) or r0 - i (reverse) of column c0.
+// Buffer resource over one batch's slab of a strided tensor (raw, unswizzled;
+// reads past `bytes` return 0).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t slab_rsrc(const float* base, unsigned bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+
+// The I steps of a lane block of a strided row (steps `ts` floats apart, e.g. a
+// (batch, dim, len) view of time-major storage): one VGPR offset, the block's
+// lowest memory step, and a wave-uniform SGPR offset per step, so the addressing
+// costs no VALU work.
+template <int I, bool REV>
+__device__ __forceinline__ void load_block_strided(__amdgpu_buffer_rsrc_t r, unsigned voff,
+                                                   long long ts, float (&v)[I]) {
+#pragma unroll
+  for (int k = 0; k < I; ++k)
+    v[REV ? I - 1 - k : k] = __builtin_bit_cast(
+        float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, (int)(k * ts * 4), 0));
+}
+
+template <int I, bool REV>
+__device__ __forceinline__ void store_block_strided(__amdgpu_buffer_rsrc_t r, unsigned voff,
+                                                    long long ts, const float (&v)[I]) {
+#pragma unroll
+  for (int k = 0; k < I; ++k)
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v[REV ? I - 1 - k : k]),
+                                          r, voff, (int)(k * ts * 4), 0);
+}
+
 // One state n of one chunk given this lane's B/C blocks (bb, cc): pass 1, the
 // row scan, pass 2, and the carry into the next chunk. a2 = A[d][n] log2(e).
 template <int LPR, int I>
@@ -244,7 +275,8 @@ __device__ __forceinline__ void chunk(const M1Kern& p, long long sb, int j, bool
                                       const float* drow, const float* zrow, float* orow,
                                       const float* Bg, const float* Cg, const float* a2s,
                                       float bias, float dskip, float* carry, float (&dn)[I],
-                                      float (&un)[I], bool have, long long pre_sb) {
+                                      float (&un)[I], bool have, long long pre_sb,
+                                      long long zts = 1, long long ots = 1) {
   constexpr bool V = VEC && FULL;
   const long long L = p.L;
   const int N = p.N;
@@ -276,11 +308,11 @@ __device__ __forceinline__ void chunk(const M1Kern& p, long long sb, int j, bool
     }
     if (zrow) {
       float zz[I];
-      load_block<I, REV, false>(zrow, Lv, sb, 0.0f, zz, L);
+      load_block<I, REV, false>(zrow, Lv, sb, 0.0f, zz, L, zts);
 #pragma unroll
       for (int i = 0; i < I; ++i) y[i] *= silu_fast(zz[i]);
     }
-    if (valid) store_block<I, REV, false>(orow, Lv, sb, y, L);
+    if (valid) store_block<I, REV, false>(orow, Lv, sb, y, L, ots);
     return;
   }
   float bv[I], cv[I], bn[I], cn[I], zz[I];
@@ -424,6 +456,80 @@ __device__ __forceinline__ void issue_tile(float* tile, const float* Bg, const f
   }
 }
 
+// Strided z through LDS: the block's 16 channels of a FULL chunk's 256 steps, as
+// [step][channel] (16 KB). With zs_d == 1 the four channels 4q .. 4q+3 of a step
+// are one 16-byte piece, so the block fetches whole 64-byte runs instead of each
+// wave pulling 16 bytes out of every line it touches. DMA op m holds the steps
+// 16m .. 16m+15 (lane block m of the chunk); its slot L holds piece
+// x = L ^ m: step 16m + x/4, channels 4(x%4) .. +3 — the XOR spreads the 16 lanes
+// that read one step of their blocks over the banks.
+constexpr int kZStageFloats = 16 * 256;
+
+template <bool REV>
+__device__ __forceinline__ void issue_z_stage(float* zbuf, const float* zslab, long long zs_t,
+                                              long long L, long long c0, int d0, int wave,
+                                              int lane) {
+  // recomputed per chunk: hoisting these addresses out of the chunk loop would hold
+  // registers through the whole scan
+  asm volatile("" : "+v"(lane));
+#pragma unroll
+  for (int m0 = 0; m0 < 16; m0 += kWavesPerBlock) {
+    const int m = m0 + wave;  // wave-uniform
+    const int x = lane ^ m;
+    const long long s = c0 + 16 * m + (x >> 2);  // traversal step
+    const float* src = zslab + d0 + 4 * (x & 3) + (REV ? L - 1 - s : s) * zs_t;
+    __builtin_amdgcn_global_load_lds((const void*)src,
+                                     (__attribute__((address_space(3))) void*)(zbuf + m * 256),
+                                     16, 0, 0);
+  }
+}
+
+// Lane (row rw of wave w, lane block j): steps 16j + i of channel 4w + rw sit in
+// slot (4i + w) ^ j of DMA op j, i.e. 4(i ^ (j>>2)) + (w ^ (j&3)).
+__device__ __forceinline__ void read_z_stage(const float* zbuf, int j, int wave, int rw,
+                                             float (&v)[16]) {
+  asm volatile("" : "+v"(j));  // keep the addresses out of the chunk loop's registers
+  const float* base = zbuf + j * 256 + 4 * (wave ^ (j & 3)) + rw;
+  const int jh = j >> 2;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) v[i] = base[16 * (i ^ jh)];
+}
+
+// The outputs through the same stage, the other way round: each lane writes its
+// 16 steps of its channel into the swizzled layout above; after a sync, lane l of
+// wave w stores slot l ^ m of op m = 4r + w (r = 0..3): step 16m + l/4, channels
+// 4(l%4) .. +3, so four adjacent lanes store one step's 16 channels as 64 bytes.
+// (Strided per-lane stores put the four channels of a step in lanes 16 apart, which
+// the memory pipeline does not combine.)
+__device__ __forceinline__ void write_out_stage(float* zbuf, int j, int wave, int rw,
+                                                const float (&v)[16]) {
+  asm volatile("" : "+v"(j));
+  float* base = zbuf + j * 256 + 4 * (wave ^ (j & 3)) + rw;
+  const int jh = j >> 2;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) base[16 * (i ^ jh)] = v[i];
+}
+
+template <bool REV>
+__device__ __forceinline__ void store_out_stage(const float* zbuf, float* oslab, long long os_t,
+                                                long long L, long long c0, int d0, int wave,
+                                                int lane) {
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int m = 4 * r + wave;
+    const float4 v = *reinterpret_cast<const float4*>(zbuf + m * 256 + 4 * (lane ^ m));
+    const long long s = c0 + 16 * m + (lane >> 2);  // traversal step
+    *reinterpret_cast<float4*>(oslab + d0 + 4 * (lane & 3) + (REV ? L - 1 - s : s) * os_t) = v;
+  }
+}
+
+// Workgroup barrier that waits for LDS accesses only (global stores stay in flight).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 __device__ __forceinline__ void tile_sync() {
   __builtin_amdgcn_s_waitcnt(0);  // this wave's DMA (and every other access) landed
   __syncthreads();
@@ -487,15 +593,19 @@ __device__ __forceinline__ void tile_states(const float* tile, int n0, int N, in
   }
 }
 
-// The rows of block `blk` (16 per block) through one traversal.
-template <int I, bool REV>
+// The rows of block `blk` (16 per block) through one traversal. SIO 0: z and out
+// (batch, dim, len) contiguous; 1: strided (p.zs_*, p.os_*), z read with buffer
+// loads and out written with buffer stores; 2: strided with unit channel stride,
+// z and out staged through LDS.
+template <int I, bool REV, int SIO>
 __device__ __forceinline__ void tile_rows(const M1Kern& p, long long blk) {
   constexpr int LPR = 16, RPW = 4;
   using G = Tile<I>;
   constexpr long long CH = G::CH;
   extern __shared__ __attribute__((aligned(16))) float s_lds[];
   float* tiles = s_lds;                                  // [2][G::FLOATS]
-  float* small = s_lds + 2 * G::FLOATS;                  // carry, A*log2e, zeros
+  float* zbuf = s_lds + 2 * G::FLOATS;                   // SIO: [256][16] z stage
+  float* small = zbuf + (SIO == 2 ? kZStageFloats : 0);  // carry, A*log2e, zeros
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -508,8 +618,12 @@ __device__ __forceinline__ void tile_rows(const M1Kern& p, long long blk) {
   const int g = d / p.group_size;
   const float* urow = p.u + row * L;
   const float* drow = p.delta + row * L;
-  const float* zrow = p.z ? p.z + row * L : nullptr;
-  float* orow = p.out + row * L;
+  const float* zrow =
+      p.z ? (SIO ? p.z + bi * p.zs_b + d * p.zs_d : p.z + row * L) : nullptr;
+  float* orow = SIO ? p.out + bi * p.os_b + d * p.os_d : p.out + row * L;
+  // strided z/out: the block's 16 rows share one batch, whose index taken from the
+  // block id is wave-uniform (a buffer resource must be)
+  const long long bib = blk * (kWavesPerBlock * RPW) / p.dim;
   const float* Bg = p.B + ((long long)bi * p.groups + g) * N * L;
   const float* Cg = p.C + ((long long)bi * p.groups + g) * N * L;
   const float* Arow = p.A + (long long)d * N;
@@ -533,6 +647,26 @@ __device__ __forceinline__ void tile_rows(const M1Kern& p, long long blk) {
   auto mem0 = [&](long long c) { return REV ? L - (c + 1) * CH : c * CH; };
   if (ntiles > 0) issue_tile<I>(tiles, Bg, Cg, L, mem0(0), 0, N, wave, lane);
   tile_sync();
+
+  // the lane block's outputs at traversal base sbo (SIO 0 and 1)
+  auto store_out = [&](long long sbo, const float (&v)[I]) {
+    if (SIO) {
+      const long long tlo = REV ? L - sbo - I : sbo;  // the block's lowest memory step
+      store_block_strided<I, REV>(slab_rsrc(p.out + bib * p.os_b, p.o_bytes),
+                                  (unsigned)((d * p.os_d + tlo * p.os_t) * 4), p.os_t, v);
+    } else {
+      store_block<I, REV, true>(orow, L, sbo, v, L);
+    }
+  };
+
+  // SIO 2: chunk c's z stage is issued once chunk c-1's outputs have left the stage
+  // (a sync), lands by chunk c's first tile sync (ng >= 2) and is read after chunk
+  // c's last tile's states.
+  const int d0 = (int)(blk * (kWavesPerBlock * RPW) % p.dim);  // the block's first channel
+  auto z_stage = [&](long long c) {
+    issue_z_stage<REV>(zbuf, p.z + bib * p.zs_b, p.zs_t, L, c * CH, d0, wave, lane);
+  };
+  if (SIO == 2 && p.z && nfull > 0) z_stage(0);
 
   long long k = 0;  // tile counter
   for (long long c = 0; c < nfull; ++c) {
@@ -561,31 +695,64 @@ __device__ __forceinline__ void tile_rows(const M1Kern& p, long long blk) {
         issue_tile<I>(tiles + ((k + 1) & 1) * G::FLOATS, Bg, Cg, L, mem0(cn),
                       qn * kTileStates, N, wave, lane);
       }
-      if (zrow && q + 1 == ng) load_block<I, REV, true>(zrow, L, sb, 0.0f, zz, L);
+      if (SIO != 2 && zrow && q + 1 == ng) {
+        if (SIO == 1) {
+          const long long tlo = REV ? L - sb - I : sb;  // the block's lowest memory step
+          load_block_strided<I, REV>(slab_rsrc(p.z + bib * p.zs_b, p.z_bytes),
+                                     (unsigned)((d * p.zs_d + tlo * p.zs_t) * 4), p.zs_t, zz);
+        } else {
+          load_block<I, REV, true>(zrow, L, sb, 0.0f, zz, L);
+        }
+      }
       tile_states<I, REV>(tiles + (k & 1) * G::FLOATS, q * kTileStates, N, j, a2s, cbase,
                           carry, (last_chunk && p.last) ? p.last + row * N : nullptr, dt, du,
                           sdt, y);
+      if (SIO == 2 && zrow && q + 1 == ng) {
+        // after the states (no registers held through them), before the sync after
+        // which the outputs overwrite it
+        static_assert(SIO != 2 || I == 16, "the stage holds 16 steps per lane block");
+        read_z_stage(zbuf, j, wave, rw, zz);
+      }
       tile_sync();
     }
     if (zrow) {
 #pragma unroll
       for (int i = 0; i < I; ++i) y[i] *= silu_fast(zz[i]);
     }
-    store_block<I, REV, true>(orow, L, sb, y, L);
+    if (SIO == 2) {
+      write_out_stage(zbuf, j, wave, rw, y);
+      lds_barrier();
+      store_out_stage<REV>(zbuf, p.out + bib * p.os_b, p.os_t, L, c * CH, d0, wave, lane);
+      lds_barrier();  // every lane has read its outputs before the next z stage lands
+      if (p.z && c + 1 < nfull) z_stage(c + 1);
+    } else {
+      store_out(sb, y);
+    }
   }
   if (nfull < nch) {
     // the row's tail chunk goes through the bounds-checked global-load path
     float dn[I], un[I];
     chunk<LPR, I, REV, true, false>(p, nfull * CH + (long long)j * I, j, true, true, row, urow,
                                     drow, zrow, orow, Bg, Cg, a2s, bias, dskip, carry, dn, un,
-                                    false, -1);
+                                    false, -1, SIO ? p.zs_t : 1, SIO ? p.os_t : 1);
   }
 }
 
-template <int I, bool REV>
-__global__ void __launch_bounds__(64 * kWavesPerBlock)
+// Block id -> row block for time-major z/out: a 128-byte line of those holds 32
+// channels, two row blocks' worth, so adjacent row blocks go to one XCD (block id
+// mod 8), dispatched back to back, and each line is fetched and written back whole
+// by one L2. Ids past the last multiple of 16 map to themselves.
+__device__ __forceinline__ long long paired_block(long long bid, long long nblk) {
+  if (bid >= (nblk & ~15LL)) return bid;
+  const long long x = bid & 7, k = bid >> 3;
+  return 2 * (8 * (k >> 1) + x) + (k & 1);
+}
+
+template <int I, bool REV, int SIO>
+__global__ void __launch_bounds__(64 * kWavesPerBlock, 3)
 m1_tile_kernel(M1Kern p) {
-  tile_rows<I, REV>(p, blockIdx.x);
+  const long long nblk = p.rows / (kWavesPerBlock * 4);
+  tile_rows<I, REV, SIO>(p, SIO ? paired_block(blockIdx.x, nblk) : (long long)blockIdx.x);
 }
 
 // Several traversals of rows of the same shape in one launch (the directions of
@@ -607,17 +774,18 @@ m1_tile_jobs_kernel(M1Kern p, M1Jobs jobs) {
   p.C = jb.C;
   p.out = jb.out;
   p.last = jb.last;
-  if (jb.rev) tile_rows<I, true>(p, blk);
-  else tile_rows<I, false>(p, blk);
+  if (jb.rev) tile_rows<I, true, 0>(p, blk);
+  else tile_rows<I, false, 0>(p, blk);
 }
 
-template <int I, bool REV>
+template <int I, bool REV, int SIO>
 hipError_t launch_tile(const M1Kern& k, hipStream_t st) {
   constexpr int RPB = kWavesPerBlock * 4;
   const long long blocks = (long long)k.rows / RPB;
   const size_t lds =
-      sizeof(float) * (2 * (size_t)Tile<I>::FLOATS + (2 * (size_t)RPB + 1) * k.N);
-  hipLaunchKernelGGL((m1_tile_kernel<I, REV>), dim3((unsigned)blocks),
+      sizeof(float) * (2 * (size_t)Tile<I>::FLOATS + (SIO == 2 ? kZStageFloats : 0) +
+                       (2 * (size_t)RPB + 1) * k.N);
+  hipLaunchKernelGGL((m1_tile_kernel<I, REV, SIO>), dim3((unsigned)blocks),
                      dim3(64 * kWavesPerBlock), lds, st, k);
   return hipGetLastError();
 }
@@ -671,6 +839,43 @@ hipError_t m1_scan_jobs(const M1Problem& pr, const M1JobSpec* spec, int n, hipSt
   return hipGetLastError();
 }
 
+namespace {
+bool contiguous_strides(const long long (&s)[3], const M1Problem& pr) {
+  const long long L = (long long)pr.len, D = (long long)pr.dim;
+  return (s[0] == 0 && s[1] == 0 && s[2] == 0) || (s[0] == D * L && s[1] == L && s[2] == 1);
+}
+// bytes of one batch's slab of a strided (batch, dim, len) tensor
+long long slab_bytes(const long long (&s)[3], const M1Problem& pr) {
+  return 4 * ((long long)(pr.dim - 1) * s[1] + (long long)(pr.len - 1) * s[2] + 1);
+}
+}  // namespace
+
+bool m1_strided_io(const M1Problem& pr) {
+  return (pr.z && !contiguous_strides(pr.z_stride, pr)) || !contiguous_strides(pr.out_stride, pr);
+}
+
+bool m1_strided_supported(const M1Problem& pr, const char** why) {
+  auto no = [&](const char* w) {
+    if (why) *why = w;
+    return false;
+  };
+  if (pr.len % 4 != 0 || !aligned16(pr.u) || !aligned16(pr.delta) || !aligned16(pr.B) ||
+      !aligned16(pr.C))
+    return no("strided z/out need len % 4 == 0 and 16-byte aligned u, delta, B, C");
+  if (pr.dim % 16 != 0 || (pr.dim / pr.groups) % 16 != 0)
+    return no("strided z/out need dim and dim/groups multiples of 16");
+  for (int t = 0; t < 2; ++t) {
+    const long long(&s)[3] = t ? pr.out_stride : pr.z_stride;
+    if (t == 0 && !pr.z) continue;
+    if (contiguous_strides(s, pr)) continue;
+    if (s[0] < 0 || s[1] < 0 || s[2] < 0) return no("negative z/out strides");
+    if (t == 1 && (s[1] == 0 || s[2] == 0)) return no("out strides must not be zero");
+    if (slab_bytes(s, pr) >= (1LL << 32) || 4LL * (M1_TILE_I - 1) * s[2] >= (1LL << 31))
+      return no("a batch of strided z/out must span less than 4 GiB");
+  }
+  return true;
+}
+
 hipError_t m1_scan_chunked(const M1Problem& pr, hipStream_t st) {
   M1Kern k{};
   k.u = pr.u; k.delta = pr.delta; k.A = pr.A; k.B = pr.B; k.C = pr.C; k.D = pr.D; k.z = pr.z;
@@ -681,9 +886,34 @@ hipError_t m1_scan_chunked(const M1Problem& pr, hipStream_t st) {
   const bool vec = pr.len % 4 == 0 && aligned16(pr.u) && aligned16(pr.delta) &&
                    aligned16(pr.B) && aligned16(pr.C) && aligned16(pr.z) && aligned16(pr.out);
   const bool rev = pr.reverse != 0;
+  if (m1_strided_io(pr)) {
+    if (!m1_strided_supported(pr, nullptr)) return hipErrorInvalidValue;
+    const long long L = (long long)pr.len, D = (long long)pr.dim;
+    const long long zc[3] = {D * L, L, 1};
+    const bool zcont = contiguous_strides(pr.z_stride, pr), ocont = contiguous_strides(pr.out_stride, pr);
+    const long long(&zs)[3] = zcont ? zc : pr.z_stride;
+    const long long(&os)[3] = ocont ? zc : pr.out_stride;
+    k.zs_b = zs[0]; k.zs_d = zs[1]; k.zs_t = zs[2];
+    k.os_b = os[0]; k.os_d = os[1]; k.os_t = os[2];
+    k.z_bytes = pr.z ? (unsigned)slab_bytes(zs, pr) : 0u;
+    // the LDS stage: 16-byte channel runs of out (and z), and for z a chunk of at
+    // least two tiles between issuing the stage and reading it
+    k.z_dma = os[1] == 1 && os[2] % 4 == 0 && os[0] % 4 == 0 && aligned16(pr.out) &&
+              (!pr.z || (zs[1] == 1 && zs[2] % 4 == 0 && zs[0] % 4 == 0 && aligned16(pr.z) &&
+                         pr.state > kTileStates)) &&
+              M1_TILE_I == 16;
+    k.o_bytes = (unsigned)slab_bytes(os, pr);
+    if (k.z_dma)
+      return rev ? launch_tile<M1_TILE_I, true, 2>(k, st)
+                 : launch_tile<M1_TILE_I, false, 2>(k, st);
+    return rev ? launch_tile<M1_TILE_I, true, 1>(k, st)
+               : launch_tile<M1_TILE_I, false, 1>(k, st);
+  }
   // the tiled path needs every 16-row block inside one batch/group and 16-byte rows
   const bool tiled = vec && pr.dim % 16 == 0 && (pr.dim / pr.groups) % 16 == 0;
-  if (tiled) return rev ? launch_tile<M1_TILE_I, true>(k, st) : launch_tile<M1_TILE_I, false>(k, st);
+  if (tiled)
+    return rev ? launch_tile<M1_TILE_I, true, 0>(k, st)
+               : launch_tile<M1_TILE_I, false, 0>(k, st);
   return launch_dir<16, 16>(k, rev, vec, st);
 }
 

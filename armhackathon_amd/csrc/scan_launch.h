@@ -16,9 +16,15 @@ struct M1Problem {
   float *out2, *last2;  // bidirectional outputs
   int softplus, reverse;
   int merge;  // bidirectional: write out = fwd + bwd instead of two outputs
+  // element strides (batch, dim, step) of z and out; all zero = (dim*len, len, 1)
+  long long z_stride[3], out_stride[3];
 };
 
 hipError_t m1_scan(const M1Problem& p, hipStream_t st);
+// True when z or out has strides other than the contiguous (batch, dim, len) ones.
+bool m1_strided_io(const M1Problem& p);
+// Whether the one-direction scan serves the strides of z/out; else *why says what fails.
+bool m1_strided_supported(const M1Problem& p, const char** why);
 // One direction through the chunked DPP-scan kernel (m1_chunk.hip).
 hipError_t m1_scan_chunked(const M1Problem& p, hipStream_t st);
 // True when the fused bidirectional kernel can hold a whole row in one pass.

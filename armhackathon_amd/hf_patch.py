@@ -12,12 +12,18 @@ original function unchanged, exactly as the reference's wrapper falls back on
 what its kernel cannot serve (python/arm_scan/patch.py:152-168). Decode steps
 use `mamba_selective_state_update`, which is not patched.
 
+The mixer hands the gate z as a (batch, dim, len) view of its time-major
+in_proj output and transposes the scan output back for out_proj. The wrapper
+reads z in place and writes the output time-major (returned as a (batch, dim,
+len) view), so neither side copies; the reference's op copies z
+(python/arm_scan/op.py:19-20).
+
 `unpatch()` restores the original; `stats()` reports engagement.
 """
 
 import torch
 
-from .op import kernel_calls, selective_scan
+from .op import kernel_calls, selective_scan_time_major
 
 _STATE = {"orig": None, "target": None, "fast_calls": 0, "fallback_calls": 0}
 
@@ -42,9 +48,13 @@ def _patch_scan_fn(modeling_mamba):
                         use_mambapy=use_mambapy, use_associative_scan=use_associative_scan,
                         **kwargs)
         _STATE["fast_calls"] += 1
-        return selective_scan(hidden_states, dt, A, B, C, D=D, z=z, delta_bias=delta_bias,
-                              delta_softplus=delta_softplus,
-                              return_last_state=return_last_state)
+        # the mixer's gate is a (b, D, L) view of time-major storage and its out_proj
+        # reads scan_output.transpose(1, 2): read z in place and write the output
+        # time-major, so neither needs a copy
+        return selective_scan_time_major(hidden_states, dt, A, B, C, D=D, z=z,
+                                         delta_bias=delta_bias,
+                                         delta_softplus=delta_softplus,
+                                         return_last_state=return_last_state)
 
     modeling_mamba.mamba_selective_scan = mamba_selective_scan
     _STATE["orig"] = orig

@@ -141,6 +141,96 @@ def selective_scan(u, delta, A, B, C, D=None, z=None, delta_bias=None,
     return (out, last_state) if return_last_state else out
 
 
+def _strided_ok(u, delta, b, c, z, dim, length, groups):
+    """Whether arm_scan_selective_scan_strided_f32 serves these tensors (the
+    conditions its declaration states)."""
+    if length % 4 or dim % 16 or (dim // groups) % 16:
+        return False
+    if any(t.data_ptr() % 16 for t in (u, delta, b, c)):
+        return False
+    for t in (z, None):
+        st = (length * dim, 1, dim) if t is None else t.stride()
+        if min(st) < 0 or 4 * ((dim - 1) * st[1] + (length - 1) * st[2] + 1) >= 1 << 32:
+            return False
+    return True
+
+
+@torch.library.custom_op("arm_scan::selective_scan_time_major", mutates_args=())
+def _selective_scan_tm_op(
+    u: torch.Tensor,
+    delta: torch.Tensor,
+    a: torch.Tensor,
+    b: torch.Tensor,
+    c: torch.Tensor,
+    d_skip: Optional[torch.Tensor],
+    z: Optional[torch.Tensor],
+    delta_bias: Optional[torch.Tensor],
+    h0: Optional[torch.Tensor],
+    delta_softplus: bool,
+    reverse: bool,
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    dev = _device_of(u, delta, a, b, c, d_skip, z, delta_bias, h0)
+    batch, dim, length, state, groups = _check_m1(u, delta, a, b, c, d_skip, z, delta_bias, h0)
+    out = u.new_empty((batch, length, dim)).transpose(1, 2)
+    last_state = u.new_empty((batch, dim, state))
+    dims = _ffi.ArmScanDims(batch, dim, length, state, groups)
+    with torch.cuda.device(dev):
+        if _strided_ok(u, delta, b, c, z, dim, length, groups):
+            _ffi.scan_strided_raw(dims, u.data_ptr(), delta.data_ptr(), a.data_ptr(),
+                                  b.data_ptr(), c.data_ptr(), _ptr(d_skip), _ptr(z),
+                                  None if z is None else z.stride(), _ptr(delta_bias),
+                                  delta_softplus, out.data_ptr(), out.stride(),
+                                  last_state.data_ptr(), _ptr(h0), reverse=reverse,
+                                  stream=_stream(dev))
+        else:
+            # a shape the strided kernel does not serve: the contiguous scan, then
+            # the output laid out time-major
+            zc = None if z is None else z.contiguous()
+            tmp = torch.empty_like(u)
+            _ffi.scan_raw(dims, u.data_ptr(), delta.data_ptr(), a.data_ptr(), b.data_ptr(),
+                          c.data_ptr(), _ptr(d_skip), _ptr(zc), _ptr(delta_bias),
+                          delta_softplus, "auto", "auto", tmp.data_ptr(),
+                          last_state.data_ptr(), ptr_h0=_ptr(h0), reverse=reverse,
+                          stream=_stream(dev))
+            out.copy_(tmp)
+    _CALLS["n"] += 1
+    return out, last_state
+
+
+@_selective_scan_tm_op.register_fake
+def _(u, delta, a, b, c, d_skip, z, delta_bias, h0, delta_softplus, reverse):
+    batch, dim, length = u.shape
+    return (u.new_empty((batch, length, dim)).transpose(1, 2),
+            u.new_empty((batch, dim, a.shape[1])))
+
+
+def selective_scan_time_major(u, delta, A, B, C, D=None, z=None, delta_bias=None,
+                              delta_softplus=False, return_last_state=False,
+                              initial_state=None, reverse=False):
+    """`selective_scan` for callers whose tensors are time-major underneath, as in
+    Hugging Face's Mamba mixer (modeling_mamba.py MambaMixer.forward): z may be any
+    strided (batch, dim, len) view (the mixer's gate is one of (batch, len, 2*dim)
+    storage) and is read in place, and out is returned as a (batch, dim, len) view
+    of (batch, len, dim) storage, so `out.transpose(1, 2)` is contiguous for the
+    mixer's out_proj. Same arguments, values and final state as `selective_scan`.
+    The reference copies z here (python/arm_scan/op.py:19-20); this has no
+    counterpart there."""
+    batch, dim, length = u.shape
+    state = A.shape[1]
+    B = _bc4(B, batch, state, length)
+    C = _bc4(C, batch, state, length)
+    if z is not None and z.dtype != torch.float32:
+        z = z.float()
+    out, last_state = _selective_scan_tm_op(
+        _c(u), _c(delta), _c(A), _c(B), _c(C),
+        None if D is None else _c(D),
+        z,
+        None if delta_bias is None else _c(delta_bias),
+        None if initial_state is None else _c(initial_state),
+        bool(delta_softplus), bool(reverse))
+    return (out, last_state) if return_last_state else out
+
+
 @torch.library.custom_op("arm_scan::selective_scan_bidirectional", mutates_args=())
 def _selective_scan_bidir_op(
     u: torch.Tensor,

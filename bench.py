@@ -21,8 +21,9 @@ The JSON line carries:
   cpu_baseline  the CPU oracle (a C++ restatement of the reference's x86
                 scalar scan path) on a bounded sample of the same workload.
 
-`--workload m3_siso|m3_mimo|ss2d` times one of configs 3-5 alone (the command
-behind their rocprofv3 summaries in profiles/).
+`--workload m3_siso|m3_mimo|ss2d` times one of configs 3-5 alone, and
+`--workload m1_seam` the config-2 scan in the Hugging Face mixer's layouts (the
+commands behind their rocprofv3 summaries in profiles/).
 """
 
 import argparse
@@ -49,9 +50,11 @@ def parse():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
-    ap.add_argument("--workload", choices=("m1", "m3_siso", "m3_mimo", "ss2d"), default="m1",
+    ap.add_argument("--workload", choices=("m1", "m1_seam", "m3_siso", "m3_mimo", "ss2d"),
+                    default="m1",
                     help="m1 (default): the headline line below; the others time one of the "
-                         "configs 3-5 alone (for profiling) and print its own line")
+                         "configs 3-5, or the config-2 scan in the HF mixer's layouts "
+                         "(m1_seam), alone (for profiling) and print its own line")
     ap.add_argument("--no-configs", action="store_true",
                     help="skip timing configs 3-5 in the headline line")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -118,6 +121,13 @@ def config_inputs(name, dev):
 
     from armhackathon_amd import workloads
 
+    if name == "m1_seam":
+        t = scan_inputs(0, dev)
+        b, d, L, n = SHAPE["batch"], SHAPE["dim"], SHAPE["length"], SHAPE["state"]
+        proj = torch.empty((b, L, 2 * d), device=dev)  # the mixer's in_proj output
+        proj[..., d:] = t["z"].transpose(1, 2)
+        t["z"] = proj.transpose(1, 2)[:, d:]
+        return t, workloads.m1_bytes(b, d, L, n, z=True, D=True, bias=True, last_state=True)
     if name == "m3_siso":
         x = workloads.m3_siso(seed=3)
         nbytes = workloads.m3_bytes(x)
@@ -131,6 +141,9 @@ def config_inputs(name, dev):
 
 
 CONFIG_NAMES = {
+    "m1_seam": "config 2 scan at the Hugging Face seam: B8 D1536 L2048 N16, bias+softplus, "
+               "D, z read in place from the mixer's (b, L, 2D) projection, out written "
+               "time-major",
     "m3_siso": "config 3: Mamba-3 SISO B4 L4096 24 heads x 64, dqk 128 (final states too)",
     "m3_mimo": "config 4: Mamba-3 MIMO rank 4, B4 L4096 24 heads x 64, dqk 128 (final state)",
     "ss2d": "config 5: SS2D 4 directions, B16 D192 64x64 N16, D, z, merge sum (final states)",
@@ -146,7 +159,12 @@ def bench_config(name, dev, steps, warmup):
 
     t, nbytes = config_inputs(name, dev)
     K = ("q", "k", "v", "adt", "dt", "trap", "q_bias", "k_bias")
-    if name == "m3_siso":
+    if name == "m1_seam":
+        def call():
+            return arm_scan.selective_scan_time_major(
+                t["u"], t["delta"], t["A"], t["B"], t["C"], D=t["D"], z=t["z"],
+                delta_bias=t["delta_bias"], delta_softplus=True, return_last_state=True)
+    elif name == "m3_siso":
         def call():
             return arm_scan.mamba3_scan(*[t[k] for k in K], cos=t["cos"], sin=t["sin"],
                                         return_last_state=True)

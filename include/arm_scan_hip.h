@@ -82,6 +82,24 @@ int arm_scan_selective_scan_f32(const ArmScanDims* dims, const float* u, const f
                                 int delta_softplus, int reverse, int backend, int threading,
                                 float* out, float* last_state, const float* h0, void* stream);
 
+/* No reference counterpart: arm_scan_selective_scan_f32 with z and out given by
+ * element strides (batch, dim, step) instead of as contiguous (batch, dim, len).
+ * It serves the Hugging Face seam, which hands the gate z as a (batch, dim, len)
+ * view of time-major (batch, len, 2*dim) storage (transformers modeling_mamba.py
+ * MambaMixer.forward -> mamba_selective_scan(..., z=gate)); the reference copies it
+ * (python/arm_scan/op.py:19-20). Writing out time-major likewise lets the caller's
+ * out_proj read it without a copy. A null stride array means contiguous. Needs
+ * len % 4 == 0, dim and dim/groups multiples of 16, 16-byte aligned u/delta/B/C and
+ * each batch of z/out inside 4 GiB; otherwise ARM_SCAN_ERR_INVALID_DIMS, and the
+ * caller makes z/out contiguous and calls arm_scan_selective_scan_f32. */
+int arm_scan_selective_scan_strided_f32(const ArmScanDims* dims, const float* u,
+                                        const float* delta, const float* a, const float* b,
+                                        const float* c, const float* d_skip, const float* z,
+                                        const long long* z_strides, const float* delta_bias,
+                                        int delta_softplus, int reverse, float* out,
+                                        const long long* out_strides, float* last_state,
+                                        const float* h0, void* stream);
+
 /* Replaces arm_scan_selective_scan_bidirectional_f32 (arm-scan-ffi/src/lib.rs:235-354):
  * the forward and the reverse scan of the same inputs in one pass sharing exp(delta*A).
  * last_fwd / last_bwd: both or neither (else ARM_SCAN_ERR_INVALID_DIMS). */

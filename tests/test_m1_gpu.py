@@ -180,3 +180,100 @@ def test_m1_benchmark_shape(batch):
     ref, ref_last = _ref(x)
     assert rel_err(host(out), ref) < TOL
     assert rel_err(host(last), ref_last) < TOL
+
+
+def _time_major_inputs(x):
+    """Device tensors laid out as the Hugging Face mixer hands them over: the gate
+    z a (b, D, L) view of (b, L, 2D) storage (modeling_mamba.py: projected_states
+    = in_proj(h).transpose(1, 2); gate = chunk(2, dim=1)[1])."""
+    import torch
+
+    t = dev(x)
+    b, d, L = x["u"].shape
+    proj = torch.empty((b, L, 2 * d), device="cuda")
+    proj[..., d:] = t["z"].transpose(1, 2)
+    proj[..., :d] = -7.0  # the other half of the storage is never read
+    t["z"] = proj.transpose(1, 2)[:, d:]
+    assert t["z"].stride() == (L * 2 * d, 1, 2 * d)
+    return t
+
+
+TM_SHAPES = [
+    # (batch, dim, len, state, groups): tiled shapes with and without row tails
+    # (z staged through LDS when state > 8, read with buffer loads at state 8),
+    # and (dim % 16 != 0) one the strided kernel does not serve
+    (2, 32, 1000, 16, 1),
+    (2, 32, 1000, 8, 1),
+    (1, 16, 256, 16, 1),
+    (3, 48, 2052, 13, 3),
+    (2, 64, 4096, 16, 2),
+    (1, 12, 700, 16, 1),
+]
+
+
+@pytest.mark.parametrize("shape", TM_SHAPES, ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("reverse", [False, True])
+def test_m1_time_major_seam(shape, reverse):
+    """selective_scan_time_major (z read in place from time-major storage, out
+    written time-major) equals selective_scan bit for bit, and the oracle."""
+    import armhackathon_amd as arm_scan
+
+    b, d, L, n, g = shape
+    case(f"m1 time-major seam {shape} reverse={reverse}")
+    rng = np.random.default_rng(hash((shape, reverse, "tm")) & 0xFFFF)
+    f = np.float32
+    x = dict(u=rng.standard_normal((b, d, L)).astype(f),
+             delta=(rng.standard_normal((b, d, L)) * 0.5).astype(f),
+             A=(-np.exp(rng.uniform(-0.7, 2.7, (d, n)))).astype(f),
+             B=rng.standard_normal((b, g, n, L)).astype(f),
+             C=rng.standard_normal((b, g, n, L)).astype(f),
+             D=rng.standard_normal(d).astype(f), z=rng.standard_normal((b, d, L)).astype(f),
+             delta_bias=rng.uniform(-6, -3, d).astype(f),
+             h0=rng.standard_normal((b, d, n)).astype(f))
+    t = _time_major_inputs(x)
+    out, last = arm_scan.selective_scan_time_major(
+        t["u"], t["delta"], t["A"], t["B"], t["C"], D=t["D"], z=t["z"],
+        delta_bias=t["delta_bias"], delta_softplus=True, return_last_state=True,
+        initial_state=t["h0"], reverse=reverse)
+    assert out.shape == (b, d, L) and out.stride() == (L * d, 1, d)
+    ref_out, ref_last = _scan(x, delta_softplus=True, reverse=reverse)
+    assert np.array_equal(host(out), host(ref_out))
+    assert np.array_equal(host(last), host(ref_last))
+    o64, l64 = _ref(x, delta_softplus=True, reverse=reverse)
+    assert rel_err(host(out), o64) < TOL and rel_err(host(last), l64) < TOL
+
+
+def test_m1_time_major_without_gate():
+    """No z: only the output is strided."""
+    import armhackathon_amd as arm_scan
+
+    case("m1 time-major seam, z absent")
+    x = workloads.m1_op(batch=2, dim=32, length=1500, state=16, seed=9, z=False)
+    t = dev(x)
+    out = arm_scan.selective_scan_time_major(t["u"], t["delta"], t["A"], t["B"], t["C"],
+                                             D=t["D"])
+    assert out.stride() == (1500 * 32, 1, 32)
+    assert np.array_equal(host(out), host(_scan(x)[0]))
+
+
+@pytest.mark.parametrize("reverse", [False, True])
+def test_m1_strided_gate_channel_stride(reverse):
+    """z with a channel stride of 2 (every other channel of a wider tensor, so no
+    16-byte channel runs): the buffer-load path of the strided kernel."""
+    import torch
+
+    import armhackathon_amd as arm_scan
+
+    case(f"m1 strided gate, channel stride 2, reverse={reverse}")
+    x = workloads.m1_op(batch=2, dim=32, length=1024, state=16, seed=11)
+    t = dev(x)
+    wide = torch.empty((2, 64, 1024), device="cuda")
+    wide[:, ::2] = t["z"]
+    wide[:, 1::2] = 5.0
+    zv = wide[:, ::2]
+    assert zv.stride() == (64 * 1024, 2 * 1024, 1)
+    out, last = arm_scan.selective_scan_time_major(
+        t["u"], t["delta"], t["A"], t["B"], t["C"], D=t["D"], z=zv, return_last_state=True,
+        reverse=reverse)
+    ref, ref_last = _scan(x, reverse=reverse)
+    assert np.array_equal(host(out), host(ref)) and np.array_equal(host(last), host(ref_last))

@@ -25,14 +25,17 @@ def _model(layers=3, hidden=64, vocab=512, seed=0):
     return MambaForCausalLM(cfg).cuda().float().eval()
 
 
-def test_patch_logits_and_engagement():
+@pytest.mark.parametrize("length", [300, 301])
+def test_patch_logits_and_engagement(length):
+    """300: the gate read in place and the output written time-major; 301 (not a
+    multiple of 4): the contiguous scan, then the time-major layout."""
     import torch
 
     import armhackathon_amd as arm_scan
 
-    case("hf patch logits")
+    case(f"hf patch logits L={length}")
     model = _model()
-    ids = torch.randint(0, 512, (2, 300), device="cuda",
+    ids = torch.randint(0, 512, (2, length), device="cuda",
                         generator=torch.Generator(device="cuda").manual_seed(1))
     with torch.no_grad():
         ref = model(ids, use_cache=False).logits
