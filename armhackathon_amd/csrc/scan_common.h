@@ -36,13 +36,18 @@ __device__ __forceinline__ float silu(float x) { return x / (1.0f + fexp(-x)); }
 __device__ __forceinline__ float silu_fast(float x) {
   return x * __builtin_amdgcn_rcpf(1.0f + fexp(-x));
 }
-// softplus as above with the division replaced by v_rcp_f32.
+// softplus for the hot loops, one transcendental fewer than the division form:
+// with u = fl(1 + e) the rounding error r = (1 + e) - u equals e - (u - 1) exactly
+// for u < 2 (u - 1 and then e - (u - 1) are exact by Sterbenz's lemma), and
+// log1p(e) = log(u) + log1p(r/u), where log1p(r/u) = r to within e * 2^-24 of the
+// result (|r| <= 2^-24). For u >= 2, r/u is below 2^-24 of log(u) and is dropped.
+// e below 2^-24 gives u = 1, log(u) = 0 and the result e exactly.
 __device__ __forceinline__ float softplus_fast(float x) {
   if (x > 20.0f) return x;
   const float e = fexp(x);
   const float u = 1.0f + e;
-  const float d = u - 1.0f;
-  return d == 0.0f ? e : (lg2(u) * kLn2) * (e * __builtin_amdgcn_rcpf(d));
+  const float r = e - (u - 1.0f);
+  return fmaf(lg2(u), kLn2, u < 2.0f ? r : 0.0f);
 }
 // sigmoid evaluated on the non-positive branch (float.rs:52-59).
 __device__ __forceinline__ float sigmoid(float x) {
