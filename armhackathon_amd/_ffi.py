@@ -115,6 +115,20 @@ def _declare(lib):
                       _ci, _ci, _ci,     # reverse backend threading
                       _vp, _vp, _vp,     # out last_state last_bx
                       _vp]               # stream
+    f = lib.arm_scan_mamba3_scan_angles_f32
+    f.restype = _ci
+    f.argtypes = [ctypes.POINTER(ArmMamba3Dims),
+                  *([_vp] * 9),          # q k v adt dt trap q_bias k_bias angles
+                  ctypes.c_size_t,       # n_angles
+                  *([_vp] * 5),          # d_skip z psi zeta phi
+                  _ci, _ci,              # backend threading
+                  _vp, _vp, _vp,         # out last_state last_bx
+                  _vp]                   # stream
+    f = lib.arm_scan_mamba3_angles_f32
+    f.restype = _ci
+    f.argtypes = [_vp, _vp,                      # angles dt
+                  *([ctypes.c_size_t] * 5),      # batch len heads n_angles half
+                  _vp, _vp, _vp]                 # cos sin stream
     f = lib.arm_scan_ss2d_f32
     f.restype = _ci
     f.argtypes = [ctypes.POINTER(ArmSS2DDims),
@@ -219,6 +233,29 @@ def mamba3_raw(dims, ptrs, reverse, backend, threading, ptr_out, ptr_last_state,
         ctypes.byref(dims), *[_p(x) for x in ptrs], int(reverse), int(backend),
         int(threading), ptr_out, _p(ptr_last_state), _p(ptr_last_bx), _p(stream))
     _check(name, code)
+
+
+def mamba3_angles_raw(dims, ptrs, n_angles, backend, threading, ptr_out, ptr_last_state,
+                      ptr_last_bx, *, stream=0):
+    """Call arm_scan_mamba3_scan_angles_f32 (forward, out (b, l, h, dv)) with the 14
+    input pointers in signature order: q, k, v, adt, dt, trap, q_bias, k_bias,
+    angles, d_skip, z, psi, zeta, phi (the last five nullable)."""
+    if len(ptrs) != 14:
+        raise ValueError(f"expected 14 input pointers, got {len(ptrs)}")
+    name = "arm_scan_mamba3_scan_angles_f32"
+    code = getattr(load(), name)(
+        ctypes.byref(dims), *[_p(x) for x in ptrs[:9]], int(n_angles),
+        *[_p(x) for x in ptrs[9:]], int(backend), int(threading), ptr_out,
+        _p(ptr_last_state), _p(ptr_last_bx), _p(stream))
+    _check(name, code)
+
+
+def angles_raw(ptr_angles, ptr_dt, batch, length, heads, n_angles, half, ptr_cos, ptr_sin,
+               *, stream=0):
+    """Call arm_scan_mamba3_angles_f32 (the RoPE angle pre-pass)."""
+    code = load().arm_scan_mamba3_angles_f32(ptr_angles, ptr_dt, batch, length, heads,
+                                             n_angles, half, ptr_cos, ptr_sin, _p(stream))
+    _check("arm_scan_mamba3_angles_f32", code)
 
 
 def ss2d_raw(dims, ptr_u, ptr_delta, ptr_a, ptr_b4, ptr_c4, ptr_d_skip, ptr_z,

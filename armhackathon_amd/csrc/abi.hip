@@ -184,9 +184,10 @@ static int mamba3_call(const ArmMamba3Dims* dims, const float* q, const float* k
                        const float* sin, const float* d_skip, const float* z,
                        const float* mimo_psi, const float* mimo_zeta, const float* mimo_phi,
                        int reverse, int backend, int threading, float* out, float* last_state,
-                       float* last_bx, void* stream, bool time_major) {
-  if (!dims || !q || !k || !v || !adt || !dt || !trap || !q_bias || !k_bias || !cos || !sin ||
-      !out)
+                       float* last_bx, void* stream, bool time_major,
+                       const float* angles = nullptr, size_t n_angles = 0) {
+  if (!dims || !q || !k || !v || !adt || !dt || !trap || !q_bias || !k_bias || !out ||
+      (angles ? false : (!cos || !sin)))
     return fail(ARM_SCAN_ERR_NULL_POINTER, "a required pointer is null");
   const int n_mimo = (mimo_psi != nullptr) + (mimo_zeta != nullptr) + (mimo_phi != nullptr);
   const bool mimo = n_mimo == 3;
@@ -220,7 +221,15 @@ static int mamba3_call(const ArmMamba3Dims* dims, const float* q, const float* k
   p.psi = mimo_psi; p.zeta = mimo_zeta; p.phi = mimo_phi;
   p.out = out; p.last_state = last_state; p.last_bx = last_bx; p.reverse = reverse != 0;
   p.out_time_major = time_major ? 1 : 0;
-  // the chunked MFMA kernel takes dv, dqk multiples of 16 (dqk <= 256) and rank 1/2/4;
+  p.angles = angles;
+  p.n_angles = n_angles;
+  if (angles) {
+    if (!prod_ok({d.batch, d.len, d.heads, n_angles}))
+      return fail(ARM_SCAN_ERR_INVALID_DIMS, "dims overflow size_t");
+    const char* why = nullptr;
+    if (!armscan::m3_angles_supported(p, &why)) return fail(ARM_SCAN_ERR_INVALID_DIMS, "%s", why);
+  }
+  // the chunked MFMA kernel takes dv, dqk multiples of 16 (dqk <= 128) and rank 1/2/4;
   // everything else runs the step-by-step kernel, whose state must fit in LDS
   const size_t need = d.dv * (d.dqk + 1) + 2 * d.rank * (d.dqk + d.dv) + d.rank * d.rank + 4;
   if (!armscan::m3_chunk_supported(p) && need > armscan::m3_max_state())
@@ -250,6 +259,35 @@ int arm_scan_mamba3_scan_time_major_f32(
   return mamba3_call(dims, q, k, v, adt, dt, trap, q_bias, k_bias, cos, sin, d_skip, z,
                      mimo_psi, mimo_zeta, mimo_phi, reverse, backend, threading, out, last_state,
                      last_bx, stream, true);
+}
+
+int arm_scan_mamba3_scan_angles_f32(
+    const ArmMamba3Dims* dims, const float* q, const float* k, const float* v, const float* adt,
+    const float* dt, const float* trap, const float* q_bias, const float* k_bias,
+    const float* angles, size_t n_angles, const float* d_skip, const float* z,
+    const float* mimo_psi, const float* mimo_zeta, const float* mimo_phi, int backend,
+    int threading, float* out, float* last_state, float* last_bx, void* stream) {
+  if (!angles) return fail(ARM_SCAN_ERR_NULL_POINTER, "a required pointer is null");
+  return mamba3_call(dims, q, k, v, adt, dt, trap, q_bias, k_bias, nullptr, nullptr, d_skip, z,
+                     mimo_psi, mimo_zeta, mimo_phi, 0, backend, threading, out, last_state,
+                     last_bx, stream, true, angles, n_angles);
+}
+
+int arm_scan_mamba3_angles_f32(const float* angles, const float* dt, size_t batch, size_t len,
+                               size_t heads, size_t n_angles, size_t half, float* cos,
+                               float* sin, void* stream) {
+  if (!angles || !dt || !cos || !sin)
+    return fail(ARM_SCAN_ERR_NULL_POINTER, "a required pointer is null");
+  if (!batch || !len || !heads || !half)
+    return fail(ARM_SCAN_ERR_INVALID_DIMS, "a dimension is zero");
+  if (n_angles > half)
+    return fail(ARM_SCAN_ERR_INVALID_DIMS, "n_angles (%zu) exceeds the pairs (%zu)", n_angles,
+                half);
+  if (!prod_ok({batch, len, heads, half}) || len > (1u << 30) || heads > (1u << 30))
+    return fail(ARM_SCAN_ERR_INVALID_DIMS, "dims overflow");
+  return run(armscan::m3_angles_to_cos_sin(angles, dt, batch, len, heads, n_angles, half, cos,
+                                           sin, (hipStream_t)stream),
+             "angle pre-pass launch");
 }
 
 int arm_scan_ss2d_f32(const ArmSS2DDims* dims, const float* u, const float* delta,

@@ -62,7 +62,9 @@ constexpr int kRecEc = 256;      // e^{c_i}
 constexpr int kRecW = 272;       // w_s
 constexpr int kRecEtot = 288;    // e^{c_last}
 constexpr int kRecFloats = 292;  // + 3 floats of padding: whole 16-byte pieces
-constexpr int kRecPieces = kRecFloats / 4;
+// With the angle pre-pass fused: pi * dt of each row follows (16 floats).
+constexpr int kRecPdt = 292;
+constexpr int kRecFloatsAng = 308;
 
 constexpr int kMaxWaves = 8;   // n-tiles per block: dqk <= 128
 constexpr int kKtStride = 20;  // floats per row of a wave's K transpose tile
@@ -80,6 +82,11 @@ struct M3K {
   int n_cs, n_v, n_z;  // cos (and again sin), v, z
   int n_ins;           // all sections, + 2 for the gate record
   int stage_floats;
+  // the fused angle pre-pass (m3_chunk_kernel<.., ANG>): raw angles (b, l, h, nang)
+  // replace cos/sin (n_cs = 0) in n_ang DMA instructions per stage
+  const float* ang;
+  int nang, n_ang;
+  int rec_floats;  // kRecFloats, or kRecFloatsAng with pi * dt per row
 };
 
 // ---------------------------------------------------------------------------
@@ -99,11 +106,12 @@ __global__ void __launch_bounds__(256) m3_gates_kernel(M3K p, int reverse) {
   }
   const int step = row / R;
   const long long g = (long long)ch * T + step;
-  float a = 0.0f, gamma = 0.0f, scale = 0.0f;
+  float a = 0.0f, gamma = 0.0f, scale = 0.0f, pdt = 0.0f;
   if (valid && g < L) {
     const long long base = (long long)seq * L;  // gates are (b, h, l): seq = b*heads + h
     const long long t = reverse ? L - 1 - g : g;
     a = p.adt[base + t];
+    pdt = 3.14159265358979f * p.dt[base + t];
     gamma = p.dt[base + t] * sigmoid(p.trap[base + t]);
     scale = gamma;
     if (g + 1 < L) {
@@ -128,7 +136,8 @@ __global__ void __launch_bounds__(256) m3_gates_kernel(M3K p, int reverse) {
     m[s] = step_s < step ? fexp(c - cs) * ss : (step_s == step ? gamma : 0.0f);
   }
   if (!valid) return;
-  float* rec = p.rec + cidx * kRecFloats;
+  float* rec = p.rec + cidx * p.rec_floats;
+  if (p.rec_floats > kRecFloats) rec[kRecPdt + row] = pdt;  // 0 past the end: theta holds
   f4* mrow = reinterpret_cast<f4*>(rec + kRecM + row * 16);
 #pragma unroll
   for (int q = 0; q < 4; ++q) mrow[q] = f4{m[4 * q], m[4 * q + 1], m[4 * q + 2], m[4 * q + 3]};
@@ -174,18 +183,19 @@ __device__ __forceinline__ f2 ld2(const float* p) { return *reinterpret_cast<con
 
 // Base pointers of a block's sequence.
 struct SeqIn {
-  const float *q, *k, *cos, *sin, *v, *z, *rec;
-  int qstride, csstride, vstride;  // floats per step
+  const float *q, *k, *cos, *sin, *ang, *v, *z, *rec;
+  int qstride, csstride, angstride, vstride;  // floats per step
 };
 
 // DMA instruction `ins` of a stage (1 KB, one 16-byte piece per lane). Stage
 // layout in pieces, each section padded to whole instructions:
 //   q, k: piece (nt, lj, li) = columns nt*16 + 4lj .. +3 of row li
 //   cos, sin: piece u4*T + step = angles 4u4 .. 4u4+3 of the step
+//   or, fused, the raw angles: piece u4*T + step = angles 4u4 .. 4u4+3 of the step
 //   v, z: piece step*4PT + c4 = columns p0 + 4c4 .. +3 of the step
 //   gate record: its 73 pieces in order
 // The lane's piece of chunk ch is src + t*stride + col with t the memory row of
-// step `step` of the chunk, or src + ch*kRecFloats + col for the gate record.
+// step `step` of the chunk, or src + ch*rec_floats + col for the gate record.
 struct DmaPiece {
   const float* src;
   int step, col, stride;
@@ -216,7 +226,14 @@ __device__ __forceinline__ DmaPiece dma_decode(const M3K& p, const SeqIn& s, int
     d.step = j % T;
     d.col = 4 * (j / T);
     d.stride = s.csstride;
-  } else if ((rel -= 2 * p.n_cs) < p.n_v + p.n_z) {
+  } else if ((rel -= 2 * p.n_cs) < p.n_ang) {
+    const int j = rel * 64 + lane;
+    d.on = j < T * (p.nang / 4);
+    d.src = s.ang;
+    d.step = j % T;
+    d.col = 4 * (j / T);
+    d.stride = s.angstride;
+  } else if ((rel -= p.n_ang) < p.n_v + p.n_z) {
     const bool zz = rel >= p.n_v;
     const int j = (zz ? rel - p.n_v : rel) * 64 + lane;
     const int w4 = 4 * p.ptiles;
@@ -227,7 +244,7 @@ __device__ __forceinline__ DmaPiece dma_decode(const M3K& p, const SeqIn& s, int
     d.stride = s.vstride;
   } else {
     const int j = (rel - p.n_v - p.n_z) * 64 + lane;
-    d.on = j < kRecPieces;
+    d.on = j < p.rec_floats / 4;
     d.src = s.rec;
     d.col = 4 * j;
     d.rec = true;
@@ -272,7 +289,7 @@ __device__ __forceinline__ void dma_plan(const M3K& p, const SeqIn& s, int first
       d.on[k] = pc.on;
       if (pc.rec) {
         d.base[k] = pc.src;
-        d.delta[k] = kRecFloats;
+        d.delta[k] = p.rec_floats;
         d.off[k] = pc.col;
       } else if (!REV) {
         d.base[k] = pc.src;
@@ -310,7 +327,7 @@ __device__ __forceinline__ void dma_clamped(const M3K& p, const SeqIn& s, const 
     int g = ch * T + pc.step;
     g = g < L - 1 ? g : L - 1;
     const int t = REV ? L - 1 - g : g;
-    const long long o = pc.rec ? (long long)ch * kRecFloats + pc.col
+    const long long o = pc.rec ? (long long)ch * p.rec_floats + pc.col
                                : (long long)t * pc.stride + pc.col;
     dma16(pc.src + o, stage + d.ins[k] * 256);
   }
@@ -348,6 +365,38 @@ __device__ __forceinline__ f4 rope(f4 x, f4 y, f4 bx, f4 by, f4 c, f4 s, bool lo
                  y[2] * s[2] + x[2] * c[2], y[3] * s[3] + x[3] * c[3]};
 }
 
+// tanh(a) = 1 - 2 / (1 + e^{2a}); saturates to +-1 through e^{2a} = inf or 0.
+__device__ __forceinline__ float tanh_fast(float a) {
+  return 1.0f - 2.0f * __builtin_amdgcn_rcpf(1.0f + fexp(2.0f * a));
+}
+
+// The angle pre-pass fused (python/arm_scan/mamba3.py:41-89: theta =
+// cumsum_l(tanh(angle) * pi * dt), then cos/sin), for NA rotation pairs of the
+// lane at row li of the chunk: the increments of rows li - R, li - 2R, .. (the
+// earlier steps, same rank) are summed by a DPP row scan, the chunk's start
+// angle `carry` is added, and the carry moves to the angle at the chunk's last
+// step. cos/sin by the hardware functions of revolutions after reducing theta/2pi
+// to [-1/2, 1/2]. All 64 lanes take part (the row scan and the carry's shuffle).
+template <int R, int NA>
+__device__ __forceinline__ void fused_angles(const float (&a)[NA], float pdt, int li,
+                                             int lane, float (&carry)[NA], float (&cs)[NA],
+                                             float (&sn)[NA]) {
+#pragma unroll
+  for (int e = 0; e < NA; ++e) {
+    float t = tanh_fast(a[e]) * pdt;
+    if (R <= 1) t += dpp<kRowShr1, 0xF>(0.0f, t);
+    if (R <= 2) t += dpp<kRowShr2, 0xF>(0.0f, t);
+    if (R <= 4) t += dpp<kRowShr4, 0xF>(0.0f, t);
+    t += dpp<kRowShr8, 0xF>(0.0f, t);
+    const float theta = carry[e] + t;
+    carry[e] = __shfl(theta, (lane & ~15) | (16 - R + li % R));
+    const float x = theta * 0.15915494309189535f;  // revolutions
+    const float f = x - __builtin_rintf(x);
+    cs[e] = __builtin_amdgcn_cosf(f);
+    sn[e] = __builtin_amdgcn_sinf(f);
+  }
+}
+
 // What a chunk's epilogue needs from its stage, kept in registers so that the
 // stage can be refilled before the epilogue runs.
 struct Stash {
@@ -360,14 +409,20 @@ struct Stash {
 // Waves 0 .. WN-1 compute the partials of n-tile `wave` for every slice of the
 // block; waves WN .. WN+PT-1 finish slice wave-WN of the previous chunk. Both kinds
 // pass one barrier per chunk.
-template <int R, bool MIMO, bool REV, int PT>
+template <int R, bool MIMO, bool REV, int PT, bool ANG>
 __global__ void __launch_bounds__(64 * (kMaxWaves + 2)) m3_chunk_kernel(M3K p) {
   extern __shared__ __attribute__((aligned(16))) float sm[];
   const int WN = p.dqk / 16;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const bool ewave = wave >= WN;                    // epilogue wave
-  const int nt = ewave ? 0 : wave;                  // n-tile of a partial wave
+  // n-tile of a partial wave. MIMO with fused angles interleaves the halves (wave
+  // 2i: n-tile i, 2i+1: WN/2 + i): the n-tiles holding the angle pairs below nang
+  // then sit on different SIMDs (waves go to SIMDs round-robin).
+  const int nt = ewave ? 0
+                       : (MIMO && ANG && WN % 2 == 0)
+                             ? ((wave & 1) ? WN / 2 + (wave >> 1) : (wave >> 1))
+                             : wave;
   const int ej = ewave ? wave - WN : 0;             // slice of an epilogue wave
   const int li = lane & 15, lj = lane >> 4;
   // blocks of one sequence share an XCD (block id mod 8), and so its L2
@@ -391,7 +446,8 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 2)) m3_chunk_kernel(M3K p) {
   float* ybuf = gbuf + 2 * kMaxWaves * 256;     // [2][PT][kMaxWaves][64][4]
   float* kt = ybuf + 2 * PT * kMaxWaves * 256 + nt * 16 * kKtStride;
   const int off_k = WN * 256, off_cs = 2 * WN * 256;
-  const int off_sn = off_cs + p.n_cs * 256, off_v = off_cs + 2 * p.n_cs * 256;
+  const int off_sn = off_cs + p.n_cs * 256, off_ang = off_cs + 2 * p.n_cs * 256;
+  const int off_v = off_ang + p.n_ang * 256;
   const int off_z = off_v + p.n_v * 256, off_rec = off_z + p.n_z * 256;
 
   if (WN < kMaxWaves) {
@@ -484,9 +540,11 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 2)) m3_chunk_kernel(M3K p) {
   in.sin = p.sin + ((long long)bi * L * H + h) * half;
   in.v = p.v + ((long long)bi * L * H + h) * dv + p0;
   in.z = p.z ? p.z + ((long long)bi * L * H + h) * dv + p0 : nullptr;
-  in.rec = p.rec + (long long)seq * p.nchunks * kRecFloats;
+  in.ang = ANG ? p.ang + ((long long)bi * L * H + h) * p.nang : nullptr;
+  in.rec = p.rec + (long long)seq * p.nchunks * p.rec_floats;
   in.qstride = R * p.groups * dqk;
   in.csstride = H * half;
+  in.angstride = H * p.nang;
   in.vstride = H * dv;
 
   // biases of the lane's columns (row li has rank li % R)
@@ -520,6 +578,9 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 2)) m3_chunk_kernel(M3K p) {
 #pragma unroll
   for (int j = 0; j < PT; ++j) S[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
   f4 kr_last = {0.0f, 0.0f, 0.0f, 0.0f};
+  // fused angles: theta before the chunk of the pairs the lane computes
+  float carry[2] = {0.0f, 0.0f};       // SISO: 2 per lane
+  float carry_m[4 / R] = {};           // MIMO: 4/R per lane
   for (int ch = 0; ch < p.nchunks; ++ch) {
     // Stage ch has landed once no more of this wave's DMA is outstanding than the
     // stages issued after it.
@@ -536,7 +597,44 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 2)) m3_chunk_kernel(M3K p) {
     const f4 q = ld4(sg + (nt * 64 + lane) * 4);
     const f4 k = ld4(sg + off_k + (nt * 64 + lane) * 4);
     f4 qp = {0.0f, 0.0f, 0.0f, 0.0f}, kp = qp, cs, sn;
-    if (MIMO) {
+    if (ANG) {
+      // pairs 4u4 .. 4u4+3 of the lane (MIMO) or 2 at 8nt + 2lj (SISO); past nang 0
+      const int u4 = MIMO ? (lo ? n0 : n0 - half) >> 2 : 2 * nt + (lj >> 1);
+      const bool have = 4 * u4 < p.nang;
+      if ((MIMO ? (16 * nt) % half : 8 * nt) >= p.nang) {
+        // every pair of the wave is past nang (wave-uniform): the identity rotation
+        cs = f4{1.0f, 1.0f, 1.0f, 1.0f};
+        sn = f4{0.0f, 0.0f, 0.0f, 0.0f};
+      } else if (MIMO) {
+        // the R lanes of a step (ranks) need the same four angles: each computes
+        // 4/R of them, pair e = (li % R) * NC + c, and gathers the rest
+        constexpr int NC = 4 / R;
+        float a[NC], c[NC], sv[NC];
+#pragma unroll
+        for (int j = 0; j < NC; ++j)
+          a[j] = have ? sg[off_ang + (u4 * T + step_i) * 4 + (li % R) * NC + j] : 0.0f;
+        fused_angles<R, NC>(a, sg[off_rec + kRecPdt + li], li, lane, carry_m, c, sv);
+        const int src = lane - li % R;  // the step's first lane
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          cs[e] = NC == 4 ? c[e % NC] : __shfl(c[e % NC], src + e / NC);
+          sn[e] = NC == 4 ? sv[e % NC] : __shfl(sv[e % NC], src + e / NC);
+        }
+      } else {
+        float a[2], c[2], sv[2];
+        const f2 a2 = have ? ld2(sg + off_ang + (u4 * T + li) * 4 + 2 * (lj & 1)) : f2{0, 0};
+        a[0] = a2[0];
+        a[1] = a2[1];
+        fused_angles<R, 2>(a, sg[off_rec + kRecPdt + li], li, lane, carry, c, sv);
+        cs = f4{c[0], c[1], 0.0f, 0.0f};
+        sn = f4{sv[0], sv[1], 0.0f, 0.0f};
+      }
+      if (MIMO) {
+        const int pl = ((m0 >> 4) * 64 + ((m0 & 15) >> 2) * 16 + li) * 4;
+        qp = ld4(sg + pl);
+        kp = ld4(sg + off_k + pl);
+      }
+    } else if (MIMO) {
       const int pl = ((m0 >> 4) * 64 + ((m0 & 15) >> 2) * 16 + li) * 4;
       qp = ld4(sg + pl);
       kp = ld4(sg + off_k + pl);
@@ -619,12 +717,17 @@ hipError_t launch_chunk(const M3K& k, bool rev, hipStream_t st) {
   const int WN = k.dqk / 16;
   const long long blocks = 8LL * (k.nparts / PT) * ((k.nseq + 7) / 8);
   const size_t lds = chunk_lds_bytes(k, PT, k.nstages);
-  if (rev)
-    hipLaunchKernelGGL((m3_chunk_kernel<R, MIMO, true, PT>), dim3((unsigned)blocks),
+  if (k.ang) {  // forward only: theta is a forward cumsum
+    if (rev) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((m3_chunk_kernel<R, MIMO, false, PT, true>), dim3((unsigned)blocks),
                        dim3(64 * (WN + PT)), lds, st, k);
-  else
-    hipLaunchKernelGGL((m3_chunk_kernel<R, MIMO, false, PT>), dim3((unsigned)blocks),
+  } else if (rev) {
+    hipLaunchKernelGGL((m3_chunk_kernel<R, MIMO, true, PT, false>), dim3((unsigned)blocks),
                        dim3(64 * (WN + PT)), lds, st, k);
+  } else {
+    hipLaunchKernelGGL((m3_chunk_kernel<R, MIMO, false, PT, false>), dim3((unsigned)blocks),
+                       dim3(64 * (WN + PT)), lds, st, k);
+  }
   return hipGetLastError();
 }
 
@@ -664,12 +767,16 @@ hipError_t m3_scan_chunked(const M3Problem& pr, hipStream_t st) {
   const int WN = k.dqk / 16;
   // Two dv slices per block share the q/k/cos/sin rows and G when dv allows.
   k.ptiles = (k.nparts % 2 == 0 && WN >= 2) ? 2 : 1;
+  k.ang = pr.angles;
+  k.nang = (int)pr.n_angles;
+  k.rec_floats = pr.angles ? kRecFloatsAng : kRecFloats;
   auto plan = [&]() {
     const int T = k.steps_per_chunk;
-    k.n_cs = (T * (k.dqk / 8) + 63) / 64;
+    k.n_cs = pr.angles ? 0 : (T * (k.dqk / 8) + 63) / 64;
+    k.n_ang = pr.angles ? (T * (k.nang / 4) + 63) / 64 : 0;
     k.n_v = (T * 4 * k.ptiles + 63) / 64;
     k.n_z = pr.z ? k.n_v : 0;
-    k.n_ins = 2 * WN + 2 * k.n_cs + k.n_v + k.n_z + (kRecPieces + 63) / 64;
+    k.n_ins = 2 * WN + 2 * k.n_cs + k.n_ang + k.n_v + k.n_z + (k.rec_floats / 4 + 63) / 64;
     k.stage_floats = k.n_ins * 256;
   };
   plan();
@@ -683,7 +790,7 @@ hipError_t m3_scan_chunked(const M3Problem& pr, hipStream_t st) {
   if (k.n_ins > kMaxDma * WN) return hipErrorInvalidValue;  // DMA by the WN partial waves
 
   const size_t nrec = (size_t)k.nseq * k.nchunks;
-  hipError_t e = stream_alloc((void**)&k.rec, nrec * kRecFloats * sizeof(float), st);
+  hipError_t e = stream_alloc((void**)&k.rec, nrec * k.rec_floats * sizeof(float), st);
   if (e != hipSuccess) return e;
   const unsigned gblocks = (unsigned)((nrec + 15) / 16);
   const int rev = pr.reverse ? 1 : 0;

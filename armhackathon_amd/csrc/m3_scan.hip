@@ -175,12 +175,36 @@ size_t m3_max_state() { return kM3MaxLdsFloats; }
 
 static bool aligned16(const void* q) { return q == nullptr || ((uintptr_t)q & 15u) == 0; }
 
+namespace {
+bool m3_aligned(const M3Problem& pr) {
+  return aligned16(pr.q) && aligned16(pr.k) && aligned16(pr.q_bias) &&
+         aligned16(pr.k_bias) && aligned16(pr.cos) && aligned16(pr.sin) &&
+         aligned16(pr.angles) && aligned16(pr.v) && aligned16(pr.z) &&
+         aligned16(pr.last_state) && aligned16(pr.last_bx);
+}
+}  // namespace
+
+bool m3_angles_supported(const M3Problem& pr, const char** why) {
+  auto no = [&](const char* w) {
+    if (why) *why = w;
+    return false;
+  };
+  if (pr.reverse) return no("fused angles are forward only (theta is a forward cumsum)");
+  if (pr.n_angles == 0 || pr.n_angles % 4 || pr.n_angles > pr.dqk / 2)
+    return no("fused angles need n_angles a positive multiple of 4, at most dqk/2");
+  if (!m3_aligned(pr)) return no("fused angles need 16-byte aligned inputs");
+  if (!m3_chunk_supported(pr)) return no("fused angles need the chunked kernel's shapes");
+  if (pr.len * pr.heads * pr.n_angles >= ((size_t)1 << 30))
+    return no("angles span too large for 32-bit offsets");
+  return true;
+}
+
 hipError_t m3_scan(const M3Problem& pr, hipStream_t st) {
-  const bool aligned = aligned16(pr.q) && aligned16(pr.k) && aligned16(pr.q_bias) &&
-                       aligned16(pr.k_bias) && aligned16(pr.cos) && aligned16(pr.sin) &&
-                       aligned16(pr.v) && aligned16(pr.z) && aligned16(pr.last_state) &&
-                       aligned16(pr.last_bx);
-  if (aligned && m3_chunk_supported(pr)) return m3_scan_chunked(pr, st);
+  if (pr.angles) {
+    if (!m3_angles_supported(pr, nullptr)) return hipErrorInvalidValue;
+    return m3_scan_chunked(pr, st);
+  }
+  if (m3_aligned(pr) && m3_chunk_supported(pr)) return m3_scan_chunked(pr, st);
   return m3_scan_sequential(pr, st);
 }
 

@@ -66,11 +66,23 @@ struct M3Problem {
   float *out, *last_state, *last_bx;
   int reverse;
   int out_time_major;  // out (b, l, h, dv) instead of head-major (b, h, l, dv)
+  // raw angles (b, l, h, n_angles) in place of cos/sin: the pre-pass fused
+  const float* angles;
+  size_t n_angles;
 };
 
 // Largest dv * dqk the Mamba-3 kernel holds on chip.
 size_t m3_max_state();
 hipError_t m3_scan(const M3Problem& p, hipStream_t st);
+// The RoPE angle pre-pass: angles (batch, len, heads, r), dt (batch, heads, len) ->
+// cos, sin (batch, len, heads, half), theta = cumsum_len(tanh(angle) pi dt), pairs past
+// r the identity (m3_angles.hip).
+hipError_t m3_angles_to_cos_sin(const float* angles, const float* dt, size_t batch,
+                                size_t len, size_t heads, size_t r, size_t half, float* cos,
+                                float* sin, hipStream_t st);
+// Whether m3_scan serves raw angles for this problem (the chunked kernel, forward,
+// n_angles a multiple of 4 up to dqk/2, 16-byte aligned inputs); else *why says why.
+bool m3_angles_supported(const M3Problem& p, const char** why);
 // One workgroup per (batch, head), step by step (any shape).
 hipError_t m3_scan_sequential(const M3Problem& p, hipStream_t st);
 // The chunked MFMA path (m3_chunk.hip): dv, dqk multiples of 16, rank 1/2/4.

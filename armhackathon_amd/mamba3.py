@@ -32,12 +32,27 @@ def angles_to_cos_sin(angles: torch.Tensor, dt: torch.Tensor,
     """theta = cumsum_L(tanh(angle) * pi * dt) -> (cos, sin), each (b, l, h, half)
     (python/arm_scan/mamba3.py:41-89). angles (b, l, h, r) raw, dt (b, h, l)
     post-softplus; pairs past r get the identity rotation (cos 1, sin 0).
-    Computed at the caller's precision, floored at float32."""
+    float32 device tensors go through the HIP pre-pass (arm_scan_mamba3_angles_f32);
+    other dtypes are computed in torch at the caller's precision, floored at float32,
+    as the reference does for float64 analysis."""
     if angles.dim() != 4:
         raise ValueError(f"angles must be (b, l, h, r), got {tuple(angles.shape)}")
     r = angles.shape[-1]
     if r > half:
         raise ValueError(f"angles has {r} rotation pairs but the head dim allows {half}")
+    if (angles.device.type == "cuda" and angles.dtype == torch.float32
+            and dt.dtype == torch.float32 and dt.device == angles.device):
+        # the HIP pre-pass: one kernel, angles and dt read once, cos/sin written once
+        b, length, h, _ = angles.shape
+        if tuple(dt.shape) != (b, h, length):
+            raise ValueError(f"dt must be {(b, h, length)}, got {tuple(dt.shape)}")
+        a, d = angles.contiguous(), dt.contiguous()
+        cos = torch.empty((b, length, h, half), dtype=torch.float32, device=a.device)
+        sin = torch.empty_like(cos)
+        with torch.cuda.device(a.device):
+            _ffi.angles_raw(a.data_ptr(), d.data_ptr(), b, length, h, r, half, cos.data_ptr(),
+                            sin.data_ptr(), stream=_stream(a.device))
+        return cos, sin
     dtype = torch.promote_types(angles.dtype, torch.float32)
     dt_blh = dt.permute(0, 2, 1).unsqueeze(-1).to(dtype)
     theta = torch.cumsum(torch.tanh(angles.to(dtype)) * math.pi * dt_blh, dim=1)
@@ -81,6 +96,81 @@ def _run(q, k, v, adt, dt, trap, q_bias, k_bias, cos, sin, d_skip, z, reverse, p
     return out, last_state, last_bx
 
 
+def _run_angles(q, k, v, adt, dt, trap, q_bias, k_bias, angles, d_skip, z, psi, zeta, phi,
+                want_state):
+    """Forward scan with the angle pre-pass fused into the kernel
+    (arm_scan_mamba3_scan_angles_f32): raw angles instead of cos/sin."""
+    dev = _device_of(q, k, v, adt, dt, trap, q_bias, k_bias, angles, d_skip, z, psi, zeta,
+                     phi)
+    mimo = psi is not None
+    if mimo:
+        b, length, rank, groups, dqk = q.shape
+    else:
+        b, length, groups, dqk = q.shape
+        rank = 1
+    h, dv = v.shape[2], v.shape[3]
+    dims = _ffi.ArmMamba3Dims(b, h, dv, dqk, length, rank, groups)
+    out = torch.empty((b, length, h, dv), dtype=torch.float32, device=dev)
+    last_state = torch.empty((b, h, dv, dqk), dtype=torch.float32, device=dev) \
+        if want_state else None
+    last_bx = torch.empty((b, h, dqk), dtype=torch.float32, device=dev) \
+        if (want_state and not mimo) else None
+    with torch.cuda.device(dev):
+        _ffi.mamba3_angles_raw(
+            dims,
+            [q.data_ptr(), k.data_ptr(), v.data_ptr(), adt.data_ptr(), dt.data_ptr(),
+             trap.data_ptr(), q_bias.data_ptr(), k_bias.data_ptr(), angles.data_ptr(),
+             _ptr(d_skip), _ptr(z), _ptr(psi), _ptr(zeta), _ptr(phi)],
+            angles.shape[-1], _ffi.BACKENDS["auto"], _ffi.THREADING["auto"],
+            out.data_ptr(), _ptr(last_state), _ptr(last_bx), stream=_stream(dev))
+    _CALLS["n"] += 1
+    return out, last_state, last_bx
+
+
+def _angles_fusable(angles, cos, sin, reverse, q, k, v, q_bias, k_bias, z, rank):
+    """Whether the fused pre-pass serves this call: the conditions
+    arm_scan_mamba3_scan_angles_f32 declares (forward; angle pairs a positive
+    multiple of 4 up to dqk/2; dv, dqk multiples of 16, dqk <= 128; rank 1, 2 or 4;
+    16-byte aligned tensors)."""
+    if angles is None or cos is not None or sin is not None or reverse or angles.dim() != 4:
+        return False
+    dqk, dv, r = q.shape[-1], v.shape[-1], angles.shape[-1]
+    if r == 0 or r % 4 or r > dqk // 2 or dv % 16 or dqk % 16 or dqk > 128:
+        return False
+    if rank not in (1, 2, 4):
+        return False
+    return all(t.data_ptr() % 16 == 0 for t in (q, k, v, q_bias, k_bias, angles)
+               if t is not None) and (z is None or z.data_ptr() % 16 == 0)
+
+
+@torch.library.custom_op("arm_scan::mamba3_scan_angles", mutates_args=())
+def _mamba3_scan_angles_op(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    adt: torch.Tensor,
+    dt: torch.Tensor,
+    trap: torch.Tensor,
+    q_bias: torch.Tensor,
+    k_bias: torch.Tensor,
+    angles: torch.Tensor,
+    d_skip: Optional[torch.Tensor],
+    z: Optional[torch.Tensor],
+    psi: Optional[torch.Tensor] = None,
+    zeta: Optional[torch.Tensor] = None,
+    phi: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    out, _, _ = _run_angles(q, k, v, adt, dt, trap, q_bias, k_bias, angles, d_skip, z, psi,
+                            zeta, phi, False)
+    return out
+
+
+@_mamba3_scan_angles_op.register_fake
+def _(q, k, v, adt, dt, trap, q_bias, k_bias, angles, d_skip, z, psi=None, zeta=None,
+      phi=None):
+    return q.new_empty((q.shape[0], q.shape[1], v.shape[2], v.shape[3]))
+
+
 @torch.library.custom_op("arm_scan::mamba3_scan", mutates_args=())
 def _mamba3_scan_op(
     q: torch.Tensor,
@@ -112,7 +202,7 @@ def _(q, k, v, adt, dt, trap, q_bias, k_bias, cos, sin, d_skip, z, reverse,
 
 
 def _check_shapes(q, k, v, adt, dt, trap, q_bias, k_bias, cos, sin, D, z,
-                  rank=None, psi=None, zeta=None, phi=None):
+                  rank=None, psi=None, zeta=None, phi=None, angles=None):
     """Every tensor against the layout contract (python/arm_scan/mamba3.py:153-195):
     a short buffer would be an out-of-bounds read on the device."""
     if v.dim() != 4:
@@ -134,10 +224,13 @@ def _check_shapes(q, k, v, adt, dt, trap, q_bias, k_bias, cos, sin, D, z,
         raise ValueError(f"q/k groups ({g}) must divide the head count ({h})")
     half = dqk // 2
     want = {"q": qshape, "k": qshape, "adt": (b, h, length), "dt": (b, h, length),
-            "trap": (b, h, length), "q_bias": bshape, "k_bias": bshape,
-            "cos": (b, length, h, half), "sin": (b, length, h, half)}
-    got = dict(q=q, k=k, adt=adt, dt=dt, trap=trap, q_bias=q_bias, k_bias=k_bias, cos=cos,
-               sin=sin)
+            "trap": (b, h, length), "q_bias": bshape, "k_bias": bshape}
+    got = dict(q=q, k=k, adt=adt, dt=dt, trap=trap, q_bias=q_bias, k_bias=k_bias)
+    if cos is not None:
+        want["cos"], got["cos"] = (b, length, h, half), cos
+        want["sin"], got["sin"] = (b, length, h, half), sin
+    if angles is not None:
+        want["angles"], got["angles"] = (b, length, h, angles.shape[-1]), angles
     if D is not None:
         want["D"], got["D"] = (h,), D
     if z is not None:
@@ -180,6 +273,19 @@ def mamba3_scan(q, k, v, adt, dt, trap, q_bias, k_bias, angles=None,
         q = q.unsqueeze(2)
     if k.dim() == 3:
         k = k.unsqueeze(2)
+    q, k, v = _c(q), _c(k), _c(v)
+    q_bias, k_bias = _c(q_bias), _c(k_bias)
+    z = None if z is None else _c(z)
+    angles = None if angles is None else _c(angles)
+    if _angles_fusable(angles, cos, sin, reverse, q, k, v, q_bias, k_bias, z, 1):
+        # the angle pre-pass runs inside the scan kernel
+        _check_shapes(q, k, v, adt, dt, trap, q_bias, k_bias, None, None, D, z,
+                      angles=angles)
+        args = (q, k, v, _c(adt), _c(dt), _c(trap), q_bias, k_bias, angles,
+                None if D is None else _c(D), z)
+        if not return_last_state:
+            return _mamba3_scan_angles_op(*args)
+        return _run_angles(*args, None, None, None, True)
     cos, sin = _cos_sin(angles, cos, sin, dt, q.shape[-1] // 2)
     _check_shapes(q, k, v, adt, dt, trap, q_bias, k_bias, cos, sin, D, z)
     args = (_c(q), _c(k), _c(v), _c(adt), _c(dt), _c(trap), _c(q_bias), _c(k_bias), _c(cos),
@@ -218,6 +324,9 @@ def mamba3_mimo_scan(q, k, v, adt, dt, trap, q_bias, k_bias, psi, zeta, phi,
     if k.dim() == 4:
         k = k.unsqueeze(3)
     rank = q.shape[2]
+    # From raw angles MIMO takes the HIP pre-pass and the scan on cos/sin: with
+    # 16/rank-step chunks the fused pre-pass lengthens every iteration of a loop that
+    # is latency-bound (arm_scan_mamba3_scan_angles_f32 still serves it).
     cos, sin = _cos_sin(angles, cos, sin, dt, q.shape[-1] // 2)
     _check_shapes(q, k, v, adt, dt, trap, q_bias, k_bias, cos, sin, D, z, rank=rank,
                   psi=psi, zeta=zeta, phi=phi)

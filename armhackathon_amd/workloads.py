@@ -80,6 +80,19 @@ def m3_mimo(batch=4, length=4096, heads=24, dv=64, dqk=128, rank=4, seed=0):
     return x
 
 
+def m3_with_angles(x, r=None, seed=0):
+    """`x` (from m3_siso / m3_mimo) with raw rotary angles (b, l, h, r) in place of
+    cos/sin, for the fused pre-pass: angle ~ N(0,1), so tanh(angle) * pi * dt is a
+    spread of increments within (-pi, pi) * dt. r defaults to dqk/4, the published
+    rotation fraction of 0.5 (python/arm_scan/mamba3.py:49-52)."""
+    b, length, h = x["v"].shape[:3]
+    r = x["q"].shape[-1] // 4 if r is None else r
+    rng = np.random.default_rng(seed)
+    y = {k: v for k, v in x.items() if k not in ("cos", "sin")}
+    y["angles"] = rng.standard_normal((b, length, h, r), dtype=F32)
+    return y
+
+
 def ss2d(batch=16, dim=192, height=64, width=64, state=16, seed=0):
     rng = np.random.default_rng(seed)
     shape = (batch, dim, height, width)

@@ -50,7 +50,8 @@ def parse():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
-    ap.add_argument("--workload", choices=("m1", "m1_seam", "m3_siso", "m3_mimo", "ss2d"),
+    ap.add_argument("--workload", choices=("m1", "m1_seam", "m3_siso", "m3_mimo", "ss2d",
+                                           "m3_siso_angles", "m3_mimo_angles"),
                     default="m1",
                     help="m1 (default): the headline line below; the others time one of the "
                          "configs 3-5, or the config-2 scan in the HF mixer's layouts "
@@ -128,6 +129,11 @@ def config_inputs(name, dev):
         proj[..., d:] = t["z"].transpose(1, 2)
         t["z"] = proj.transpose(1, 2)[:, d:]
         return t, workloads.m1_bytes(b, d, L, n, z=True, D=True, bias=True, last_state=True)
+    if name in ("m3_siso_angles", "m3_mimo_angles"):
+        base = workloads.m3_siso(seed=3) if name == "m3_siso_angles" else \
+            workloads.m3_mimo(seed=4)
+        x = workloads.m3_with_angles(base, seed=6)
+        return {k: torch.from_numpy(v).to(dev) for k, v in x.items()}, workloads.m3_bytes(x)
     if name == "m3_siso":
         x = workloads.m3_siso(seed=3)
         nbytes = workloads.m3_bytes(x)
@@ -145,6 +151,8 @@ CONFIG_NAMES = {
                "D, z read in place from the mixer's (b, L, 2D) projection, out written "
                "time-major",
     "m3_siso": "config 3: Mamba-3 SISO B4 L4096 24 heads x 64, dqk 128 (final states too)",
+    "m3_siso_angles": "config 3 from raw angles (b, l, h, 32): the angle pre-pass fused",
+    "m3_mimo_angles": "config 4 from raw angles (b, l, h, 32): the angle pre-pass fused",
     "m3_mimo": "config 4: Mamba-3 MIMO rank 4, B4 L4096 24 heads x 64, dqk 128 (final state)",
     "ss2d": "config 5: SS2D 4 directions, B16 D192 64x64 N16, D, z, merge sum (final states)",
 }
@@ -164,6 +172,15 @@ def bench_config(name, dev, steps, warmup):
             return arm_scan.selective_scan_time_major(
                 t["u"], t["delta"], t["A"], t["B"], t["C"], D=t["D"], z=t["z"],
                 delta_bias=t["delta_bias"], delta_softplus=True, return_last_state=True)
+    elif name == "m3_siso_angles":
+        def call():
+            return arm_scan.mamba3_scan(*[t[k] for k in K], angles=t["angles"],
+                                        return_last_state=True)
+    elif name == "m3_mimo_angles":
+        def call():
+            return arm_scan.mamba3_mimo_scan(*[t[k] for k in K], t["psi"], t["zeta"],
+                                             t["phi"], angles=t["angles"],
+                                             return_last_state=True)
     elif name == "m3_siso":
         def call():
             return arm_scan.mamba3_scan(*[t[k] for k in K], cos=t["cos"], sin=t["sin"],
@@ -189,10 +206,33 @@ def bench_config(name, dev, steps, warmup):
     torch.cuda.synchronize()
     ms = start.elapsed_time(stop) / steps
     gbs = nbytes / (ms * 1e-3) / 1e9
+    extra = {}
+    if name.endswith("_angles"):
+        # the same call through the unfused route: the pre-pass in torch ops, then
+        # the scan on cos/sin (what the reference's Python layer does)
+        from armhackathon_amd.mamba3 import angles_to_cos_sin
+
+        def unfused():
+            cos, sin = angles_to_cos_sin(t["angles"], t["dt"], t["q"].shape[-1] // 2)
+            if name == "m3_siso_angles":
+                return arm_scan.mamba3_scan(*[t[k] for k in K], cos=cos, sin=sin,
+                                            return_last_state=True)
+            return arm_scan.mamba3_mimo_scan(*[t[k] for k in K], t["psi"], t["zeta"],
+                                             t["phi"], cos=cos, sin=sin,
+                                             return_last_state=True)
+        for _ in range(warmup):
+            unfused()
+        start.record(stream)
+        for _ in range(steps):
+            unfused()
+        stop.record(stream)
+        torch.cuda.synchronize()
+        extra["unfused_ms_per_call"] = round(start.elapsed_time(stop) / steps, 4)
     del t
     torch.cuda.empty_cache()
     return dict(workload=CONFIG_NAMES[name], ms_per_call=round(ms, 4), bytes_per_call=nbytes,
-                gbs=round(gbs, 2), frac_of_8tbs=round(gbs / HBM_PEAK_GBS, 4), steps=steps)
+                gbs=round(gbs, 2), frac_of_8tbs=round(gbs / HBM_PEAK_GBS, 4), steps=steps,
+                **extra)
 
 
 def bench_config_cpu(name, seconds):

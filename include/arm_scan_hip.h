@@ -14,7 +14,11 @@
  *   - ArmMamba3Dims gains `groups` (q/k carry a groups axis, head h reads group
  *     h / (heads / groups); groups == 1 is the reference layout);
  *   - Mamba-3 MIMO may write `last_state` (the reference rejects any MIMO carry);
- *   - one new entry point, arm_scan_ss2d_f32, the fused four-direction 2D scan;
+ *   - new entry points: arm_scan_ss2d_f32 (the fused four-direction 2D scan), and
+ *     variants for callers' layouts and the fused Mamba-3 angle pre-pass
+ *     (arm_scan_selective_scan_strided_f32, arm_scan_mamba3_scan_time_major_f32,
+ *     arm_scan_mamba3_scan_angles_f32, arm_scan_mamba3_angles_f32), each described
+ *     at its declaration;
  *   - code 6 reports a HIP launch / device error; arm_scan_last_error() explains
  *     the most recent nonzero code on the calling thread.
  *
@@ -132,6 +136,33 @@ int arm_scan_mamba3_scan_time_major_f32(
     const float* cos, const float* sin, const float* d_skip, const float* z,
     const float* mimo_psi, const float* mimo_zeta, const float* mimo_phi, int reverse,
     int backend, int threading, float* out, float* last_state, float* last_bx, void* stream);
+
+/* No reference counterpart: arm_scan_mamba3_scan_time_major_f32 (forward) with the
+ * angle pre-pass fused into the scan. The reference computes cos/sin in Python
+ * (python/arm_scan/mamba3.py:41-89, theta = cumsum_l(tanh(angle) * pi * dt)) and
+ * passes them in; here raw `angles` (b, l, h, n_angles) replace cos and sin, the
+ * pairs past n_angles rotating by zero as in its padding. Needs n_angles a positive
+ * multiple of 4 up to dqk/2, 16-byte aligned inputs and the chunked kernel's shapes
+ * (dv, dqk multiples of 16, dqk <= 128, rank 1/2/4); otherwise
+ * ARM_SCAN_ERR_INVALID_DIMS and the caller runs the pre-pass and calls
+ * arm_scan_mamba3_scan_time_major_f32. There is no reverse: theta is a forward
+ * cumsum, which a backward walk does not have. */
+int arm_scan_mamba3_scan_angles_f32(
+    const ArmMamba3Dims* dims, const float* q, const float* k, const float* v, const float* adt,
+    const float* dt, const float* trap, const float* q_bias, const float* k_bias,
+    const float* angles, size_t n_angles, const float* d_skip, const float* z,
+    const float* mimo_psi, const float* mimo_zeta, const float* mimo_phi, int backend,
+    int threading, float* out, float* last_state, float* last_bx, void* stream);
+
+/* No reference counterpart: the RoPE angle pre-pass the reference runs in Python
+ * (python/arm_scan/mamba3.py:41-89) as one kernel. angles (batch, len, heads,
+ * n_angles) raw, dt (batch, heads, len) post-softplus -> cos, sin (batch, len, heads,
+ * half) with theta = cumsum_len(tanh(angle) * pi * dt); pairs n_angles .. half-1 get
+ * cos 1, sin 0. Feeds arm_scan_mamba3_scan[_time_major]_f32 where the fused entry
+ * point does not apply (reverse, MIMO, n_angles not a multiple of 4). */
+int arm_scan_mamba3_angles_f32(const float* angles, const float* dt, size_t batch, size_t len,
+                               size_t heads, size_t n_angles, size_t half, float* cos,
+                               float* sin, void* stream);
 
 /* New in ABI 8 (no single reference symbol: it fuses python/arm_scan/ss2d.py:277-342,
  * which composes two bidirectional calls). Four directions over a (H, W) grid:

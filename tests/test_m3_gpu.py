@@ -221,3 +221,166 @@ def test_m3_head_major_entry_matches_time_major():
         torch.cuda.synchronize()
         assert torch.equal(hm.permute(0, 2, 1, 3), tm)
         assert rel_err(host(tm), _siso_ref(x).transpose(0, 2, 1, 3)) < TOL
+
+
+ANGLE_SISO = [
+    # (batch, len, heads, dv, dqk, groups, r): r < dqk/2 rotates only the first r pairs
+    (2, 37, 4, 16, 32, 1, 8),
+    (1, 300, 3, 64, 128, 3, 32),
+    (2, 130, 4, 32, 64, 2, 16),
+    (1, 1000, 2, 32, 64, 2, 32),
+]
+
+
+def _angle_inputs(x, r, seed):
+    rng = np.random.default_rng(seed)
+    b, L, h = x["v"].shape[0], x["v"].shape[1], x["v"].shape[2]
+    angles = rng.standard_normal((b, L, h, r)).astype(np.float32)
+    cos, sin = oracle.angles_to_cos_sin(angles, x["dt"], x["q"].shape[-1] // 2)
+    return angles, cos, sin
+
+
+@pytest.mark.parametrize("shape", ANGLE_SISO, ids=lambda s: "x".join(map(str, s)))
+def test_m3_siso_fused_angles(shape):
+    """The angle pre-pass fused into the scan (raw angles in, no cos/sin) against
+    the oracle fed the float64 pre-pass (python/arm_scan/mamba3.py:41-89)."""
+    import armhackathon_amd as arm_scan
+    from armhackathon_amd.mamba3 import _run_angles
+
+    b, L, h, dv, dqk, g, r = shape
+    case(f"siso fused angles {shape}")
+    x = workloads.m3_siso(batch=b, length=L, heads=h, dv=dv, dqk=dqk, seed=L + 5)
+    if g != h:
+        x["q"] = np.ascontiguousarray(x["q"][:, :, :g])
+        x["k"] = np.ascontiguousarray(x["k"][:, :, :g])
+    rng = np.random.default_rng(L)
+    x["q_bias"] = (rng.standard_normal((h, dqk)) * 0.1).astype(np.float32)
+    x["k_bias"] = (rng.standard_normal((h, dqk)) * 0.1).astype(np.float32)
+    x["D"] = rng.standard_normal(h).astype(np.float32)
+    x["z"] = rng.standard_normal(x["v"].shape).astype(np.float32)
+    angles, x["cos"], x["sin"] = _angle_inputs(x, r, L)
+    ref, rls, rlbx = _siso_ref(x, want_state=True)
+    t = dev(x)
+    ta = dev(angles)
+    # the raw entry point (fused for sure), then the public op (which picks it)
+    out, ls, lbx = _run_angles(*[t[k] for k in SISO_KEYS], ta, t["D"], t["z"], None, None,
+                               None, True)
+    assert rel_err(host(out), ref.transpose(0, 2, 1, 3)) < TOL
+    assert rel_err(host(ls), rls) < TOL
+    assert rel_err(host(lbx), rlbx) < TOL
+    out2 = arm_scan.mamba3_scan(*[t[k] for k in SISO_KEYS], angles=ta, D=t["D"], z=t["z"])
+    assert np.array_equal(host(out2), host(out))
+
+
+ANGLE_MIMO = [
+    # (batch, len, heads, dv, dqk, rank, groups, r)
+    (1, 20, 2, 16, 32, 4, 1, 8),
+    (2, 65, 4, 32, 64, 2, 4, 32),
+    (1, 150, 2, 64, 128, 4, 2, 32),
+    (1, 600, 2, 32, 64, 4, 2, 16),
+]
+
+
+@pytest.mark.parametrize("shape", ANGLE_MIMO, ids=lambda s: "x".join(map(str, s)))
+def test_m3_mimo_fused_angles(shape):
+    import armhackathon_amd as arm_scan
+    from armhackathon_amd.mamba3 import _run_angles
+
+    b, L, h, dv, dqk, rk, g, r = shape
+    case(f"mimo fused angles {shape}")
+    x = workloads.m3_mimo(batch=b, length=L, heads=h, dv=dv, dqk=dqk, rank=rk, seed=L + 3)
+    if g != h:
+        x["q"] = np.ascontiguousarray(x["q"][:, :, :, :g])
+        x["k"] = np.ascontiguousarray(x["k"][:, :, :, :g])
+    rng = np.random.default_rng(L + 1)
+    x["zeta"] = rng.standard_normal((h, rk, dv)).astype(np.float32)
+    x["D"] = rng.standard_normal(h).astype(np.float32)
+    x["z"] = rng.standard_normal(x["v"].shape).astype(np.float32)
+    angles, x["cos"], x["sin"] = _angle_inputs(x, r, L + 2)
+    ref, rls, _ = oracle.mamba3_scan(*[x[k] for k in SISO_KEYS], x["cos"], x["sin"], D=x["D"],
+                                     z=x["z"], psi=x["psi"], zeta=x["zeta"], phi=x["phi"],
+                                     dtype=np.float64, want_state=True)
+    t = dev(x)
+    ta = dev(angles)
+    out, ls, _ = _run_angles(*[t[k] for k in SISO_KEYS], ta, t["D"], t["z"], t["psi"],
+                             t["zeta"], t["phi"], True)
+    assert rel_err(host(out), ref.transpose(0, 2, 1, 3)) < TOL
+    assert rel_err(host(ls), rls) < TOL
+    # the public op takes the HIP pre-pass and the scan on cos/sin for MIMO
+    out2 = arm_scan.mamba3_mimo_scan(*[t[k] for k in SISO_KEYS], t["psi"], t["zeta"],
+                                     t["phi"], angles=ta, D=t["D"], z=t["z"])
+    assert rel_err(host(out2), ref.transpose(0, 2, 1, 3)) < TOL
+
+
+def test_m3_fused_angles_config_shapes():
+    """Configs 3 and 4 (batch 1, L 2048 to bound the oracle) through the fused
+    pre-pass with the published rotation fraction (r = dqk/4 = 32)."""
+    from armhackathon_amd.mamba3 import _run_angles
+
+    for mimo in (False, True):
+        case(f"fused angles, config {4 if mimo else 3} shape")
+        x = (workloads.m3_mimo if mimo else workloads.m3_siso)(batch=1, length=2048, seed=8)
+        angles, x["cos"], x["sin"] = _angle_inputs(x, 32, 8)
+        kw = dict(psi=x["psi"], zeta=x["zeta"], phi=x["phi"]) if mimo else {}
+        ref, rls, _ = oracle.mamba3_scan(*[x[k] for k in SISO_KEYS], x["cos"], x["sin"],
+                                         dtype=np.float64, want_state=True, **kw)
+        t = dev(x)
+        mk = (t["psi"], t["zeta"], t["phi"]) if mimo else (None, None, None)
+        out, ls, _ = _run_angles(*[t[k] for k in SISO_KEYS], dev(angles), None, None, *mk,
+                                 True)
+        assert rel_err(host(out), ref.transpose(0, 2, 1, 3)) < TOL
+        assert rel_err(host(ls), rls) < TOL
+
+
+def test_m3_fused_angles_declines():
+    """What the fused entry point does not serve goes through the pre-pass: reverse,
+    and angle pairs not a multiple of 4; the entry point itself rejects them."""
+    import armhackathon_amd as arm_scan
+    from armhackathon_amd import _ffi
+    from armhackathon_amd.mamba3 import _run_angles
+
+    x = workloads.m3_siso(batch=1, length=100, heads=2, dv=16, dqk=32, seed=12)
+    for r, reverse in ((6, False), (8, True)):
+        case(f"fused angles declined: r={r} reverse={reverse}")
+        angles, x["cos"], x["sin"] = _angle_inputs(x, r, 12)
+        t = dev(x)
+        out = arm_scan.mamba3_scan(*[t[k] for k in SISO_KEYS], angles=dev(angles),
+                                   reverse=reverse)
+        ref = _siso_ref(x, reverse=reverse)
+        assert rel_err(host(out), ref.transpose(0, 2, 1, 3)) < TOL
+    with pytest.raises(_ffi.ArmScanError) as e:
+        _run_angles(*[t[k] for k in SISO_KEYS], dev(angles[..., :6].copy()), None, None,
+                    None, None, None, False)
+    assert e.value.code == 2
+
+
+PREPASS = [
+    # (batch, len, heads, r, half): 16-byte pieces, and the scalar path (r or half
+    # not a multiple of 4, partial last piece), and lengths across the 1024-step tile
+    (1, 4096, 24, 32, 64),
+    (2, 1500, 4, 16, 16),
+    (2, 37, 3, 3, 4),
+    (1, 2100, 2, 6, 10),
+    (1, 1, 1, 1, 1),
+    (3, 1024, 5, 40, 40),
+]
+
+
+@pytest.mark.parametrize("shape", PREPASS, ids=lambda s: "x".join(map(str, s)))
+def test_m3_angle_prepass(shape):
+    """The HIP pre-pass against the float64 oracle: |cos - ref|, |sin - ref| below
+    2e-5 (theta is summed in float32 over up to 4096 steps; the angles are N(0,1)
+    and dt as in config 3, so theta stays within a few radians)."""
+    from armhackathon_amd.mamba3 import angles_to_cos_sin
+
+    b, L, h, r, half = shape
+    case(f"angle pre-pass {shape}")
+    rng = np.random.default_rng(L + r)
+    angles = rng.standard_normal((b, L, h, r)).astype(np.float32)
+    dt = np.log1p(np.exp(rng.standard_normal((b, h, L)) - 4.0)).astype(np.float32)
+    cos, sin = angles_to_cos_sin(dev(angles), dev(dt), half)
+    rc, rs = oracle.angles_to_cos_sin(angles, dt, half)
+    assert cos.shape == (b, L, h, half) and sin.shape == (b, L, h, half)
+    assert np.abs(host(cos) - rc).max() < 2e-5
+    assert np.abs(host(sin) - rs).max() < 2e-5
+    assert np.all(host(cos)[..., r:] == 1.0) and np.all(host(sin)[..., r:] == 0.0)
