@@ -47,6 +47,12 @@ struct M1Kern {
   long long zs_b, zs_d, zs_t, os_b, os_d, os_t;
   unsigned z_bytes, o_bytes;
   int z_dma;  // strided z and out staged through LDS (m1_tile_kernel<.., 2>)
+  // Rows cut into `segs` segments of `seg_chunks` chunks when there are too few rows
+  // to fill the chip: segmap[row][s][n] = (A, B), the affine map of segment s < segs-1
+  // (h_end = A h_start + B), from m1_seg_fold_kernel. segs <= 1: whole rows.
+  int segs;
+  long long seg_chunks;
+  float* segmap;
 };
 
 // One traversal of a multi-traversal launch: its own inputs, B/C, outputs and
@@ -597,8 +603,8 @@ __device__ __forceinline__ void tile_states(const float* tile, int n0, int N, in
 // (batch, dim, len) contiguous; 1: strided (p.zs_*, p.os_*), z read with buffer
 // loads and out written with buffer stores; 2: strided with unit channel stride,
 // z and out staged through LDS.
-template <int I, bool REV, int SIO>
-__device__ __forceinline__ void tile_rows(const M1Kern& p, long long blk) {
+template <int I, bool REV, int SIO, bool SEG = false>
+__device__ __forceinline__ void tile_rows(const M1Kern& p, long long blk, int seg = 0) {
   constexpr int LPR = 16, RPW = 4;
   using G = Tile<I>;
   constexpr long long CH = G::CH;
@@ -633,20 +639,34 @@ __device__ __forceinline__ void tile_rows(const M1Kern& p, long long blk) {
   float* a2s = small + (kWavesPerBlock * RPW + wave * RPW + rw) * N;
   float* zeros = small + 2 * kWavesPerBlock * RPW * N;
   const float* cbase = j == 0 ? carry : zeros;
-  if (j == 0)
-    for (int n = 0; n < N; ++n) {
-      carry[n] = p.h0 ? p.h0[row * N + n] : 0.0f;
-      a2s[n] = Arow[n] * kLog2e;
-    }
-  for (int i = threadIdx.x; i < N; i += blockDim.x) zeros[i] = 0.0f;
-
   const long long nch = (L + CH - 1) / CH;
   const long long nfull = L / CH;
+  // this segment's full chunks [cb, ce); the last segment also runs the tail chunk
+  constexpr bool segd = SEG;  // launched with p.segs > 1
+  const long long cb = segd ? seg * p.seg_chunks : 0;
+  const long long ce = segd ? (cb + p.seg_chunks < nfull ? cb + p.seg_chunks : nfull) : nfull;
+  const bool last_seg = !segd || seg == p.segs - 1;
+  // the row's 16 lanes take a state each: the state entering the segment is h0
+  // through the maps of the segments before it
+  for (int n = j; n < N; n += LPR) {
+    float h = p.h0 ? p.h0[row * N + n] : 0.0f;
+    for (int s2 = 0; SEG && s2 < seg; ++s2) {
+      const float2 mp = *reinterpret_cast<const float2*>(
+          p.segmap + ((row * (p.segs - 1) + s2) * N + n) * 2);
+      h = fmaf(mp.x, h, mp.y);
+    }
+    carry[n] = h;
+    a2s[n] = Arow[n] * kLog2e;
+  }
+  for (int i = threadIdx.x; i < N; i += blockDim.x) zeros[i] = 0.0f;
+
   const int ng = (N + kTileStates - 1) / kTileStates;  // tiles per chunk
-  const long long ntiles = nfull * ng;
+  const long long ntiles = (ce - cb) * ng;
   auto mem0 = [&](long long c) { return REV ? L - (c + 1) * CH : c * CH; };
-  if (ntiles > 0) issue_tile<I>(tiles, Bg, Cg, L, mem0(0), 0, N, wave, lane);
-  tile_sync();
+  if (ntiles > 0) issue_tile<I>(tiles, Bg, Cg, L, mem0(cb), 0, N, wave, lane);
+  // In a segment (one or a few chunks per block) the first tile's sync comes after
+  // the first chunk's delta/u loads, in the loop, so that their latencies overlap.
+  if (!segd || ce == cb) tile_sync();
 
   // the lane block's outputs at traversal base sbo (SIO 0 and 1)
   auto store_out = [&](long long sbo, const float (&v)[I]) {
@@ -666,10 +686,10 @@ __device__ __forceinline__ void tile_rows(const M1Kern& p, long long blk) {
   auto z_stage = [&](long long c) {
     issue_z_stage<REV>(zbuf, p.z + bib * p.zs_b, p.zs_t, L, c * CH, d0, wave, lane);
   };
-  if (SIO == 2 && p.z && nfull > 0) z_stage(0);
+  if (SIO == 2 && p.z && ce > cb) z_stage(cb);
 
   long long k = 0;  // tile counter
-  for (long long c = 0; c < nfull; ++c) {
+  for (long long c = cb; c < ce; ++c) {
     const long long sb = c * CH + (long long)j * I;
     float dt[I], du[I], y[I], zz[I];
     float sdt = 0.0f;
@@ -687,10 +707,11 @@ __device__ __forceinline__ void tile_rows(const M1Kern& p, long long blk) {
         sdt += x;
       }
     }
+    if (segd && c == cb) tile_sync();  // the first tile, the carries and A*log2e above
     const bool last_chunk = c + 1 == nch;
     for (int q = 0; q < ng; ++q, ++k) {
       if (k + 1 < ntiles) {
-        const long long cn = (k + 1) / ng;
+        const long long cn = cb + (k + 1) / ng;
         const int qn = (int)((k + 1) % ng);
         issue_tile<I>(tiles + ((k + 1) & 1) * G::FLOATS, Bg, Cg, L, mem0(cn),
                       qn * kTileStates, N, wave, lane);
@@ -724,18 +745,128 @@ __device__ __forceinline__ void tile_rows(const M1Kern& p, long long blk) {
       lds_barrier();
       store_out_stage<REV>(zbuf, p.out + bib * p.os_b, p.os_t, L, c * CH, d0, wave, lane);
       lds_barrier();  // every lane has read its outputs before the next z stage lands
-      if (p.z && c + 1 < nfull) z_stage(c + 1);
+      if (p.z && c + 1 < ce) z_stage(c + 1);
     } else {
       store_out(sb, y);
     }
   }
-  if (nfull < nch) {
+  if (last_seg && nfull < nch) {
     // the row's tail chunk goes through the bounds-checked global-load path
     float dn[I], un[I];
     chunk<LPR, I, REV, true, false>(p, nfull * CH + (long long)j * I, j, true, true, row, urow,
                                     drow, zrow, orow, Bg, Cg, a2s, bias, dskip, carry, dn, un,
                                     false, -1, SIO ? p.zs_t : 1, SIO ? p.os_t : 1);
   }
+}
+
+// Pass 1 of a segmented scan: the affine map h -> A h + B of each state over one
+// segment of 16 rows (segments 0 .. segs-2), with the same discretisation and
+// fold as tile_state; the chunk maps compose in order. A of a chunk is
+// 2^(a2 * sum of the row's dt over it), one exponential.
+template <int I, bool REV>
+__device__ __forceinline__ void fold_rows(const M1Kern& p, long long blk, int seg) {
+  constexpr int LPR = 16, RPW = 4;
+  using G = Tile<I>;
+  constexpr long long CH = G::CH;
+  extern __shared__ __attribute__((aligned(16))) float s_lds[];
+  float* tiles = s_lds;                  // [2][G::FLOATS]
+  float* small = s_lds + 2 * G::FLOATS;  // segment A, B, A*log2e per row and state
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int j = lane % LPR;
+  const int rw = lane / LPR;
+  const long long row = (blk * kWavesPerBlock + wave) * RPW + rw;
+  const long long L = p.L;
+  const int N = p.N;
+  const int bi = (int)(row / p.dim), d = (int)(row - (long long)bi * p.dim);
+  const int g = d / p.group_size;
+  const float* urow = p.u + row * L;
+  const float* drow = p.delta + row * L;
+  const float* Bg = p.B + ((long long)bi * p.groups + g) * N * L;
+  const float* Cg = p.C + ((long long)bi * p.groups + g) * N * L;
+  const float bias = p.bias ? p.bias[d] : 0.0f;
+  float* sA = small + (wave * RPW + rw) * N;
+  float* sB = small + (kWavesPerBlock * RPW + wave * RPW + rw) * N;
+  float* a2s = small + (2 * kWavesPerBlock * RPW + wave * RPW + rw) * N;
+  for (int n = j; n < N; n += LPR) {
+    sA[n] = 1.0f;
+    sB[n] = 0.0f;
+    a2s[n] = p.A[(long long)d * N + n] * kLog2e;
+  }
+
+  const long long nfull = L / CH;
+  const long long cb = seg * p.seg_chunks;
+  const long long ce = cb + p.seg_chunks < nfull ? cb + p.seg_chunks : nfull;
+  const int ng = (N + kTileStates - 1) / kTileStates;
+  const long long ntiles = (ce - cb) * ng;
+  auto mem0 = [&](long long c) { return REV ? L - (c + 1) * CH : c * CH; };
+  if (ntiles > 0) issue_tile<I>(tiles, Bg, Cg, L, mem0(cb), 0, N, wave, lane);
+  long long k = 0;
+  for (long long c = cb; c < ce; ++c) {
+    const long long sb = c * CH + (long long)j * I;
+    float dt[I], du[I];
+    float sdt = 0.0f;
+    {
+      float dd[I], uu[I];
+      load_block<I, REV, true>(drow, L, sb, 0.0f, dd, L);
+      load_block<I, REV, true>(urow, L, sb, 0.0f, uu, L);
+#pragma unroll
+      for (int i = 0; i < I; ++i) {
+        float x = dd[i] + bias;
+        if (p.softplus) x = softplus_fast(x);
+        dt[i] = x;
+        du[i] = x * uu[i];
+        sdt += x;
+      }
+    }
+    if (c == cb) tile_sync();  // the first tile, and the initial maps above
+    float srow = sdt;  // the row's dt over the chunk
+#pragma unroll
+    for (int m = 1; m < LPR; m <<= 1) srow += __shfl_xor(srow, m, LPR);
+    for (int q = 0; q < ng; ++q, ++k) {
+      if (k + 1 < ntiles) {
+        const long long cn = cb + (k + 1) / ng;
+        const int qn = (int)((k + 1) % ng);
+        issue_tile<I>(tiles + ((k + 1) & 1) * G::FLOATS, Bg, Cg, L, mem0(cn),
+                      qn * kTileStates, N, wave, lane);
+      }
+      const float* tile = tiles + (k & 1) * G::FLOATS;
+#pragma unroll
+      for (int s2 = 0; s2 < kTileStates; ++s2) {
+        const int n = q * kTileStates + s2;
+        if (n < N) {
+          float bb[I];
+          lds_block<I, REV>(tile + s2 * CH, j, bb);
+          const float a2 = a2s[n];
+          float bt = 0.0f;
+#pragma unroll
+          for (int i = 0; i < I; ++i) bt = fmaf(ex2(dt[i] * a2), bt, du[i] * bb[i]);
+          float at = ex2(a2 * sdt);
+          Row<16>::scan(at, bt);  // lane 15: the chunk's B from a zero state
+          if (j == LPR - 1) {
+            const float ac = ex2(a2 * srow);
+            sB[n] = fmaf(ac, sB[n], bt);
+            sA[n] = ac * sA[n];
+          }
+        }
+      }
+      tile_sync();
+    }
+  }
+  if (j == LPR - 1)
+    for (int n = 0; n < N; ++n) {
+      float* mp = p.segmap + ((row * (p.segs - 1) + seg) * N + n) * 2;
+      mp[0] = sA[n];
+      mp[1] = sB[n];
+    }
+}
+
+template <int I, bool REV>
+__global__ void __launch_bounds__(64 * kWavesPerBlock, 3)
+m1_seg_fold_kernel(M1Kern p) {
+  const long long nblk = p.rows / (kWavesPerBlock * 4);
+  fold_rows<I, REV>(p, blockIdx.x % nblk, (int)(blockIdx.x / nblk));
 }
 
 // Block id -> row block for time-major z/out: a 128-byte line of those holds 32
@@ -748,11 +879,14 @@ __device__ __forceinline__ long long paired_block(long long bid, long long nblk)
   return 2 * (8 * (k >> 1) + x) + (k & 1);
 }
 
-template <int I, bool REV, int SIO>
+// Block id -> (row block, segment): with SEG the segments are blockIdx / (row blocks).
+template <int I, bool REV, int SIO, bool SEG>
 __global__ void __launch_bounds__(64 * kWavesPerBlock, 3)
 m1_tile_kernel(M1Kern p) {
   const long long nblk = p.rows / (kWavesPerBlock * 4);
-  tile_rows<I, REV, SIO>(p, SIO ? paired_block(blockIdx.x, nblk) : (long long)blockIdx.x);
+  const long long bid = SEG ? blockIdx.x % nblk : (long long)blockIdx.x;
+  const int seg = SEG ? (int)(blockIdx.x / nblk) : 0;
+  tile_rows<I, REV, SIO, SEG>(p, SIO ? paired_block(bid, nblk) : bid, seg);
 }
 
 // Several traversals of rows of the same shape in one launch (the directions of
@@ -782,11 +916,23 @@ template <int I, bool REV, int SIO>
 hipError_t launch_tile(const M1Kern& k, hipStream_t st) {
   constexpr int RPB = kWavesPerBlock * 4;
   const long long blocks = (long long)k.rows / RPB;
+  const int segs = k.segs > 1 ? k.segs : 1;
+  if (segs > 1) {  // pass 1: the maps of segments 0 .. segs-2
+    const size_t lds1 = sizeof(float) * (2 * (size_t)Tile<I>::FLOATS + 3 * (size_t)RPB * k.N);
+    hipLaunchKernelGGL((m1_seg_fold_kernel<I, REV>), dim3((unsigned)(blocks * (segs - 1))),
+                       dim3(64 * kWavesPerBlock), lds1, st, k);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
   const size_t lds =
       sizeof(float) * (2 * (size_t)Tile<I>::FLOATS + (SIO == 2 ? kZStageFloats : 0) +
                        (2 * (size_t)RPB + 1) * k.N);
-  hipLaunchKernelGGL((m1_tile_kernel<I, REV, SIO>), dim3((unsigned)blocks),
-                     dim3(64 * kWavesPerBlock), lds, st, k);
+  if (segs > 1)
+    hipLaunchKernelGGL((m1_tile_kernel<I, REV, SIO, true>), dim3((unsigned)(blocks * segs)),
+                       dim3(64 * kWavesPerBlock), lds, st, k);
+  else
+    hipLaunchKernelGGL((m1_tile_kernel<I, REV, SIO, false>), dim3((unsigned)blocks),
+                       dim3(64 * kWavesPerBlock), lds, st, k);
   return hipGetLastError();
 }
 
@@ -850,6 +996,44 @@ long long slab_bytes(const long long (&s)[3], const M1Problem& pr) {
 }
 }  // namespace
 
+namespace {
+// Rows cut into segments when there are too few to fill the chip: a 16-row block per
+// CU slot, 768 slots (three per CU) resident at once. Sets k.segs / k.seg_chunks and
+// allocates the segment maps on the stream.
+hipError_t plan_segments(M1Kern& k, hipStream_t st) {
+  const long long blocks = k.rows / 16;
+  const long long nfull = k.L / (16 * M1_TILE_I);
+  k.segs = 1;
+  k.seg_chunks = nfull;
+  k.segmap = nullptr;
+  if (blocks >= 512 || nfull < 2) return hipSuccess;
+  long long segs = (768 + blocks - 1) / blocks;
+  if (segs > nfull) segs = nfull;
+  if (segs < 2) return hipSuccess;
+  k.seg_chunks = (nfull + segs - 1) / segs;
+  k.segs = (int)((nfull + k.seg_chunks - 1) / k.seg_chunks);
+  if (k.segs < 2) {
+    k.segs = 1;
+    k.seg_chunks = nfull;
+    return hipSuccess;
+  }
+  return stream_alloc((void**)&k.segmap,
+                      (size_t)k.rows * (k.segs - 1) * k.N * 2 * sizeof(float), st);
+}
+
+template <int SIO>
+hipError_t run_tile(M1Kern& k, bool rev, hipStream_t st) {
+  hipError_t e = plan_segments(k, st);
+  if (e != hipSuccess) return e;
+  e = rev ? launch_tile<M1_TILE_I, true, SIO>(k, st) : launch_tile<M1_TILE_I, false, SIO>(k, st);
+  if (k.segmap) {
+    const hipError_t fe = hipFreeAsync(k.segmap, st);
+    if (e == hipSuccess) e = fe;
+  }
+  return e;
+}
+}  // namespace
+
 bool m1_strided_io(const M1Problem& pr) {
   return (pr.z && !contiguous_strides(pr.z_stride, pr)) || !contiguous_strides(pr.out_stride, pr);
 }
@@ -903,17 +1087,11 @@ hipError_t m1_scan_chunked(const M1Problem& pr, hipStream_t st) {
                          pr.state > kTileStates)) &&
               M1_TILE_I == 16;
     k.o_bytes = (unsigned)slab_bytes(os, pr);
-    if (k.z_dma)
-      return rev ? launch_tile<M1_TILE_I, true, 2>(k, st)
-                 : launch_tile<M1_TILE_I, false, 2>(k, st);
-    return rev ? launch_tile<M1_TILE_I, true, 1>(k, st)
-               : launch_tile<M1_TILE_I, false, 1>(k, st);
+    return k.z_dma ? run_tile<2>(k, rev, st) : run_tile<1>(k, rev, st);
   }
   // the tiled path needs every 16-row block inside one batch/group and 16-byte rows
   const bool tiled = vec && pr.dim % 16 == 0 && (pr.dim / pr.groups) % 16 == 0;
-  if (tiled)
-    return rev ? launch_tile<M1_TILE_I, true, 0>(k, st)
-               : launch_tile<M1_TILE_I, false, 0>(k, st);
+  if (tiled) return run_tile<0>(k, rev, st);
   return launch_dir<16, 16>(k, rev, vec, st);
 }
 

@@ -50,7 +50,8 @@ def parse():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
-    ap.add_argument("--workload", choices=("m1", "m1_seam", "m3_siso", "m3_mimo", "ss2d",
+    ap.add_argument("--workload", choices=("m1", "m1_b1", "m1_seam", "m3_siso", "m3_mimo",
+                                           "ss2d",
                                            "m3_siso_angles", "m3_mimo_angles"),
                     default="m1",
                     help="m1 (default): the headline line below; the others time one of the "
@@ -122,6 +123,12 @@ def config_inputs(name, dev):
 
     from armhackathon_amd import workloads
 
+    if name == "m1_b1":
+        sets = []
+        for sd in range(8):
+            x = workloads.m1_op(batch=1, dim=1536, length=2048, state=16, seed=100 + sd)
+            sets.append({k: torch.from_numpy(v).to(dev) for k, v in x.items() if v is not None})
+        return sets, workloads.m1_bytes(1, 1536, 2048, 16, z=True, D=True, last_state=True)
     if name == "m1_seam":
         t = scan_inputs(0, dev)
         b, d, L, n = SHAPE["batch"], SHAPE["dim"], SHAPE["length"], SHAPE["state"]
@@ -147,6 +154,8 @@ def config_inputs(name, dev):
 
 
 CONFIG_NAMES = {
+    "m1_b1": "config 1: Mamba-1 selective_scan B1 D1536 L2048 N16, z and D, final state "
+             "(8 input sets rotated: one set fits in the 256 MB MALL)",
     "m1_seam": "config 2 scan at the Hugging Face seam: B8 D1536 L2048 N16, bias+softplus, "
                "D, z read in place from the mixer's (b, L, 2D) projection, out written "
                "time-major",
@@ -167,7 +176,22 @@ def bench_config(name, dev, steps, warmup):
 
     t, nbytes = config_inputs(name, dev)
     K = ("q", "k", "v", "adt", "dt", "trap", "q_bias", "k_bias")
-    if name == "m1_seam":
+    if name == "m1_b1":
+        from armhackathon_amd import _ffi
+        outs = [torch.empty_like(x["u"]) for x in t]
+        lasts = [x["u"].new_empty((1, 1536, 16)) for x in t]
+        dims = _ffi.ArmScanDims(1, 1536, 2048, 16, 1)
+        it = {"i": 0}
+
+        def call():
+            i = it["i"] = (it["i"] + 1) % len(t)
+            x = t[i]
+            _ffi.scan_raw(dims, x["u"].data_ptr(), x["delta"].data_ptr(), x["A"].data_ptr(),
+                          x["B"].data_ptr(), x["C"].data_ptr(), x["D"].data_ptr(),
+                          x["z"].data_ptr(), 0, False, "auto", "auto", outs[i].data_ptr(),
+                          lasts[i].data_ptr(), 0, reverse=False,
+                          stream=torch.cuda.current_stream(dev).cuda_stream)
+    elif name == "m1_seam":
         def call():
             return arm_scan.selective_scan_time_major(
                 t["u"], t["delta"], t["A"], t["B"], t["C"], D=t["D"], z=t["z"],
@@ -237,8 +261,9 @@ def bench_config(name, dev, steps, warmup):
 
 def bench_config_cpu(name, seconds):
     """The C++ restatement of the reference's x86 path on host cores for one of
-    configs 3-5, over a bounded sample of the config (batch 1 of 4 for Mamba-3,
-    2 of 16 for SS2D), repeated until `seconds` of wall time have passed."""
+    configs 1 and 3-5, over a bounded sample of the config (config 1 whole, batch 1 of
+    4 for Mamba-3, 2 of 16 for SS2D), repeated until `seconds` of wall time have
+    passed."""
     import numpy as np
 
     import oracle
@@ -247,7 +272,15 @@ def bench_config_cpu(name, seconds):
     threads = min(16, os.cpu_count() or 1)
     oracle.set_threads(threads)
     K = ("q", "k", "v", "adt", "dt", "trap", "q_bias", "k_bias")
-    if name == "m3_siso":
+    if name == "m1_b1":
+        x = workloads.m1_op(batch=1, dim=1536, length=2048, state=16, seed=100)
+        nbytes = workloads.m1_bytes(1, 1536, 2048, 16, z=True, D=True, last_state=True)
+        sample = "config 1"
+
+        def call():
+            oracle.selective_scan(x["u"], x["delta"], x["A"], x["B"], x["C"], D=x["D"],
+                                  z=x["z"])
+    elif name == "m3_siso":
         x = workloads.m3_siso(batch=1, seed=3)
         nbytes, sample = workloads.m3_bytes(x), "batch 1 of config 3"
 
@@ -387,7 +420,7 @@ def main():
     prefill = None if args.no_prefill else bench_prefill(args, dev)
     configs = None if args.no_configs else {
         name: bench_config(name, dev, steps, 10)
-        for name, steps in (("m3_siso", 100), ("m3_mimo", 40), ("ss2d", 100))}
+        for name, steps in (("m1_b1", 400), ("m3_siso", 100), ("m3_mimo", 40), ("ss2d", 100))}
     cpu = None if args.no_cpu else bench_cpu(args.cpu_seconds)
     if configs is not None and not args.no_cpu:
         for name in configs:
