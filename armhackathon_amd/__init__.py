@@ -23,6 +23,7 @@ __all__ = [
     "selective_scan",
     "selective_scan_bidirectional",
     "selective_scan_time_major",
+    "selective_state_update",
     "bidirectional_scan",
     "ss2d_scan",
     "use_arm_scan",
@@ -42,6 +43,7 @@ _LAZY = {
     "selective_scan": ".op",
     "selective_scan_bidirectional": ".op",
     "selective_scan_time_major": ".op",
+    "selective_state_update": ".op",
     "kernel_calls": ".op",
     "bidirectional_scan": ".bidirectional",
     "ss2d_scan": ".ss2d",

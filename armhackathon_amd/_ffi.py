@@ -100,6 +100,13 @@ def _declare(lib):
                   _vp, _vp,              # out out_strides
                   _vp, _vp,              # last_state h0
                   _vp]                   # stream
+    f = lib.arm_scan_selective_state_update_f32
+    f.restype = _ci
+    f.argtypes = [*([ctypes.c_size_t] * 3),      # batch dim state_dim
+                  _vp, _vp, _vp, _vp, _vp,       # state x x_strides dt dt_strides
+                  _vp, _vp, _vp, _vp, _vp,       # a b b_strides c c_strides
+                  _vp, _vp, _vp, _vp,            # d_skip z z_strides dt_bias
+                  _ci, _vp, _vp]                 # dt_softplus out stream
     f = lib.arm_scan_selective_scan_bidirectional_f32
     f.restype = _ci
     f.argtypes = [ctypes.POINTER(ArmScanDims),
@@ -206,6 +213,20 @@ def scan_strided_raw(dims, ptr_u, ptr_delta, ptr_a, ptr_b, ptr_c, ptr_d_skip, pt
         zs, _p(ptr_delta_bias), int(bool(delta_softplus)), int(bool(reverse)), ptr_out, os_,
         _p(ptr_last), _p(ptr_h0), _p(stream))
     _check("arm_scan_selective_scan_strided_f32", code)
+
+
+def state_update_raw(batch, dim, state_dim, ptr_state, ptr_x, x_strides, ptr_dt, dt_strides,
+                     ptr_a, ptr_b, b_strides, ptr_c, c_strides, ptr_d_skip, ptr_z, z_strides,
+                     ptr_dt_bias, dt_softplus, ptr_out, *, stream=0):
+    """Call arm_scan_selective_state_update_f32 (one decode step, state in place);
+    strides are pairs of element strides or None (contiguous)."""
+    def arr(s):
+        return None if s is None else (ctypes.c_longlong * 2)(*[int(v) for v in s])
+    code = load().arm_scan_selective_state_update_f32(
+        batch, dim, state_dim, ptr_state, ptr_x, arr(x_strides), ptr_dt, arr(dt_strides),
+        ptr_a, ptr_b, arr(b_strides), ptr_c, arr(c_strides), _p(ptr_d_skip), _p(ptr_z),
+        arr(z_strides), _p(ptr_dt_bias), int(bool(dt_softplus)), ptr_out, _p(stream))
+    _check("arm_scan_selective_state_update_f32", code)
 
 
 def scan_bidir_raw(dims, ptr_u, ptr_delta, ptr_a, ptr_b, ptr_c, ptr_d_skip, ptr_z,

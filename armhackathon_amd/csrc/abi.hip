@@ -150,6 +150,34 @@ int arm_scan_selective_scan_strided_f32(const ArmScanDims* dims, const float* u,
   return run(armscan::m1_scan(p, (hipStream_t)stream), "selective_scan (strided) launch");
 }
 
+int arm_scan_selective_state_update_f32(
+    size_t batch, size_t dim, size_t state_dim, float* state, const float* x,
+    const long long* x_strides, const float* dt, const long long* dt_strides, const float* a,
+    const float* b, const long long* b_strides, const float* c, const long long* c_strides,
+    const float* d_skip, const float* z, const long long* z_strides, const float* dt_bias,
+    int dt_softplus, float* out, void* stream) {
+  if (!state || !x || !dt || !a || !b || !c || !out)
+    return fail(ARM_SCAN_ERR_NULL_POINTER, "a required pointer is null");
+  if (!batch || !dim || !state_dim) return fail(ARM_SCAN_ERR_INVALID_DIMS, "a dimension is zero");
+  if (!prod_ok({batch, dim, state_dim}) || batch * dim > (1u << 30) || state_dim > (1u << 20))
+    return fail(ARM_SCAN_ERR_INVALID_DIMS, "problem too large for this build");
+  armscan::M1Step p{};
+  p.state = state; p.x = x; p.dt = dt; p.A = a; p.B = b; p.C = c; p.D = d_skip; p.z = z;
+  p.bias = dt_bias; p.out = out;
+  p.batch = (int)batch; p.dim = (int)dim; p.N = (int)state_dim; p.softplus = dt_softplus != 0;
+  auto st2 = [](long long* dst, const long long* src, long long s0, long long s1) {
+    dst[0] = src ? src[0] : s0;
+    dst[1] = src ? src[1] : s1;
+    return dst[0] >= 0 && dst[1] >= 0;
+  };
+  const long long D = (long long)dim, N = (long long)state_dim;
+  if (!st2(p.xs, x_strides, D, 1) || !st2(p.dts, dt_strides, D, 1) ||
+      !st2(p.zs, z_strides, D, 1) || !st2(p.Bs, b_strides, N, 1) ||
+      !st2(p.Cs, c_strides, N, 1))
+    return fail(ARM_SCAN_ERR_INVALID_DIMS, "negative strides");
+  return run(armscan::m1_step(p, (hipStream_t)stream), "state update launch");
+}
+
 int arm_scan_selective_scan_bidirectional_f32(
     const ArmScanDims* dims, const float* u, const float* delta, const float* a,
     const float* b, const float* c, const float* d_skip, const float* z,

@@ -21,6 +21,17 @@ struct M1Problem {
 };
 
 hipError_t m1_scan(const M1Problem& p, hipStream_t st);
+
+// One decode step of the Mamba-1 scan, the state (batch, dim, N) updated in place
+// (m1_step.hip). Element strides: x, dt, z (batch, dim); B, C (batch, state).
+struct M1Step {
+  float* state;
+  const float *x, *dt, *A, *B, *C, *D, *z, *bias;
+  float* out;  // (batch, dim)
+  long long xs[2], dts[2], zs[2], Bs[2], Cs[2];
+  int batch, dim, N, softplus;
+};
+hipError_t m1_step(const M1Step& p, hipStream_t st);
 // True when z or out has strides other than the contiguous (batch, dim, len) ones.
 bool m1_strided_io(const M1Problem& p);
 // Whether the one-direction scan serves the strides of z/out; else *why says what fails.

@@ -9,8 +9,12 @@ caches stay upstream's; only the recurrence moves.
 The wrapper takes the fast path for float32 device tensors with no gradient
 required; anything else (host tensors, other dtypes, autograd) goes to the
 original function unchanged, exactly as the reference's wrapper falls back on
-what its kernel cannot serve (python/arm_scan/patch.py:152-168). Decode steps
-use `mamba_selective_state_update`, which is not patched.
+what its kernel cannot serve (python/arm_scan/patch.py:152-168).
+
+Decode steps (one token) go through `mamba_selective_state_update`, which the
+reference leaves to upstream (README.md:320-322). It is patched here as well, with
+the same fallback rule: the fast path runs the step as one kernel instead of the
+dozen small torch kernels upstream launches per layer and token.
 
 The mixer hands the gate z as a (batch, dim, len) view of its time-major
 in_proj output and transposes the scan output back for out_proj. The wrapper
@@ -23,9 +27,34 @@ len) view), so neither side copies; the reference's op copies z
 
 import torch
 
-from .op import kernel_calls, selective_scan_time_major
+from .op import kernel_calls, selective_scan_time_major, selective_state_update
 
-_STATE = {"orig": None, "target": None, "fast_calls": 0, "fallback_calls": 0}
+_STATE = {"orig": None, "orig_step": None, "target": None, "fast_calls": 0,
+          "fallback_calls": 0, "step_calls": 0, "step_fallback_calls": 0}
+
+
+def _patch_step_fn(modeling_mamba):
+    orig = modeling_mamba.mamba_selective_state_update
+
+    def mamba_selective_state_update(state, hidden_states, dt, A, B, C, D=None,
+                                     dt_bias=None, dt_softplus=False, z=None, **kwargs):
+        tensors = (state, hidden_states, dt, A, B, C)
+        optional = tuple(t for t in (D, z, dt_bias) if t is not None)
+        needs_grad = torch.is_grad_enabled() and any(
+            t.requires_grad for t in (*tensors, *optional))
+        if (needs_grad or kwargs
+                or any(t.device.type != "cuda" for t in (*tensors, *optional))
+                or any(t.dtype != torch.float32 for t in (*tensors, *optional))
+                or state.dim() != 3 or not state.is_contiguous()):
+            _STATE["step_fallback_calls"] += 1
+            return orig(state, hidden_states, dt, A, B, C, D=D, dt_bias=dt_bias,
+                        dt_softplus=dt_softplus, z=z, **kwargs)
+        _STATE["step_calls"] += 1
+        return selective_state_update(state, hidden_states, dt, A, B, C, D=D, z=z,
+                                      dt_bias=dt_bias, dt_softplus=dt_softplus)
+
+    modeling_mamba.mamba_selective_state_update = mamba_selective_state_update
+    _STATE["orig_step"] = orig
 
 
 def _patch_scan_fn(modeling_mamba):
@@ -59,7 +88,11 @@ def _patch_scan_fn(modeling_mamba):
     modeling_mamba.mamba_selective_scan = mamba_selective_scan
     _STATE["orig"] = orig
     _STATE["target"] = "mamba_selective_scan"
-    return ["transformers mamba_selective_scan (selective_scan_fn API)"]
+    done = ["transformers mamba_selective_scan (selective_scan_fn API)"]
+    if hasattr(modeling_mamba, "mamba_selective_state_update"):
+        _patch_step_fn(modeling_mamba)
+        done.append("transformers mamba_selective_state_update (decode step)")
+    return done
 
 
 def patch():
@@ -88,7 +121,10 @@ def unpatch():
     from transformers.models.mamba import modeling_mamba
 
     modeling_mamba.mamba_selective_scan = _STATE["orig"]
+    if _STATE["orig_step"] is not None:
+        modeling_mamba.mamba_selective_state_update = _STATE["orig_step"]
     _STATE["orig"] = None
+    _STATE["orig_step"] = None
     _STATE["target"] = None
     return True
 
@@ -98,6 +134,8 @@ def stats():
     return {
         "fast_calls": _STATE["fast_calls"],
         "fallback_calls": _STATE["fallback_calls"],
+        "step_calls": _STATE["step_calls"],
+        "step_fallback_calls": _STATE["step_fallback_calls"],
         "kernel_calls": kernel_calls(),
         "patched": _STATE["orig"] is not None,
         "api": "selective_scan_fn" if _STATE["orig"] is not None else None,

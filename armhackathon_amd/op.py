@@ -231,6 +231,58 @@ def selective_scan_time_major(u, delta, A, B, C, D=None, z=None, delta_bias=None
     return (out, last_state) if return_last_state else out
 
 
+@torch.library.custom_op("arm_scan::selective_state_update", mutates_args=("state",))
+def _state_update_op(
+    state: torch.Tensor,
+    x: torch.Tensor,
+    dt: torch.Tensor,
+    a: torch.Tensor,
+    b: torch.Tensor,
+    c: torch.Tensor,
+    d_skip: Optional[torch.Tensor],
+    z: Optional[torch.Tensor],
+    dt_bias: Optional[torch.Tensor],
+    dt_softplus: bool,
+) -> torch.Tensor:
+    dev = _device_of(state, x, dt, a, b, c, d_skip, z, dt_bias)
+    batch, dim, n = state.shape
+    for name, t, want in (("x", x, (batch, dim)), ("dt", dt, (batch, dim)),
+                          ("A", a, (dim, n)), ("B", b, (batch, n)), ("C", c, (batch, n)),
+                          ("D", d_skip, (dim,)), ("z", z, (batch, dim)),
+                          ("dt_bias", dt_bias, (dim,))):
+        if t is not None and tuple(t.shape) != want:
+            raise ValueError(f"{name} must be {want}, got {tuple(t.shape)}")
+    if not state.is_contiguous():
+        raise ValueError("state must be contiguous (it is updated in place)")
+    out = x.new_empty((batch, dim))
+    with torch.cuda.device(dev):
+        _ffi.state_update_raw(batch, dim, n, state.data_ptr(), x.data_ptr(), x.stride(),
+                              dt.data_ptr(), dt.stride(), a.data_ptr(), b.data_ptr(), b.stride(),
+                              c.data_ptr(), c.stride(), _ptr(d_skip), _ptr(z),
+                              None if z is None else z.stride(), _ptr(dt_bias), dt_softplus,
+                              out.data_ptr(), stream=_stream(dev))
+    _CALLS["n"] += 1
+    return out
+
+
+@_state_update_op.register_fake
+def _(state, x, dt, a, b, c, d_skip, z, dt_bias, dt_softplus):
+    return x.new_empty((state.shape[0], state.shape[1]))
+
+
+def selective_state_update(state, x, dt, A, B, C, D=None, z=None, dt_bias=None,
+                           dt_softplus=False):
+    """One decode step of the Mamba-1 scan with `state` (batch, dim, N) updated in
+    place; returns y (batch, dim). x, dt, z (batch, dim) and B, C (batch, N) may be
+    strided views (they are read in place); A (dim, N); D, dt_bias (dim,). The
+    semantics of transformers' mamba_selective_state_update, in one kernel; the
+    reference has no counterpart (it leaves decoding to upstream, README.md:320-322)."""
+    f = lambda t: None if t is None else (t if t.dtype == torch.float32 else t.float())
+    return _state_update_op(state, f(x), f(dt), _c(A), f(B), f(C),
+                            None if D is None else _c(D), f(z),
+                            None if dt_bias is None else _c(dt_bias), bool(dt_softplus))
+
+
 @torch.library.custom_op("arm_scan::selective_scan_bidirectional", mutates_args=())
 def _selective_scan_bidir_op(
     u: torch.Tensor,

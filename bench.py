@@ -57,6 +57,9 @@ def parse():
                     help="m1 (default): the headline line below; the others time one of the "
                          "configs 3-5, or the config-2 scan in the HF mixer's layouts "
                          "(m1_seam), alone (for profiling) and print its own line")
+    ap.add_argument("--decode", action="store_true",
+                    help="also time greedy generation (config-2 architecture, batch 1) "
+                         "with and without the patched decode step")
     ap.add_argument("--no-configs", action="store_true",
                     help="skip timing configs 3-5 in the headline line")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -344,6 +347,56 @@ def bench_prefill(args, dev):
                 logits="last position only (logits_to_keep=1)")
 
 
+def bench_decode(dev, new_tokens=64, prompt=128):
+    """Greedy generation with the cache (Mamba-130M architecture, random init, batch 1):
+    ms per new token unpatched, with the scan patched only, and with the decode step
+    patched too (transformers' mamba_selective_state_update)."""
+    import torch
+    from transformers import MambaConfig, MambaForCausalLM
+    from transformers.models.mamba import modeling_mamba
+
+    import armhackathon_amd as arm_scan
+    from armhackathon_amd import hf_patch
+
+    cfg = MambaConfig(vocab_size=50280, hidden_size=768, state_size=16, num_hidden_layers=24,
+                      expand=2, conv_kernel=4, time_step_rank=48)
+    torch.manual_seed(0)
+    model = MambaForCausalLM(cfg).to(dev).float().eval()
+    ids = torch.randint(0, 50280, (1, prompt), device=dev,
+                        generator=torch.Generator(device=dev).manual_seed(1))
+
+    def gen(n):
+        return model.generate(ids, max_new_tokens=n, min_new_tokens=n, do_sample=False)
+
+    def ms_per_token():
+        with torch.no_grad():
+            gen(4)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            gen(1)
+            torch.cuda.synchronize()
+            t1 = time.perf_counter()
+            out = gen(new_tokens + 1)
+            torch.cuda.synchronize()
+            t2 = time.perf_counter()
+        # the prefill and first token cost (t1 - t0); the rest are decode steps
+        return ((t2 - t1) - (t1 - t0)) / new_tokens * 1e3, out
+
+    r = {"batch": 1, "prompt": prompt, "new_tokens": new_tokens}
+    r["unpatched_ms_per_token"], ref = ms_per_token()
+    arm_scan.patch()
+    try:
+        step = modeling_mamba.mamba_selective_state_update
+        modeling_mamba.mamba_selective_state_update = hf_patch._STATE["orig_step"]
+        r["scan_patched_ms_per_token"], _ = ms_per_token()
+        modeling_mamba.mamba_selective_state_update = step
+        r["ms_per_token"], got = ms_per_token()
+    finally:
+        arm_scan.unpatch()
+    r["tokens_identical"] = bool(torch.equal(ref, got))
+    return {k: (round(v, 3) if isinstance(v, float) else v) for k, v in r.items()}
+
+
 def bench_cpu(seconds):
     """The C++ restatement of the reference's x86 scalar path on host cores,
     over a bounded sample: the same layer scan restricted to a slice of
@@ -418,6 +471,7 @@ def main():
         return
     r = bench_scan(args, dev)
     prefill = None if args.no_prefill else bench_prefill(args, dev)
+    decode = bench_decode(dev) if args.decode else None
     configs = None if args.no_configs else {
         name: bench_config(name, dev, steps, 10)
         for name, steps in (("m1_b1", 400), ("m3_siso", 100), ("m3_mimo", 40), ("ss2d", 100))}
@@ -447,6 +501,7 @@ def main():
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic_from_profiles()},
         "prefill": prefill,
+        **({"decode": decode} if decode is not None else {}),
         "other_configs": configs,
         "cpu_baseline": cpu,
     }

@@ -17,8 +17,8 @@
  *   - new entry points: arm_scan_ss2d_f32 (the fused four-direction 2D scan), and
  *     variants for callers' layouts and the fused Mamba-3 angle pre-pass
  *     (arm_scan_selective_scan_strided_f32, arm_scan_mamba3_scan_time_major_f32,
- *     arm_scan_mamba3_scan_angles_f32, arm_scan_mamba3_angles_f32), each described
- *     at its declaration;
+ *     arm_scan_mamba3_scan_angles_f32, arm_scan_mamba3_angles_f32) and the decode
+ *     step arm_scan_selective_state_update_f32, each described at its declaration;
  *   - code 6 reports a HIP launch / device error; arm_scan_last_error() explains
  *     the most recent nonzero code on the calling thread.
  *
@@ -103,6 +103,20 @@ int arm_scan_selective_scan_strided_f32(const ArmScanDims* dims, const float* u,
                                         int delta_softplus, int reverse, float* out,
                                         const long long* out_strides, float* last_state,
                                         const float* h0, void* stream);
+
+/* No reference counterpart (the reference leaves decoding to upstream,
+ * README.md:320-322): one step of the Mamba-1 scan for a generation loop, as
+ * transformers' mamba_selective_state_update computes it, in one launch. state
+ * (batch, dim, state_dim) is read and rewritten in place; x, dt, z are (batch, dim)
+ * and B, C (batch, state_dim), each by element strides (null: contiguous); a
+ * (dim, state_dim); out (batch, dim). dt_bias/dt_softplus as for the scan; d_skip, z
+ * and dt_bias nullable. */
+int arm_scan_selective_state_update_f32(
+    size_t batch, size_t dim, size_t state_dim, float* state, const float* x,
+    const long long* x_strides, const float* dt, const long long* dt_strides, const float* a,
+    const float* b, const long long* b_strides, const float* c, const long long* c_strides,
+    const float* d_skip, const float* z, const long long* z_strides, const float* dt_bias,
+    int dt_softplus, float* out, void* stream);
 
 /* Replaces arm_scan_selective_scan_bidirectional_f32 (arm-scan-ffi/src/lib.rs:235-354):
  * the forward and the reverse scan of the same inputs in one pass sharing exp(delta*A).

@@ -277,3 +277,64 @@ def test_m1_strided_gate_channel_stride(reverse):
         reverse=reverse)
     ref, ref_last = _scan(x, reverse=reverse)
     assert np.array_equal(host(out), host(ref)) and np.array_equal(host(last), host(ref_last))
+
+
+STEP_SHAPES = [(1, 1536, 16), (8, 1536, 16), (3, 40, 5), (2, 7, 1)]
+
+
+@pytest.mark.parametrize("shape", STEP_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_m1_decode_step(shape):
+    """One decode step (the state updated in place) against the oracle's one-step
+    scan from h0 = the state: x, dt and z as strided (b, D) views and B, C as
+    strided (b, N) views, the way a decoder hands them over."""
+    import torch
+
+    import armhackathon_amd as arm_scan
+
+    b, d, n = shape
+    case(f"m1 decode step {shape}")
+    rng = np.random.default_rng(b * d + n)
+    f = np.float32
+    x = rng.standard_normal((b, d)).astype(f)
+    dt = (rng.standard_normal((b, d)) * 0.5).astype(f)
+    z = rng.standard_normal((b, d)).astype(f)
+    A = (-np.exp(rng.uniform(-0.7, 2.7, (d, n)))).astype(f)
+    B = rng.standard_normal((b, n)).astype(f)
+    C = rng.standard_normal((b, n)).astype(f)
+    D = rng.standard_normal(d).astype(f)
+    bias = rng.uniform(-6, -3, d).astype(f)
+    h = rng.standard_normal((b, d, n)).astype(f)
+    ref, ref_h = oracle.selective_scan(x[..., None], dt[..., None], A, B[..., None],
+                                       C[..., None], D=D, z=z[..., None], delta_bias=bias,
+                                       delta_softplus=True, h0=h, dtype=np.float64)
+
+    def strided(a2, extra):  # a (rows, cols) view inside a wider tensor
+        wide = torch.zeros((a2.shape[0], a2.shape[1] + extra), device="cuda")
+        wide[:, extra:] = torch.from_numpy(a2).cuda()
+        return wide[:, extra:]
+
+    t = dev(dict(A=A, D=D, bias=bias, h=h))
+    out = arm_scan.selective_state_update(
+        t["h"], strided(x, 3), strided(dt, 5).t().contiguous().t(), t["A"], strided(B, 2),
+        strided(C, 1), D=t["D"], z=strided(z, 7), dt_bias=t["bias"], dt_softplus=True)
+    assert rel_err(host(out), ref[..., 0]) < TOL
+    assert rel_err(host(t["h"]), ref_h) < TOL
+
+
+def test_m1_decode_step_optional_absent():
+    import armhackathon_amd as arm_scan
+
+    case("m1 decode step without D, z, bias")
+    rng = np.random.default_rng(3)
+    f = np.float32
+    b, d, n = 2, 64, 16
+    x, dt = rng.standard_normal((b, d)).astype(f), np.abs(rng.standard_normal((b, d))).astype(f)
+    A = (-np.exp(rng.uniform(-0.7, 2.7, (d, n)))).astype(f)
+    B, C = rng.standard_normal((b, n)).astype(f), rng.standard_normal((b, n)).astype(f)
+    h = rng.standard_normal((b, d, n)).astype(f)
+    ref, ref_h = oracle.selective_scan(x[..., None], dt[..., None], A, B[..., None],
+                                       C[..., None], h0=h, dtype=np.float64)
+    t = dev(dict(x=x, dt=dt, A=A, B=B, C=C, h=h))
+    out = arm_scan.selective_state_update(t["h"], t["x"], t["dt"], t["A"], t["B"], t["C"])
+    assert rel_err(host(out), ref[..., 0]) < TOL
+    assert rel_err(host(t["h"]), ref_h) < TOL

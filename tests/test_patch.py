@@ -14,6 +14,7 @@ def test_patch_falls_back_on_host_tensors():
     import armhackathon_amd as arm_scan
 
     orig = modeling_mamba.mamba_selective_scan
+    orig_step = modeling_mamba.mamba_selective_state_update
     cfg = MambaConfig(vocab_size=64, hidden_size=16, state_size=4, num_hidden_layers=2,
                       expand=2, conv_kernel=4, time_step_rank=2)
     torch.manual_seed(0)
@@ -24,6 +25,8 @@ def test_patch_falls_back_on_host_tensors():
         targets = arm_scan.patch()
         try:
             assert targets and "mamba_selective_scan" in targets[0]
+            assert any("mamba_selective_state_update" in t for t in targets)
+            assert modeling_mamba.mamba_selective_state_update is not orig_step
             assert arm_scan.patch() == ["transformers mamba_selective_scan (already patched)"]
             assert modeling_mamba.mamba_selective_scan is not orig
             before = arm_scan.stats()
@@ -32,6 +35,7 @@ def test_patch_falls_back_on_host_tensors():
         finally:
             assert arm_scan.unpatch()
     assert modeling_mamba.mamba_selective_scan is orig
+    assert modeling_mamba.mamba_selective_state_update is orig_step
     assert not arm_scan.unpatch()
     assert after["fallback_calls"] - before["fallback_calls"] == 2
     assert after["fast_calls"] == before["fast_calls"]

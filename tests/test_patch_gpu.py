@@ -71,4 +71,5 @@ def test_patch_cached_generation():
         finally:
             arm_scan.unpatch()
     assert st["fast_calls"] >= 3  # the prefill went through the kernel
+    assert st["step_calls"] >= 3 * 11 and st["step_fallback_calls"] == 0  # and the decode
     assert torch.equal(ref, got)
