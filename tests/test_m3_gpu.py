@@ -356,7 +356,7 @@ def test_m3_fused_angles_declines():
 
 PREPASS = [
     # (batch, len, heads, r, half): 16-byte pieces, and the scalar path (r or half
-    # not a multiple of 4, partial last piece), and lengths across the 1024-step tile
+    # not a multiple of 4, partial last piece), and lengths across tiles and segments
     (1, 4096, 24, 32, 64),
     (2, 1500, 4, 16, 16),
     (2, 37, 3, 3, 4),
