@@ -10,6 +10,7 @@ The public names are the reference package's (python/arm_scan/__init__.py:24-42)
     arm_scan.ss2d_scan(u, delta, A, B, C)  # four-direction 2D cross-scan
     arm_scan.mamba3_scan(...), mamba3_scan_pair(...), mamba3_mimo_scan(...)
     arm_scan.ss2d_scan_mamba3(...)
+    arm_scan.noncausal_scan(...), noncausal_scan_dense(...), ss2d_noncausal_mamba3(...)
     arm_scan.selective_scan_numpy(...)     # numpy in/out (copies through HBM)
 
 Every scan runs in hand-written HIP kernels (libarm_scan_hip.so, built from
@@ -31,6 +32,9 @@ __all__ = [
     "mamba3_scan_pair",
     "mamba3_mimo_scan",
     "ss2d_scan_mamba3",
+    "noncausal_scan",
+    "noncausal_scan_dense",
+    "ss2d_noncausal_mamba3",
     "angles_to_cos_sin",
     "selective_scan_numpy",
     "patch",
@@ -53,6 +57,9 @@ _LAZY = {
     "mamba3_mimo_scan": ".mamba3",
     "angles_to_cos_sin": ".mamba3",
     "ss2d_scan_mamba3": ".ss2d_mamba3",
+    "noncausal_scan": ".mamba3_noncausal",
+    "noncausal_scan_dense": ".mamba3_noncausal",
+    "ss2d_noncausal_mamba3": ".mamba3_noncausal",
     "selective_scan_numpy": ".numpy_api",
     "patch": ".hf_patch",
     "unpatch": ".hf_patch",

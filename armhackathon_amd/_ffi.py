@@ -131,6 +131,12 @@ def _declare(lib):
                   _ci, _ci,              # backend threading
                   _vp, _vp, _vp,         # out last_state last_bx
                   _vp]                   # stream
+    f = lib.arm_scan_mamba3_noncausal_f32
+    f.restype = _ci
+    f.argtypes = [ctypes.POINTER(ArmMamba3Dims),
+                  *([_vp] * 12),         # q k v adt dt trap q_bias k_bias cos sin d_skip z
+                  _ci, _ci,              # backend threading
+                  _vp, _vp]              # out stream
     f = lib.arm_scan_mamba3_angles_f32
     f.restype = _ci
     f.argtypes = [_vp, _vp,                      # angles dt
@@ -268,6 +274,18 @@ def mamba3_angles_raw(dims, ptrs, n_angles, backend, threading, ptr_out, ptr_las
         ctypes.byref(dims), *[_p(x) for x in ptrs[:9]], int(n_angles),
         *[_p(x) for x in ptrs[9:]], int(backend), int(threading), ptr_out,
         _p(ptr_last_state), _p(ptr_last_bx), _p(stream))
+    _check(name, code)
+
+
+def mamba3_noncausal_raw(dims, ptrs, backend, threading, ptr_out, *, stream=0):
+    """Call arm_scan_mamba3_noncausal_f32 (SISO, out (b, l, h, dv)) with the 12 input
+    pointers in signature order: q, k, v, adt, dt, trap, q_bias, k_bias, cos, sin,
+    d_skip, z (the last two nullable)."""
+    if len(ptrs) != 12:
+        raise ValueError(f"expected 12 input pointers, got {len(ptrs)}")
+    name = "arm_scan_mamba3_noncausal_f32"
+    code = getattr(load(), name)(ctypes.byref(dims), *[_p(x) for x in ptrs], int(backend),
+                                 int(threading), ptr_out, _p(stream))
     _check(name, code)
 
 

@@ -213,7 +213,8 @@ static int mamba3_call(const ArmMamba3Dims* dims, const float* q, const float* k
                        const float* mimo_psi, const float* mimo_zeta, const float* mimo_phi,
                        int reverse, int backend, int threading, float* out, float* last_state,
                        float* last_bx, void* stream, bool time_major,
-                       const float* angles = nullptr, size_t n_angles = 0) {
+                       const float* angles = nullptr, size_t n_angles = 0,
+                       bool accumulate = false) {
   if (!dims || !q || !k || !v || !adt || !dt || !trap || !q_bias || !k_bias || !out ||
       (angles ? false : (!cos || !sin)))
     return fail(ARM_SCAN_ERR_NULL_POINTER, "a required pointer is null");
@@ -251,6 +252,9 @@ static int mamba3_call(const ArmMamba3Dims* dims, const float* q, const float* k
   p.out_time_major = time_major ? 1 : 0;
   p.angles = angles;
   p.n_angles = n_angles;
+  p.accumulate = accumulate ? 1 : 0;
+  if (accumulate && (mimo || d.rank != 1))
+    return fail(ARM_SCAN_ERR_INVALID_DIMS, "the non-causal sum is SISO (rank 1)");
   if (angles) {
     if (!prod_ok({d.batch, d.len, d.heads, n_angles}))
       return fail(ARM_SCAN_ERR_INVALID_DIMS, "dims overflow size_t");
@@ -299,6 +303,25 @@ int arm_scan_mamba3_scan_angles_f32(
   return mamba3_call(dims, q, k, v, adt, dt, trap, q_bias, k_bias, nullptr, nullptr, d_skip, z,
                      mimo_psi, mimo_zeta, mimo_phi, 0, backend, threading, out, last_state,
                      last_bx, stream, true, angles, n_angles);
+}
+
+int arm_scan_mamba3_noncausal_f32(const ArmMamba3Dims* dims, const float* q, const float* k,
+                                  const float* v, const float* adt, const float* dt,
+                                  const float* trap, const float* q_bias, const float* k_bias,
+                                  const float* cos, const float* sin, const float* d_skip,
+                                  const float* z, int backend, int threading, float* out,
+                                  void* stream) {
+  if (dims && dims->rank != 1)
+    return fail(ARM_SCAN_ERR_INVALID_DIMS, "the non-causal sum is SISO (rank %zu given)",
+                dims->rank);
+  // forward writes out; backward adds its strictly-later terms
+  if (int rc = mamba3_call(dims, q, k, v, adt, dt, trap, q_bias, k_bias, cos, sin, d_skip, z,
+                           nullptr, nullptr, nullptr, 0, backend, threading, out, nullptr,
+                           nullptr, stream, true))
+    return rc;
+  return mamba3_call(dims, q, k, v, adt, dt, trap, q_bias, k_bias, cos, sin, d_skip, z,
+                     nullptr, nullptr, nullptr, 1, backend, threading, out, nullptr, nullptr,
+                     stream, true, nullptr, 0, true);
 }
 
 int arm_scan_mamba3_angles_f32(const float* angles, const float* dt, size_t batch, size_t len,

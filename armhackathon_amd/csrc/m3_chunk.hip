@@ -87,6 +87,8 @@ struct M3K {
   const float* ang;
   int nang, n_ang;
   int rec_floats;  // kRecFloats, or kRecFloatsAng with pi * dt per row
+  // SISO: no same-step term (gamma on M's diagonal, D x) and out += the result
+  int accum;
 };
 
 // ---------------------------------------------------------------------------
@@ -133,7 +135,7 @@ __global__ void __launch_bounds__(256) m3_gates_kernel(M3K p, int reverse) {
     const float cs = __shfl(c, s, 16);
     const float ss = __shfl(scale, s, 16);
     const int step_s = s / R;
-    m[s] = step_s < step ? fexp(c - cs) * ss : (step_s == step ? gamma : 0.0f);
+    m[s] = step_s < step ? fexp(c - cs) * ss : (step_s == step && !p.accum ? gamma : 0.0f);
   }
   if (!valid) return;
   float* rec = p.rec + cidx * p.rec_floats;
@@ -460,7 +462,7 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 2)) m3_chunk_kernel(M3K p) {
 
   if (ewave) {
     // ================= epilogue wave: slice ej =================
-    const float dskip = p.D ? p.D[h] : 0.0f;
+    const float dskip = p.D && !p.accum ? p.D[h] : 0.0f;
     const int pcol = p0 + ej * 16 + li;
     float psi[4], zeta[4], phi[4];
 #pragma unroll
@@ -478,6 +480,14 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 2)) m3_chunk_kernel(M3K p) {
                                 : (((long long)bi * H + h) * L + t0) * dv);
     Stash st = {};
     auto epilogue = [&](int ch) {
+      float* orow = out_lane + (REV ? -(long long)ch : (long long)ch) * T * ostep;
+      // the other traversal's output, under accumulation (loaded first, used last)
+      float prev[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      if (p.accum) {
+#pragma unroll
+        for (int r = 0; r < 4; r += R)
+          if (ch * T + (4 * lj + r) / R < L) prev[r] = orow[(REV ? -(r / R) : r / R) * ostep];
+      }
       const float* gb = gbuf + (ch & 1) * kMaxWaves * 256;
       const float* yb = ybuf + ((ch & 1) * PT + ej) * kMaxWaves * 256;
       f4 gs[kMaxWaves], ys[kMaxWaves];  // all reads in flight at once
@@ -497,11 +507,10 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 2)) m3_chunk_kernel(M3K p) {
       f4 Y = ys[0] * st.ec;  // lane holds Y[row = 4lj + r][p], the inter-chunk part
 #pragma unroll
       for (int m = 0; m < 4; ++m) Y = mfma(G[m], st.x[m], Y);
-      float* orow = out_lane + (REV ? -(long long)ch : (long long)ch) * T * ostep;
 #pragma unroll
       for (int r = 0; r < 4; r += R) {
         if (ch * T + (4 * lj + r) / R < L) {
-          float acc = 0.0f;
+          float acc = prev[r];
 #pragma unroll
           for (int rr = 0; rr < R; ++rr) {
             float term = Y[r + rr] + dskip * st.x[r + rr];
@@ -757,6 +766,7 @@ hipError_t m3_scan_chunked(const M3Problem& pr, hipStream_t st) {
   k.psi = pr.psi; k.zeta = pr.zeta; k.phi = pr.phi;
   k.out = pr.out; k.last_state = pr.last_state; k.last_bx = pr.last_bx;
   k.out_tm = pr.out_time_major;
+  k.accum = pr.accumulate;
   k.heads = (int)pr.heads; k.dv = (int)pr.dv; k.dqk = (int)pr.dqk;
   k.len = (int)pr.len; k.groups = (int)pr.groups;
   const int R = (int)pr.rank;

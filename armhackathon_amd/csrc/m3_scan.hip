@@ -35,7 +35,7 @@ constexpr size_t kM3MaxLdsFloats = 15 * 1024;  // 60 KB
 struct M3Args {
   const float *q, *k, *v, *adt, *dt, *trap, *qb, *kb, *cos, *sin, *D, *z, *psi, *zeta, *phi;
   float *out, *last_state, *last_bx;
-  int heads, dv, dqk, len, rank, groups, reverse, mimo, out_tm;
+  int heads, dv, dqk, len, rank, groups, reverse, mimo, out_tm, accumulate;
 };
 
 __global__ void __launch_bounds__(kM3Threads) m3_seq_kernel(M3Args p) {
@@ -133,9 +133,10 @@ __global__ void __launch_bounds__(kM3Threads) m3_seq_kernel(M3Args p) {
     for (int pp = tid; pp < dv; pp += kM3Threads) {
       float o;
       if (!p.mimo) {
-        const float diag = dskip + gamma * gram[0];
+        const float diag = p.accumulate ? 0.0f : dskip + gamma * gram[0];
         o = fmaf(alpha, acc[pp], diag * xs[pp]);
         if (p.z) o *= silu(p.z[v_off + pp]);
+        if (p.accumulate) o += dst[pp];  // the other traversal's output
       } else {
         o = 0.0f;
         const float zz = p.z ? p.z[v_off + pp] : 0.0f;
@@ -200,6 +201,8 @@ bool m3_angles_supported(const M3Problem& pr, const char** why) {
 }
 
 hipError_t m3_scan(const M3Problem& pr, hipStream_t st) {
+  if (pr.accumulate && (pr.psi != nullptr || pr.rank != 1 || pr.angles))
+    return hipErrorInvalidValue;  // the non-causal sum is defined for SISO on cos/sin
   if (pr.angles) {
     if (!m3_angles_supported(pr, nullptr)) return hipErrorInvalidValue;
     return m3_scan_chunked(pr, st);
@@ -220,6 +223,7 @@ hipError_t m3_scan_sequential(const M3Problem& pr, hipStream_t st) {
   a.rank = (int)pr.rank; a.groups = (int)pr.groups; a.reverse = pr.reverse;
   a.mimo = pr.psi != nullptr;
   a.out_tm = pr.out_time_major;
+  a.accumulate = pr.accumulate;
   const unsigned blocks = (unsigned)(pr.batch * pr.heads);
   hipLaunchKernelGGL(m3_seq_kernel, dim3(blocks), dim3(kM3Threads), fl * sizeof(float), st, a);
   return hipGetLastError();

@@ -80,6 +80,11 @@ struct M3Problem {
   // raw angles (b, l, h, n_angles) in place of cos/sin: the pre-pass fused
   const float* angles;
   size_t n_angles;
+  // SISO only: leave the same-step term (gamma q.k + D) out of every output and add
+  // the result to what out already holds. Run as the second traversal after the
+  // other direction has written out, that gives the non-causal sum
+  // forward + backward - diagonal (python/arm_scan/mamba3_noncausal.py:89-98).
+  int accumulate;
 };
 
 // Largest dv * dqk the Mamba-3 kernel holds on chip.

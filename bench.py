@@ -52,7 +52,8 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--workload", choices=("m1", "m1_b1", "m1_seam", "m3_siso", "m3_mimo",
                                            "ss2d",
-                                           "m3_siso_angles", "m3_mimo_angles"),
+                                           "m3_siso_angles", "m3_mimo_angles",
+                                           "m3_noncausal"),
                     default="m1",
                     help="m1 (default): the headline line below; the others time one of the "
                          "configs 3-5, or the config-2 scan in the HF mixer's layouts "
@@ -144,7 +145,10 @@ def config_inputs(name, dev):
             workloads.m3_mimo(seed=4)
         x = workloads.m3_with_angles(base, seed=6)
         return {k: torch.from_numpy(v).to(dev) for k, v in x.items()}, workloads.m3_bytes(x)
-    if name == "m3_siso":
+    if name == "m3_noncausal":
+        x = workloads.m3_siso(seed=3)
+        nbytes = workloads.m3_bytes(x, want_state=False)
+    elif name == "m3_siso":
         x = workloads.m3_siso(seed=3)
         nbytes = workloads.m3_bytes(x)
     elif name == "m3_mimo":
@@ -165,6 +169,9 @@ CONFIG_NAMES = {
     "m3_siso": "config 3: Mamba-3 SISO B4 L4096 24 heads x 64, dqk 128 (final states too)",
     "m3_siso_angles": "config 3 from raw angles (b, l, h, 32): the angle pre-pass fused",
     "m3_mimo_angles": "config 4 from raw angles (b, l, h, 32): the angle pre-pass fused",
+    "m3_noncausal": "config 3 shapes aggregated non-causally (every position over every "
+                    "other): forward traversal, then the backward one accumulated without "
+                    "the same-step term",
     "m3_mimo": "config 4: Mamba-3 MIMO rank 4, B4 L4096 24 heads x 64, dqk 128 (final state)",
     "ss2d": "config 5: SS2D 4 directions, B16 D192 64x64 N16, D, z, merge sum (final states)",
 }
@@ -208,6 +215,9 @@ def bench_config(name, dev, steps, warmup):
             return arm_scan.mamba3_mimo_scan(*[t[k] for k in K], t["psi"], t["zeta"],
                                              t["phi"], angles=t["angles"],
                                              return_last_state=True)
+    elif name == "m3_noncausal":
+        def call():
+            return arm_scan.noncausal_scan(*[t[k] for k in K], cos=t["cos"], sin=t["sin"])
     elif name == "m3_siso":
         def call():
             return arm_scan.mamba3_scan(*[t[k] for k in K], cos=t["cos"], sin=t["sin"],
@@ -255,6 +265,29 @@ def bench_config(name, dev, steps, warmup):
         stop.record(stream)
         torch.cuda.synchronize()
         extra["unfused_ms_per_call"] = round(start.elapsed_time(stop) / steps, 4)
+    if name == "m3_noncausal":
+        # the reference's composition on the same kernels: both traversals into two
+        # outputs, then forward + backward - the same-step term in torch ops
+        # (python/arm_scan/mamba3_noncausal.py:47-98)
+        def pair_route():
+            fwd, bwd = arm_scan.mamba3_scan_pair(*[t[k] for k in K], cos=t["cos"],
+                                                 sin=t["sin"])
+            qk = ((t["q"] + t["q_bias"]) * (t["k"] + t["k_bias"])).sum(-1)  # (b, l, h)
+            gamma = (t["dt"] * torch.sigmoid(t["trap"])).permute(0, 2, 1)
+            return fwd + bwd - (gamma * qk).unsqueeze(-1) * t["v"]
+
+        def causal():
+            return arm_scan.mamba3_scan(*[t[k] for k in K], cos=t["cos"], sin=t["sin"])
+        for key, fn in (("pair_route_ms_per_call", pair_route),
+                        ("causal_ms_per_call", causal)):
+            for _ in range(warmup):
+                fn()
+            start.record(stream)
+            for _ in range(steps):
+                fn()
+            stop.record(stream)
+            torch.cuda.synchronize()
+            extra[key] = round(start.elapsed_time(stop) / steps, 4)
     del t
     torch.cuda.empty_cache()
     return dict(workload=CONFIG_NAMES[name], ms_per_call=round(ms, 4), bytes_per_call=nbytes,
@@ -289,6 +322,18 @@ def bench_config_cpu(name, seconds):
 
         def call():
             oracle.mamba3_scan(*[x[k] for k in K], x["cos"], x["sin"], want_state=True)
+    elif name == "m3_noncausal":
+        from oracle import naive
+        x = workloads.m3_siso(batch=1, seed=3)
+        nbytes = workloads.m3_bytes(x, want_state=False)
+        sample = "batch 1 of config 3, both traversals and the same-step term"
+
+        def call():
+            args = [x[k] for k in K] + [x["cos"], x["sin"]]
+            fwd = oracle.mamba3_scan(*args)
+            bwd = oracle.mamba3_scan(*args, reverse=True)
+            return fwd + bwd - naive.m3_same_step(x["q"], x["k"], x["v"], x["dt"], x["trap"],
+                                                  x["q_bias"], x["k_bias"]).transpose(0, 2, 1, 3)
     elif name == "m3_mimo":
         x = workloads.m3_mimo(batch=1, seed=4)
         nbytes, sample = workloads.m3_bytes(x), "batch 1 of config 4"
@@ -474,7 +519,8 @@ def main():
     decode = bench_decode(dev) if args.decode else None
     configs = None if args.no_configs else {
         name: bench_config(name, dev, steps, 10)
-        for name, steps in (("m1_b1", 400), ("m3_siso", 100), ("m3_mimo", 40), ("ss2d", 100))}
+        for name, steps in (("m1_b1", 400), ("m3_siso", 100), ("m3_mimo", 40), ("ss2d", 100),
+                            ("m3_noncausal", 50))}
     cpu = None if args.no_cpu else bench_cpu(args.cpu_seconds)
     if configs is not None and not args.no_cpu:
         for name in configs:

@@ -17,8 +17,9 @@
  *   - new entry points: arm_scan_ss2d_f32 (the fused four-direction 2D scan), and
  *     variants for callers' layouts and the fused Mamba-3 angle pre-pass
  *     (arm_scan_selective_scan_strided_f32, arm_scan_mamba3_scan_time_major_f32,
- *     arm_scan_mamba3_scan_angles_f32, arm_scan_mamba3_angles_f32) and the decode
- *     step arm_scan_selective_state_update_f32, each described at its declaration;
+ *     arm_scan_mamba3_scan_angles_f32, arm_scan_mamba3_angles_f32), the decode
+ *     step arm_scan_selective_state_update_f32 and the non-causal Mamba-3 sum
+ *     arm_scan_mamba3_noncausal_f32, each described at its declaration;
  *   - code 6 reports a HIP launch / device error; arm_scan_last_error() explains
  *     the most recent nonzero code on the calling thread.
  *
@@ -174,6 +175,21 @@ int arm_scan_mamba3_scan_angles_f32(
  * half) with theta = cumsum_len(tanh(angle) * pi * dt); pairs n_angles .. half-1 get
  * cos 1, sin 0. Feeds arm_scan_mamba3_scan[_time_major]_f32 where the fused entry
  * point does not apply (reverse, MIMO, n_angles not a multiple of 4). */
+/* No reference counterpart: the non-causal Mamba-3 SISO aggregation, which the
+ * reference composes in Python over its two traversals (python/arm_scan/
+ * mamba3_noncausal.py:89-98: forward + backward - the same-step term counted twice).
+ * Arguments are arm_scan_mamba3_scan_f32's for rank 1 without the MIMO projections,
+ * carries or direction; out is written TIME-MAJOR (batch, len, heads, dv). The
+ * forward traversal writes out; the backward one leaves the same-step term
+ * (gamma q.k + D) out and adds onto it, so no second output and no diagonal pass
+ * exist. ARM_SCAN_ERR_INVALID_DIMS for rank != 1. */
+int arm_scan_mamba3_noncausal_f32(const ArmMamba3Dims* dims, const float* q, const float* k,
+                                  const float* v, const float* adt, const float* dt,
+                                  const float* trap, const float* q_bias, const float* k_bias,
+                                  const float* cos, const float* sin, const float* d_skip,
+                                  const float* z, int backend, int threading, float* out,
+                                  void* stream);
+
 int arm_scan_mamba3_angles_f32(const float* angles, const float* dt, size_t batch, size_t len,
                                size_t heads, size_t n_angles, size_t half, float* cos,
                                float* sin, void* stream);

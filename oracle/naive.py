@@ -13,6 +13,10 @@ operand, the wrong trapezoid neighbour under reverse) shows up as a mismatch:
 * `m3_siso_dense`: the O(L^2) dual (attention-like) form of the same SISO
   recurrence — no state matrix at all.
 * `m3_mimo_scan`: the rank-r sequential form, einsum-free.
+* `m3_noncausal_dense`: the non-causal (and, with causal=True, the causal) O(L^2)
+  mask form with every weight a running product of decays (no cumsum), and
+  `m3_same_step`, the same-step term from UNROTATED q/k, so that
+  forward + backward - same-step == dense also pins RoPE's invariance of q_t . k_t.
 
 Only for small shapes: these are loops in numpy.
 """
@@ -168,6 +172,70 @@ def m3_siso_dense(q, k, v, adt, dt, trap, q_bias, k_bias, cos, sin, D=None, z=No
                  decay * scale[..., None, :], 0.0)
     idx = np.arange(L)
     W[..., idx, idx] = gamma
+    out = np.einsum("bhts,bshp->bthp", G * W, v)
+    if D is not None:
+        out = out + np.asarray(D, np.float64)[None, None, :, None] * v
+    if z is not None:
+        out = out * silu(z)
+    return out
+
+
+def m3_same_step(q, k, v, dt, trap, q_bias, k_bias, D=None, z=None):
+    """The s == t term of Mamba-3 SISO, (D + gamma_t (q_t . k_t)) v_t, gated
+    (python/arm_scan/mamba3_noncausal.py:47-86). q_t . k_t from q + bias, k + bias
+    WITHOUT rotation: RoPE turns both by the same angle at one position."""
+    v = np.asarray(v, np.float64)
+    b, L, h, dv = v.shape
+    g = q.shape[-2]
+    hidx = np.arange(h) // (h // g)
+    qb = np.asarray(q, np.float64)[..., hidx, :] + np.asarray(q_bias, np.float64)
+    kb = np.asarray(k, np.float64)[..., hidx, :] + np.asarray(k_bias, np.float64)
+    gamma = np.asarray(dt, np.float64) * sigmoid(trap)  # (b, h, L)
+    coef = gamma.transpose(0, 2, 1) * (qb * kb).sum(-1)  # (b, L, h)
+    if D is not None:
+        coef = coef + np.asarray(D, np.float64)
+    out = coef[..., None] * v
+    return out if z is None else out * silu(z)
+
+
+def m3_noncausal_dense(q, k, v, adt, dt, trap, q_bias, k_bias, cos, sin, D=None, z=None,
+                       causal=False):
+    """Mamba-3 SISO over every position (python/arm_scan/mamba3_noncausal.py:101-178)
+    in float64: y_t = sum_s W[t, s] (q_t . k_s) v_s + D v_t, gated, with
+
+      W[t, s] = alpha_{s+1} ... alpha_t * scale_s          s < t (forward trapezoid,
+                                                           scale_s = gamma_s + dt_{s+1}(1 - lam_{s+1}))
+      W[t, t] = gamma_t
+      W[t, s] = alpha_t ... alpha_{s-1} * scale'_s         s > t (backward traversal,
+                                                           scale'_s = gamma_s + dt_{s-1}(1 - lam_{s-1}))
+
+    alpha = exp(adt), lam = sigmoid(trap); the s > t half is dropped when causal.
+    """
+    v = np.asarray(v, np.float64)
+    b, L, h, dv = v.shape
+    q, k = _m3_prep(q, k, v, adt, dt, trap, q_bias, k_bias, cos, sin, z, h,
+                    _rope_interleaved)
+    dt = np.asarray(dt, np.float64)
+    lam = sigmoid(trap)
+    alpha = np.exp(np.asarray(adt, np.float64))
+    gamma = dt * lam
+    scale_f = gamma.copy()
+    scale_f[..., :-1] += dt[..., 1:] * (1.0 - lam[..., 1:])
+    scale_b = gamma.copy()
+    scale_b[..., 1:] += dt[..., :-1] * (1.0 - lam[..., :-1])
+    W = np.zeros((b, h, L, L))
+    for t in range(L):
+        W[..., t, t] = gamma[..., t]
+        decay = np.ones((b, h))
+        for s in range(t - 1, -1, -1):
+            decay = decay * alpha[..., s + 1]
+            W[..., t, s] = decay * scale_f[..., s]
+        if not causal:
+            decay = np.ones((b, h))
+            for s in range(t + 1, L):
+                decay = decay * alpha[..., s - 1]
+                W[..., t, s] = decay * scale_b[..., s]
+    G = np.einsum("bthn,bshn->bhts", q, k)
     out = np.einsum("bhts,bshp->bthp", G * W, v)
     if D is not None:
         out = out + np.asarray(D, np.float64)[None, None, :, None] * v

@@ -87,6 +87,20 @@ def test_m3_rejections():
     assert _m3(ok, psi=FAKE, zeta=FAKE, phi=FAKE, ls=FAKE, lb=FAKE) == 2  # MIMO last_bx
 
 
+def test_m3_noncausal_rejections():
+    L = _ffi.load()
+    D = _ffi.ArmMamba3Dims
+
+    def call(dims, q=FAKE):
+        return L.arm_scan_mamba3_noncausal_f32(ctypes.byref(dims), q, FAKE, FAKE, FAKE, FAKE,
+                                               FAKE, FAKE, FAKE, FAKE, FAKE, None, None, 0,
+                                               0, FAKE, None)
+
+    assert call(D(1, 2, 4, 4, 3, 2, 1)) == 2   # the non-causal sum is rank 1
+    assert call(D(1, 2, 4, 4, 3, 1, 1), q=None) == 1
+    assert call(D(1, 2, 4, 5, 3, 1, 1)) == 2   # odd dqk
+
+
 def test_ss2d_rejections():
     L = _ffi.load()
     d = _ffi.ArmSS2DDims(1, 2, 3, 3, 4)

@@ -298,6 +298,35 @@ def test_m3_siso_independent_forms():
         np.testing.assert_allclose(out.transpose(0, 2, 1, 3), dense, rtol=1e-9, atol=1e-11)
 
 
+def test_m3_noncausal_forms():
+    """Non-causal Mamba-3 (python/arm_scan/mamba3_noncausal.py:89-98, 101-178), pinned
+    the way tests/check_mamba3_noncausal.py pins it, in float64:
+    * the mask form restricted to its causal half == the forward scan;
+    * the full mask form == forward + backward - same-step (the recurrent route,
+      with the same-step term from unrotated q/k);
+    * it differs from the causal scan once L > 1 and equals it at L = 1."""
+    keys = ("q", "k", "v", "adt", "dt", "trap", "q_bias", "k_bias", "cos", "sin")
+    for seed, (b, L, h, dv, dqk, g) in enumerate(
+            [(1, 8, 2, 4, 8, 1), (2, 19, 4, 8, 12, 2), (1, 33, 3, 6, 16, 1)]):
+        x = _m3_rand(20 + seed, b=b, L=L, h=h, dv=dv, dqk=dqk, g=g)
+        args = [x[k] for k in keys]
+        fwd = oracle.mamba3_scan(*args, D=x["D"], z=x["z"], dtype=np.float64)
+        bwd = oracle.mamba3_scan(*args, D=x["D"], z=x["z"], reverse=True, dtype=np.float64)
+        fwd, bwd = fwd.transpose(0, 2, 1, 3), bwd.transpose(0, 2, 1, 3)
+        causal = naive.m3_noncausal_dense(*args, D=x["D"], z=x["z"], causal=True)
+        np.testing.assert_allclose(causal, fwd, rtol=1e-10, atol=1e-12)
+        full = naive.m3_noncausal_dense(*args, D=x["D"], z=x["z"])
+        diag = naive.m3_same_step(x["q"], x["k"], x["v"], x["dt"], x["trap"], x["q_bias"],
+                                  x["k_bias"], D=x["D"], z=x["z"])
+        np.testing.assert_allclose(full, fwd + bwd - diag, rtol=1e-10, atol=1e-12)
+        assert np.abs(full - fwd).max() > 1e-3 * np.abs(fwd).max()
+    x = _m3_rand(30, L=1)
+    args = [x[k] for k in keys]
+    np.testing.assert_allclose(naive.m3_noncausal_dense(*args, D=x["D"], z=x["z"]),
+                               naive.m3_noncausal_dense(*args, D=x["D"], z=x["z"],
+                                                        causal=True), rtol=0, atol=0)
+
+
 def test_m3_groups_equal_per_head_slices():
     """groups=heads (extension) == running each head alone with the v7 layout."""
     x = _m3_rand(5, g=4, h=4)
