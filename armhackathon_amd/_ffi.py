@@ -131,6 +131,24 @@ def _declare(lib):
                   _ci, _ci,              # backend threading
                   _vp, _vp, _vp,         # out last_state last_bx
                   _vp]                   # stream
+    f = lib.arm_scan_mamba3_scan_strided_f32
+    f.restype = _ci
+    f.argtypes = [ctypes.POINTER(ArmMamba3Dims),
+                  _vp, _vp, _vp, _vp,    # q k v v_strides
+                  *([_vp] * 5),          # adt dt trap q_bias k_bias
+                  _vp, ctypes.c_size_t, _vp,   # angles n_angles angle_strides
+                  _vp, _vp, _vp,         # d_skip z z_strides
+                  _vp, _vp, _vp,         # psi zeta phi
+                  _ci, _ci,              # backend threading
+                  _vp, _vp]              # out stream
+    f = lib.arm_scan_mamba3_block_frontend_f32
+    f.restype = _ci
+    f.argtypes = [_vp, *([ctypes.c_size_t] * 9),   # proj batch len row_stride heads
+                                                   # headdim d_state rank groups n_angles
+                  _vp, ctypes.c_float, _vp, _vp,   # dt_bias a_floor b_norm c_norm
+                  ctypes.c_float,                  # norm_eps
+                  *([_vp] * 5),                    # q k adt dt trap
+                  _vp]                             # stream
     f = lib.arm_scan_mamba3_noncausal_f32
     f.restype = _ci
     f.argtypes = [ctypes.POINTER(ArmMamba3Dims),
@@ -287,6 +305,40 @@ def mamba3_noncausal_raw(dims, ptrs, backend, threading, ptr_out, *, stream=0):
     code = getattr(load(), name)(ctypes.byref(dims), *[_p(x) for x in ptrs], int(backend),
                                  int(threading), ptr_out, _p(stream))
     _check(name, code)
+
+
+def _i64x(vals):
+    return (ctypes.c_int64 * len(vals))(*[int(v) for v in vals])
+
+
+def mamba3_strided_raw(dims, ptrs, strides, n_angles, backend, threading, ptr_out, *,
+                       stream=0):
+    """Call arm_scan_mamba3_scan_strided_f32 (forward, from raw angles, out (b, l, h, dv)).
+    ptrs: q, k, v, adt, dt, trap, q_bias, k_bias, angles, d_skip, z, psi, zeta, phi (the
+    last five nullable); strides: dict with "v" (batch, step), "angles" (batch, step,
+    head) and, with z, "z" (batch, step), in elements."""
+    if len(ptrs) != 14:
+        raise ValueError(f"expected 14 input pointers, got {len(ptrs)}")
+    q, k, v, adt, dt, trap, qb, kb, ang, d_skip, z, psi, zeta, phi = ptrs
+    vs, angs = _i64x(strides["v"]), _i64x(strides["angles"])
+    zs = _i64x(strides["z"]) if z else None
+    name = "arm_scan_mamba3_scan_strided_f32"
+    code = getattr(load(), name)(
+        ctypes.byref(dims), _p(q), _p(k), _p(v), vs, _p(adt), _p(dt), _p(trap), _p(qb), _p(kb),
+        _p(ang), int(n_angles), angs, _p(d_skip), _p(z), zs, _p(psi), _p(zeta), _p(phi),
+        int(backend), int(threading), ptr_out, _p(stream))
+    _check(name, code)
+
+
+def block_frontend_raw(ptr_proj, batch, length, row_stride, heads, headdim, d_state, rank,
+                       groups, n_angles, ptr_dt_bias, a_floor, ptr_b_norm, ptr_c_norm,
+                       norm_eps, ptr_q, ptr_k, ptr_adt, ptr_dt, ptr_trap, *, stream=0):
+    """Call arm_scan_mamba3_block_frontend_f32 (the Mamba-3 mixer's front-end)."""
+    code = load().arm_scan_mamba3_block_frontend_f32(
+        ptr_proj, batch, length, row_stride, heads, headdim, d_state, rank, groups, n_angles,
+        ptr_dt_bias, float(a_floor), ptr_b_norm, ptr_c_norm, float(norm_eps), ptr_q, ptr_k,
+        ptr_adt, ptr_dt, ptr_trap, _p(stream))
+    _check("arm_scan_mamba3_block_frontend_f32", code)
 
 
 def angles_raw(ptr_angles, ptr_dt, batch, length, heads, n_angles, half, ptr_cos, ptr_sin,

@@ -91,7 +91,8 @@ hipError_t stream_alloc(void** p, size_t bytes, hipStream_t st) {
     hipMemPool_t pool;
     if (hipDeviceGetDefaultMemPool(&pool, dev) == hipSuccess) {
       uint64_t keep = UINT64_MAX;
-      hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep);
+      // best effort: without it freed scratch returns to the device between calls
+      (void)hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep);
     }
     pools_set.fetch_or(bit);
   }
@@ -214,7 +215,9 @@ static int mamba3_call(const ArmMamba3Dims* dims, const float* q, const float* k
                        int reverse, int backend, int threading, float* out, float* last_state,
                        float* last_bx, void* stream, bool time_major,
                        const float* angles = nullptr, size_t n_angles = 0,
-                       bool accumulate = false) {
+                       bool accumulate = false, const int64_t* v_strides = nullptr,
+                       const int64_t* z_strides = nullptr,
+                       const int64_t* angle_strides = nullptr, bool unfused_ok = false) {
   if (!dims || !q || !k || !v || !adt || !dt || !trap || !q_bias || !k_bias || !out ||
       (angles ? false : (!cos || !sin)))
     return fail(ARM_SCAN_ERR_NULL_POINTER, "a required pointer is null");
@@ -255,11 +258,39 @@ static int mamba3_call(const ArmMamba3Dims* dims, const float* q, const float* k
   p.accumulate = accumulate ? 1 : 0;
   if (accumulate && (mimo || d.rank != 1))
     return fail(ARM_SCAN_ERR_INVALID_DIMS, "the non-causal sum is SISO (rank 1)");
+  for (int i = 0; i < 3; ++i) {
+    if ((i < 2 && v_strides && v_strides[i] < 0) || (i < 2 && z_strides && z_strides[i] < 0) ||
+        (angle_strides && angle_strides[i] < 0))
+      return fail(ARM_SCAN_ERR_INVALID_DIMS, "strides must be non-negative");
+    if (i < 2 && v_strides) p.v_strides[i] = (long long)v_strides[i];
+    if (i < 2 && z_strides) p.z_strides[i] = (long long)z_strides[i];
+    if (angle_strides) p.ang_strides[i] = (long long)angle_strides[i];
+  }
+  armscan::m3_fill_strides(p);
   if (angles) {
     if (!prod_ok({d.batch, d.len, d.heads, n_angles}))
       return fail(ARM_SCAN_ERR_INVALID_DIMS, "dims overflow size_t");
+    if (n_angles == 0 || n_angles > d.dqk / 2)
+      return fail(ARM_SCAN_ERR_INVALID_DIMS, "n_angles (%zu) must be 1 .. dqk/2", n_angles);
     const char* why = nullptr;
-    if (!armscan::m3_angles_supported(p, &why)) return fail(ARM_SCAN_ERR_INVALID_DIMS, "%s", why);
+    if (!armscan::m3_angles_supported(p, &why)) {
+      if (!unfused_ok) return fail(ARM_SCAN_ERR_INVALID_DIMS, "%s", why);
+      // the pre-pass kernels into scratch cos/sin, then the scan on them
+      const size_t half = d.dqk / 2, n_cs = d.batch * d.len * d.heads * half;
+      hipStream_t st = (hipStream_t)stream;
+      float* cs = nullptr;
+      hipError_t e = armscan::stream_alloc((void**)&cs, 2 * n_cs * sizeof(float), st);
+      if (e != hipSuccess) return hip_fail(e, "angle scratch allocation");
+      e = armscan::m3_angles_to_cos_sin(angles, dt, d.batch, d.len, d.heads, n_angles, half, cs,
+                                        cs + n_cs, st, p.ang_strides);
+      p.angles = nullptr;
+      p.n_angles = 0;
+      p.cos = cs;
+      p.sin = cs + n_cs;
+      if (e == hipSuccess) e = armscan::m3_scan(p, st);
+      const hipError_t ef = hipFreeAsync(cs, st);
+      return run(e != hipSuccess ? e : ef, "mamba3 (angle pre-pass, then scan) launch");
+    }
   }
   // the chunked MFMA kernel takes dv, dqk multiples of 16 (dqk <= 128) and rank 1/2/4;
   // everything else runs the step-by-step kernel, whose state must fit in LDS
@@ -303,6 +334,56 @@ int arm_scan_mamba3_scan_angles_f32(
   return mamba3_call(dims, q, k, v, adt, dt, trap, q_bias, k_bias, nullptr, nullptr, d_skip, z,
                      mimo_psi, mimo_zeta, mimo_phi, 0, backend, threading, out, last_state,
                      last_bx, stream, true, angles, n_angles);
+}
+
+int arm_scan_mamba3_scan_strided_f32(
+    const ArmMamba3Dims* dims, const float* q, const float* k, const float* v,
+    const int64_t* v_strides, const float* adt, const float* dt, const float* trap,
+    const float* q_bias, const float* k_bias, const float* angles, size_t n_angles,
+    const int64_t* angle_strides, const float* d_skip, const float* z, const int64_t* z_strides,
+    const float* mimo_psi, const float* mimo_zeta, const float* mimo_phi, int backend,
+    int threading, float* out, void* stream) {
+  if (!angles || !v_strides || !angle_strides || (z && !z_strides))
+    return fail(ARM_SCAN_ERR_NULL_POINTER, "a required pointer is null");
+  return mamba3_call(dims, q, k, v, adt, dt, trap, q_bias, k_bias, nullptr, nullptr, d_skip, z,
+                     mimo_psi, mimo_zeta, mimo_phi, 0, backend, threading, out, nullptr,
+                     nullptr, stream, true, angles, n_angles, false, v_strides,
+                     z ? z_strides : nullptr, angle_strides, true);
+}
+
+int arm_scan_mamba3_block_frontend_f32(
+    const float* proj, size_t batch, size_t len, size_t row_stride, size_t heads,
+    size_t headdim, size_t d_state, size_t rank, size_t groups, size_t n_angles,
+    const float* dt_bias, float a_floor, const float* b_norm_weight, const float* c_norm_weight,
+    float norm_eps, float* q, float* k, float* adt, float* dt, float* trap, void* stream) {
+  if (!proj || !dt_bias || !b_norm_weight || !c_norm_weight || !q || !k || !adt || !dt ||
+      !trap)
+    return fail(ARM_SCAN_ERR_NULL_POINTER, "a required pointer is null");
+  if (!batch || !len || !heads || !headdim || !d_state || !rank || !groups)
+    return fail(ARM_SCAN_ERR_INVALID_DIMS, "a dimension is zero");
+  if (heads % groups)
+    return fail(ARM_SCAN_ERR_INVALID_DIMS, "groups (%zu) does not divide heads (%zu)", groups,
+                heads);
+  if (batch > 65535 || len > (1u << 30) || heads > 4096 || d_state > (1u << 20) ||
+      rank * groups > 4096 || headdim > (1u << 20))
+    return fail(ARM_SCAN_ERR_INVALID_DIMS, "problem too large for this build");
+  const size_t need = 2 * heads * headdim + 2 * rank * groups * d_state + 3 * heads + n_angles;
+  if (row_stride < need)
+    return fail(ARM_SCAN_ERR_INVALID_DIMS,
+                "row_stride (%zu) is shorter than the projection's columns (%zu)", row_stride,
+                need);
+  if (!prod_ok({batch, len, row_stride}) || !prod_ok({batch, len, rank, groups, d_state}))
+    return fail(ARM_SCAN_ERR_INVALID_DIMS, "dims overflow size_t");
+  if (!(norm_eps >= 0.0f) || !(a_floor == a_floor))
+    return fail(ARM_SCAN_ERR_INVALID_DIMS, "norm_eps must be >= 0 and a_floor a number");
+  armscan::M3Frontend f{};
+  f.proj = proj; f.row_stride = (long long)row_stride;
+  f.batch = (int)batch; f.len = (int)len; f.heads = (int)heads; f.headdim = (int)headdim;
+  f.d_state = (int)d_state; f.rank = (int)rank; f.groups = (int)groups;
+  f.dt_bias = dt_bias; f.b_norm = b_norm_weight; f.c_norm = c_norm_weight;
+  f.a_floor = a_floor; f.eps = norm_eps;
+  f.q = q; f.k = k; f.adt = adt; f.dt = dt; f.trap = trap;
+  return run(armscan::m3_frontend(f, (hipStream_t)stream), "mamba3 front-end launch");
 }
 
 int arm_scan_mamba3_noncausal_f32(const ArmMamba3Dims* dims, const float* q, const float* k,

@@ -36,6 +36,7 @@ struct AngK {
   int L, H, r, half;
   long long nlines;  // (batch * heads) * ceil(half / 32)
   int vec;           // 16-byte pieces for angles (r % 4 == 0) and cos/sin (half % 4 == 0)
+  long long ab, at, ah;  // element strides of the angles: batch, step, head
   int segs, seg_len;  // sequence segments per line, steps per segment (multiple of kTile)
   float* seg_tot;     // [nlines][segs][32]: the increments summed over each segment
 };
@@ -70,8 +71,8 @@ struct AngLine {
     sinp = p.sin + (b * p.L * p.H + h) * p.half + u0;
     nu = u0 >= p.half ? 0 : (p.half - u0 < 4 ? p.half - u0 : 4);  // pairs here
     na = u0 >= p.r ? 0 : (p.r - u0 < 4 ? p.r - u0 : 4);           // pairs with an angle
-    angp = p.ang + (b * p.L * p.H + h) * p.r + u0;
-    astride = (long long)p.H * p.r;
+    angp = p.ang + b * p.ab + h * p.ah + u0;
+    astride = p.at;
     dtp = p.dt + bh * p.L;
   }
 
@@ -227,14 +228,22 @@ __global__ void __launch_bounds__(kAngThreads) m3_angles_kernel(AngK p) {
 
 hipError_t m3_angles_to_cos_sin(const float* angles, const float* dt, size_t batch,
                                 size_t len, size_t heads, size_t r, size_t half, float* cos,
-                                float* sin, hipStream_t st) {
+                                float* sin, hipStream_t st, const long long* ang_strides) {
   AngK k{};
   k.ang = angles; k.dt = dt; k.cos = cos; k.sin = sin;
   k.L = (int)len; k.H = (int)heads; k.r = (int)r; k.half = (int)half;
   k.nlines = (long long)(batch * heads) * (long long)((half + 31) / 32);
   const bool a16 = ((uintptr_t)angles & 15u) == 0 && ((uintptr_t)cos & 15u) == 0 &&
                    ((uintptr_t)sin & 15u) == 0;
-  k.vec = a16 && r % 4 == 0 && half % 4 == 0;
+  if (ang_strides) {
+    k.ab = ang_strides[0]; k.at = ang_strides[1]; k.ah = ang_strides[2];
+  } else {
+    k.ah = (long long)r;
+    k.at = (long long)(heads * r);
+    k.ab = (long long)(len * heads * r);
+  }
+  k.vec = a16 && r % 4 == 0 && half % 4 == 0 && k.ab % 4 == 0 && k.at % 4 == 0 &&
+          k.ah % 4 == 0;
   if (len == 0 || k.nlines == 0) return hipSuccess;
   // segments: enough blocks to fill the chip a few times over
   const long long tiles = ((long long)len + kTile - 1) / kTile;

@@ -87,6 +87,8 @@ struct M3K {
   const float* ang;
   int nang, n_ang;
   int rec_floats;  // kRecFloats, or kRecFloatsAng with pi * dt per row
+  long long vb, zb, ab, ah;  // element strides: v, z per batch; angles per batch, head
+  int vt, zt, at;            // and per step
   // SISO: no same-step term (gamma on M's diagonal, D x) and out += the result
   int accum;
 };
@@ -186,7 +188,7 @@ __device__ __forceinline__ f2 ld2(const float* p) { return *reinterpret_cast<con
 // Base pointers of a block's sequence.
 struct SeqIn {
   const float *q, *k, *cos, *sin, *ang, *v, *z, *rec;
-  int qstride, csstride, angstride, vstride;  // floats per step
+  int qstride, csstride, angstride, vstride, zstride;  // floats per step
 };
 
 // DMA instruction `ins` of a stage (1 KB, one 16-byte piece per lane). Stage
@@ -243,7 +245,7 @@ __device__ __forceinline__ DmaPiece dma_decode(const M3K& p, const SeqIn& s, int
     d.src = zz ? s.z : s.v;
     d.step = j / w4;
     d.col = 4 * (j % w4);
-    d.stride = s.vstride;
+    d.stride = zz ? s.zstride : s.vstride;
   } else {
     const int j = (rel - p.n_v - p.n_z) * 64 + lane;
     d.on = j < p.rec_floats / 4;
@@ -547,14 +549,15 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 2)) m3_chunk_kernel(M3K p) {
   in.k = p.k + ((long long)bi * L * R * p.groups + grp) * dqk;
   in.cos = p.cos + ((long long)bi * L * H + h) * half;
   in.sin = p.sin + ((long long)bi * L * H + h) * half;
-  in.v = p.v + ((long long)bi * L * H + h) * dv + p0;
-  in.z = p.z ? p.z + ((long long)bi * L * H + h) * dv + p0 : nullptr;
-  in.ang = ANG ? p.ang + ((long long)bi * L * H + h) * p.nang : nullptr;
+  in.v = p.v + (long long)bi * p.vb + (long long)h * dv + p0;
+  in.z = p.z ? p.z + (long long)bi * p.zb + (long long)h * dv + p0 : nullptr;
+  in.ang = ANG ? p.ang + (long long)bi * p.ab + (long long)h * p.ah : nullptr;
   in.rec = p.rec + (long long)seq * p.nchunks * p.rec_floats;
   in.qstride = R * p.groups * dqk;
   in.csstride = H * half;
-  in.angstride = H * p.nang;
-  in.vstride = H * dv;
+  in.angstride = p.at;
+  in.vstride = p.vt;
+  in.zstride = p.zt;
 
   // biases of the lane's columns (row li has rank li % R)
   f4 bq, bk, bqp = {0.0f, 0.0f, 0.0f, 0.0f}, bkp = bqp;
@@ -753,8 +756,12 @@ bool m3_chunk_supported(const M3Problem& pr) {
   const bool rank_ok = mimo ? (pr.rank == 1 || pr.rank == 2 || pr.rank == 4) : pr.rank == 1;
   // 32-bit offsets within a sequence: q/k, cos/sin and v/z/out spans below 2^30 floats
   const size_t lim = (size_t)1 << 30;
+  const long long llim = (long long)lim;
+  auto step_ok = [&](long long s) { return s >= 0 && s < llim && s * (long long)pr.len < llim; };
   const bool spans = pr.len * pr.rank * pr.groups * pr.dqk < lim &&
-                     pr.len * pr.heads * pr.dv < lim && pr.len * pr.heads * pr.dqk < lim;
+                     pr.len * pr.heads * pr.dv < lim && pr.len * pr.heads * pr.dqk < lim &&
+                     step_ok(pr.v_strides[1]) && step_ok(pr.z_strides[1]) &&
+                     step_ok(pr.ang_strides[1]);
   return rank_ok && pr.dv % 16 == 0 && pr.dqk % 16 == 0 && pr.dqk >= 16 &&
          pr.dqk <= 16 * (size_t)kMaxWaves && pr.len > 0 && spans;
 }
@@ -779,6 +786,9 @@ hipError_t m3_scan_chunked(const M3Problem& pr, hipStream_t st) {
   k.ptiles = (k.nparts % 2 == 0 && WN >= 2) ? 2 : 1;
   k.ang = pr.angles;
   k.nang = (int)pr.n_angles;
+  k.vb = pr.v_strides[0]; k.vt = (int)pr.v_strides[1];
+  k.zb = pr.z_strides[0]; k.zt = (int)pr.z_strides[1];
+  k.ab = pr.ang_strides[0]; k.at = (int)pr.ang_strides[1]; k.ah = pr.ang_strides[2];
   k.rec_floats = pr.angles ? kRecFloatsAng : kRecFloats;
   auto plan = [&]() {
     const int T = k.steps_per_chunk;

@@ -36,6 +36,7 @@ struct M3Args {
   const float *q, *k, *v, *adt, *dt, *trap, *qb, *kb, *cos, *sin, *D, *z, *psi, *zeta, *phi;
   float *out, *last_state, *last_bx;
   int heads, dv, dqk, len, rank, groups, reverse, mimo, out_tm, accumulate;
+  long long vb, vt, zb, zt;  // element strides of v and z: batch, step
 };
 
 __global__ void __launch_bounds__(kM3Threads) m3_seq_kernel(M3Args p) {
@@ -86,7 +87,8 @@ __global__ void __launch_bounds__(kM3Threads) m3_seq_kernel(M3Args p) {
       qr[e] = first ? (qa * c - qc * s) : (qa * s + qc * c);
       kr[e] = first ? (ka * c - kc * s) : (ka * s + kc * c);
     }
-    const long long v_off = (((long long)bi * L + t) * p.heads + h) * dv;
+    const long long v_off = (long long)bi * p.vb + (long long)t * p.vt + (long long)h * dv;
+    const long long z_off = (long long)bi * p.zb + (long long)t * p.zt + (long long)h * dv;
     for (int e = tid; e < R * dv; e += kM3Threads) {
       const int rr = e / dv, pp = e - rr * dv;
       const float vv = p.v[v_off + pp];
@@ -135,11 +137,11 @@ __global__ void __launch_bounds__(kM3Threads) m3_seq_kernel(M3Args p) {
       if (!p.mimo) {
         const float diag = p.accumulate ? 0.0f : dskip + gamma * gram[0];
         o = fmaf(alpha, acc[pp], diag * xs[pp]);
-        if (p.z) o *= silu(p.z[v_off + pp]);
+        if (p.z) o *= silu(p.z[z_off + pp]);
         if (p.accumulate) o += dst[pp];  // the other traversal's output
       } else {
         o = 0.0f;
-        const float zz = p.z ? p.z[v_off + pp] : 0.0f;
+        const float zz = p.z ? p.z[z_off + pp] : 0.0f;
         for (int rr = 0; rr < R; ++rr) {
           float dsum = 0.0f;
           for (int b = 0; b < R; ++b) dsum = fmaf(gram[rr * R + b], xs[b * dv + pp], dsum);
@@ -178,7 +180,13 @@ static bool aligned16(const void* q) { return q == nullptr || ((uintptr_t)q & 15
 
 namespace {
 bool m3_aligned(const M3Problem& pr) {
-  return aligned16(pr.q) && aligned16(pr.k) && aligned16(pr.q_bias) &&
+  // 16-byte pieces at every (batch, step, head) row start, strides included
+  const bool strides4 = pr.v_strides[0] % 4 == 0 && pr.v_strides[1] % 4 == 0 &&
+                        pr.z_strides[0] % 4 == 0 && pr.z_strides[1] % 4 == 0 &&
+                        (pr.angles == nullptr ||
+                         (pr.ang_strides[0] % 4 == 0 && pr.ang_strides[1] % 4 == 0 &&
+                          pr.ang_strides[2] % 4 == 0));
+  return strides4 && aligned16(pr.q) && aligned16(pr.k) && aligned16(pr.q_bias) &&
          aligned16(pr.k_bias) && aligned16(pr.cos) && aligned16(pr.sin) &&
          aligned16(pr.angles) && aligned16(pr.v) && aligned16(pr.z) &&
          aligned16(pr.last_state) && aligned16(pr.last_bx);
@@ -224,6 +232,8 @@ hipError_t m3_scan_sequential(const M3Problem& pr, hipStream_t st) {
   a.mimo = pr.psi != nullptr;
   a.out_tm = pr.out_time_major;
   a.accumulate = pr.accumulate;
+  a.vb = pr.v_strides[0]; a.vt = pr.v_strides[1];
+  a.zb = pr.z_strides[0]; a.zt = pr.z_strides[1];
   const unsigned blocks = (unsigned)(pr.batch * pr.heads);
   hipLaunchKernelGGL(m3_seq_kernel, dim3(blocks), dim3(kM3Threads), fl * sizeof(float), st, a);
   return hipGetLastError();

@@ -85,17 +85,54 @@ struct M3Problem {
   // other direction has written out, that gives the non-causal sum
   // forward + backward - diagonal (python/arm_scan/mamba3_noncausal.py:89-98).
   int accumulate;
+  // Element strides of v and z (batch, step) and of the raw angles (batch, step,
+  // head). Within a step the heads of v and z lie dv apart; the angles' head stride
+  // may be 0 (one set shared by every head). All zero = the contiguous layouts;
+  // m3_fill_strides writes those in.
+  long long v_strides[2], z_strides[2], ang_strides[3];
 };
+
+inline void m3_fill_strides(M3Problem& p) {
+  const long long L = (long long)p.len, H = (long long)p.heads;
+  if (p.v_strides[0] == 0 && p.v_strides[1] == 0) {
+    p.v_strides[0] = L * H * (long long)p.dv;
+    p.v_strides[1] = H * (long long)p.dv;
+  }
+  if (p.z_strides[0] == 0 && p.z_strides[1] == 0) {
+    p.z_strides[0] = L * H * (long long)p.dv;
+    p.z_strides[1] = H * (long long)p.dv;
+  }
+  if (p.ang_strides[0] == 0 && p.ang_strides[1] == 0 && p.ang_strides[2] == 0) {
+    p.ang_strides[0] = L * H * (long long)p.n_angles;
+    p.ang_strides[1] = H * (long long)p.n_angles;
+    p.ang_strides[2] = (long long)p.n_angles;
+  }
+}
 
 // Largest dv * dqk the Mamba-3 kernel holds on chip.
 size_t m3_max_state();
 hipError_t m3_scan(const M3Problem& p, hipStream_t st);
 // The RoPE angle pre-pass: angles (batch, len, heads, r), dt (batch, heads, len) ->
 // cos, sin (batch, len, heads, half), theta = cumsum_len(tanh(angle) pi dt), pairs past
-// r the identity (m3_angles.hip).
+// r the identity (m3_angles.hip). ang_strides (batch, step, head) in elements, or null
+// for the contiguous layout.
 hipError_t m3_angles_to_cos_sin(const float* angles, const float* dt, size_t batch,
                                 size_t len, size_t heads, size_t r, size_t half, float* cos,
-                                float* sin, hipStream_t st);
+                                float* sin, hipStream_t st,
+                                const long long* ang_strides = nullptr);
+// The Mamba-3 mixer's front-end (m3_block.hip, apps/mamba3_lm/block.py:146-178): from
+// the in_proj output, the head-major gates and the RMS-normalised q (C) and k (B).
+struct M3Frontend {
+  const float* proj;     // (batch, len, row_stride): [z | x | B | C | dd_dt | dd_A | trap | ...]
+  long long row_stride;  // floats between tokens
+  int batch, len, heads, headdim, d_state, rank, groups;
+  const float *dt_bias, *b_norm, *c_norm;  // (heads), (d_state), (d_state)
+  float a_floor, eps;
+  float *q, *k;               // (batch, len, rank, groups, d_state)
+  float *adt, *dt, *trap;     // (batch, heads, len)
+};
+hipError_t m3_frontend(const M3Frontend& p, hipStream_t st);
+
 // Whether m3_scan serves raw angles for this problem (the chunked kernel, forward,
 // n_angles a multiple of 4 up to dqk/2, 16-byte aligned inputs); else *why says why.
 bool m3_angles_supported(const M3Problem& p, const char** why);

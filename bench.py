@@ -53,7 +53,7 @@ def parse():
     ap.add_argument("--workload", choices=("m1", "m1_b1", "m1_seam", "m3_siso", "m3_mimo",
                                            "ss2d",
                                            "m3_siso_angles", "m3_mimo_angles",
-                                           "m3_noncausal"),
+                                           "m3_noncausal", "m3_block"),
                     default="m1",
                     help="m1 (default): the headline line below; the others time one of the "
                          "configs 3-5, or the config-2 scan in the HF mixer's layouts "
@@ -145,6 +145,22 @@ def config_inputs(name, dev):
             workloads.m3_mimo(seed=4)
         x = workloads.m3_with_angles(base, seed=6)
         return {k: torch.from_numpy(v).to(dev) for k, v in x.items()}, workloads.m3_bytes(x)
+    if name == "m3_block":
+        from armhackathon_amd.mamba3_block import Mamba3Mixer
+
+        torch.manual_seed(7)
+        m = Mamba3Mixer().to(dev)  # the published SISO mixer's dimensions
+        with torch.no_grad():
+            for pname, prm in m.named_parameters():
+                if pname.endswith("proj.weight"):
+                    prm.normal_(0.0, prm.shape[1] ** -0.5)
+                elif pname == "dt_bias":
+                    prm.uniform_(-4.0, -2.0)
+        u = torch.randn((4, 4096, m.d_model), device=dev)
+        # what the mixer's scan core reads and writes once: the projection, the
+        # parameters, the output (b, l, h, p)
+        nbytes = 4 * (u.shape[0] * u.shape[1] * (sum(m.split_sizes) + m.d_inner))
+        return {"mixer": m, "u": u}, nbytes
     if name == "m3_noncausal":
         x = workloads.m3_siso(seed=3)
         nbytes = workloads.m3_bytes(x, want_state=False)
@@ -169,6 +185,9 @@ CONFIG_NAMES = {
     "m3_siso": "config 3: Mamba-3 SISO B4 L4096 24 heads x 64, dqk 128 (final states too)",
     "m3_siso_angles": "config 3 from raw angles (b, l, h, 32): the angle pre-pass fused",
     "m3_mimo_angles": "config 4 from raw angles (b, l, h, 32): the angle pre-pass fused",
+    "m3_block": "Mamba-3 SISO mixer forward at the published dimensions (d_model 768, "
+                "d_state 128, 24 heads x 64, 32 angles), B4 L4096: in_proj, front-end, "
+                "scan, out_proj (random-init weights)",
     "m3_noncausal": "config 3 shapes aggregated non-causally (every position over every "
                     "other): forward traversal, then the backward one accumulated without "
                     "the same-step term",
@@ -215,6 +234,12 @@ def bench_config(name, dev, steps, warmup):
             return arm_scan.mamba3_mimo_scan(*[t[k] for k in K], t["psi"], t["zeta"],
                                              t["phi"], angles=t["angles"],
                                              return_last_state=True)
+    elif name == "m3_block":
+        mixer, u = t["mixer"], t["u"]
+
+        def call():
+            with torch.no_grad():
+                return mixer(u)
     elif name == "m3_noncausal":
         def call():
             return arm_scan.noncausal_scan(*[t[k] for k in K], cos=t["cos"], sin=t["sin"])
@@ -265,6 +290,48 @@ def bench_config(name, dev, steps, warmup):
         stop.record(stream)
         torch.cuda.synchronize()
         extra["unfused_ms_per_call"] = round(start.elapsed_time(stop) / steps, 4)
+    if name == "m3_block":
+        # the reference's block on the same scan kernel: the front-end in torch ops and
+        # the contiguous copies of x, z and the head-broadcast angles the scan's Python
+        # layer makes (apps/mamba3_lm/block.py:146-199, python/arm_scan/mamba3.py)
+        import torch.nn.functional as F
+
+        m = mixer
+
+        def torch_route():
+            with torch.no_grad():
+                b, L, _ = u.shape
+                h, p, n = m.nheads, m.headdim, m.d_state
+                zz, xx, B, C, ddt, dda, tr, ang = torch.split(m.in_proj(u), m.split_sizes,
+                                                              dim=-1)
+                zz, xx = zz.reshape(b, L, h, p), xx.reshape(b, L, h, p)
+                B = m.B_norm(B.reshape(b, L, 1, 1, n))
+                C = m.C_norm(C.reshape(b, L, 1, 1, n))
+                A = torch.clamp(-(dda.clamp_min(0) + torch.reciprocal(1 - dda.clamp_max(0))),
+                                max=-m.A_floor)
+                DT = F.softplus(ddt + m.dt_bias)
+                ADT = (A * DT).permute(0, 2, 1)
+                DT = DT.permute(0, 2, 1)
+                ang = ang.unsqueeze(-2).expand(-1, -1, h, -1)
+                y = arm_scan.mamba3_scan(C[:, :, 0], B[:, :, 0], xx, ADT, DT,
+                                         tr.permute(0, 2, 1), m.C_bias[:, 0], m.B_bias[:, 0],
+                                         angles=ang, D=m.D, z=zz)
+                return m.out_proj(y.reshape(b, L, h * p))
+
+        def gemms():
+            with torch.no_grad():
+                proj = m.in_proj(u)
+                return m.out_proj(proj[..., :m.d_inner])
+        for key, fn in (("torch_front_end_ms_per_call", torch_route),
+                        ("gemms_only_ms_per_call", gemms)):
+            for _ in range(warmup):
+                fn()
+            start.record(stream)
+            for _ in range(steps):
+                fn()
+            stop.record(stream)
+            torch.cuda.synchronize()
+            extra[key] = round(start.elapsed_time(stop) / steps, 4)
     if name == "m3_noncausal":
         # the reference's composition on the same kernels: both traversals into two
         # outputs, then forward + backward - the same-step term in torch ops

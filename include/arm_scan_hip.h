@@ -18,8 +18,10 @@
  *     variants for callers' layouts and the fused Mamba-3 angle pre-pass
  *     (arm_scan_selective_scan_strided_f32, arm_scan_mamba3_scan_time_major_f32,
  *     arm_scan_mamba3_scan_angles_f32, arm_scan_mamba3_angles_f32), the decode
- *     step arm_scan_selective_state_update_f32 and the non-causal Mamba-3 sum
- *     arm_scan_mamba3_noncausal_f32, each described at its declaration;
+ *     step arm_scan_selective_state_update_f32, the non-causal Mamba-3 sum
+ *     arm_scan_mamba3_noncausal_f32, and the Mamba-3 mixer's front-end and strided
+ *     scan (arm_scan_mamba3_block_frontend_f32, arm_scan_mamba3_scan_strided_f32),
+ *     each described at its declaration;
  *   - code 6 reports a HIP launch / device error; arm_scan_last_error() explains
  *     the most recent nonzero code on the calling thread.
  *
@@ -175,6 +177,43 @@ int arm_scan_mamba3_scan_angles_f32(
  * half) with theta = cumsum_len(tanh(angle) * pi * dt); pairs n_angles .. half-1 get
  * cos 1, sin 0. Feeds arm_scan_mamba3_scan[_time_major]_f32 where the fused entry
  * point does not apply (reverse, MIMO, n_angles not a multiple of 4). */
+/* No reference counterpart: the forward Mamba-3 scan from raw angles with v, z and the
+ * angles given by element strides, as the Mamba-3 mixer holds them: views into its
+ * in_proj output, the angles shared by every head (apps/mamba3_lm/block.py:150-174
+ * splits the projection, `expand`s the angles over heads, and the reference's
+ * python/arm_scan/mamba3.py then copies each one contiguous).
+ *   v_strides, z_strides: (batch, step) in elements; within a step the heads lie dv
+ *     apart. angle_strides: (batch, step, head); the head stride may be 0.
+ * Other arguments as arm_scan_mamba3_scan_angles_f32; out is time-major (b, l, h, dv)
+ * and contiguous. Where the fused SISO kernel does not apply (MIMO, n_angles not a
+ * multiple of 4, strides that are not multiples of 4), the angle pre-pass runs into
+ * stream-ordered scratch and the scan reads cos/sin from it. The strides must keep
+ * every access inside the caller's buffers; negative strides return
+ * ARM_SCAN_ERR_INVALID_DIMS. */
+int arm_scan_mamba3_scan_strided_f32(
+    const ArmMamba3Dims* dims, const float* q, const float* k, const float* v,
+    const int64_t* v_strides, const float* adt, const float* dt, const float* trap,
+    const float* q_bias, const float* k_bias, const float* angles, size_t n_angles,
+    const int64_t* angle_strides, const float* d_skip, const float* z, const int64_t* z_strides,
+    const float* mimo_psi, const float* mimo_zeta, const float* mimo_phi, int backend,
+    int threading, float* out, void* stream);
+
+/* No reference counterpart: the Mamba-3 mixer's front-end, which the reference runs as
+ * torch ops (apps/mamba3_lm/block.py:146-178), in one kernel. proj (batch, len,
+ * row_stride) is the in_proj output with the checkpoint's column order
+ * [z (h*headdim) | x (h*headdim) | B (r*g*d_state) | C (r*g*d_state) | dd_dt (h) |
+ * dd_A (h) | trap (h) | angles (n_angles)] (block.py:113-118). Writes
+ *   dt = softplus(dd_dt + dt_bias), adt = min(-heavy_tail(dd_A), -a_floor) * dt and
+ *   trap, each (batch, heads, len);
+ *   k = RMSNorm(B) * b_norm_weight and q = RMSNorm(C) * c_norm_weight, each (batch,
+ *   len, rank, groups, d_state), eps inside the square root (Q <- C, K <- B).
+ * z, x and the angles are left where they are, for arm_scan_mamba3_scan_strided_f32. */
+int arm_scan_mamba3_block_frontend_f32(
+    const float* proj, size_t batch, size_t len, size_t row_stride, size_t heads,
+    size_t headdim, size_t d_state, size_t rank, size_t groups, size_t n_angles,
+    const float* dt_bias, float a_floor, const float* b_norm_weight, const float* c_norm_weight,
+    float norm_eps, float* q, float* k, float* adt, float* dt, float* trap, void* stream);
+
 /* No reference counterpart: the non-causal Mamba-3 SISO aggregation, which the
  * reference composes in Python over its two traversals (python/arm_scan/
  * mamba3_noncausal.py:89-98: forward + backward - the same-step term counted twice).

@@ -13,6 +13,9 @@ operand, the wrong trapezoid neighbour under reverse) shows up as a mismatch:
 * `m3_siso_dense`: the O(L^2) dual (attention-like) form of the same SISO
   recurrence — no state matrix at all.
 * `m3_mimo_scan`: the rank-r sequential form, einsum-free.
+* `m3_mixer`: the Mamba-3 mixer (apps/mamba3_lm/block.py:146-199) around the
+  sequential scans: in_proj, the split, `heavy_tail`, softplus, `rms_norm`, Q <- C /
+  K <- B, the head-shared angles, out_proj.
 * `m3_noncausal_dense`: the non-causal (and, with causal=True, the causal) O(L^2)
   mask form with every weight a running product of decays (no cumsum), and
   `m3_same_step`, the same-step term from UNROTATED q/k, so that
@@ -292,3 +295,51 @@ def m3_mimo_scan(q, k, v, adt, dt, trap, q_bias, k_bias, psi, zeta, phi, cos, si
     if reverse:
         out = out[:, ::-1]
     return np.ascontiguousarray(out), S
+
+
+def heavy_tail(x):
+    """1 + x for x >= 0, 1 / (1 - x) below (apps/mamba3_lm/block.py:52-62)."""
+    x = np.asarray(x, np.float64)
+    return np.where(x >= 0, 1.0 + x, 1.0 / (1.0 - np.minimum(x, 0.0)))
+
+
+def rms_norm(x, w, eps):
+    """x / sqrt(mean(x^2) + eps) * w over the last axis (block.py:65-82)."""
+    x = np.asarray(x, np.float64)
+    return x / np.sqrt((x * x).mean(-1, keepdims=True) + eps) * np.asarray(w, np.float64)
+
+
+def m3_mixer(u, p, heads, headdim, d_state, rank, groups, n_angles, a_floor, eps=1e-5):
+    """The Mamba-3 mixer forward (apps/mamba3_lm/block.py:146-199) in float64.
+
+    u (b, l, d_model); p: in_proj (d_in_proj, d_model), out_proj (d_model, d_inner),
+    dt_bias, D (h), B_bias, C_bias (h, r, n), B_norm, C_norm (n) and, for MIMO,
+    mimo_x / mimo_z / mimo_o (h, r, headdim). Projection columns in the checkpoint's
+    order [z, x, B, C, dd_dt, dd_A, trap, angles] (block.py:113-118).
+    """
+    import oracle
+
+    u = np.asarray(u, np.float64)
+    b, L, _ = u.shape
+    d_inner, bc = heads * headdim, rank * groups * d_state
+    proj = u @ np.asarray(p["in_proj"], np.float64).T
+    sizes = [d_inner, d_inner, bc, bc, heads, heads, heads, n_angles]
+    z, x, B, C, dd_dt, dd_A, trap, ang = np.split(proj, np.cumsum(sizes)[:-1], axis=-1)
+    z = z.reshape(b, L, heads, headdim)
+    x = x.reshape(b, L, heads, headdim)
+    B = rms_norm(B.reshape(b, L, rank, groups, d_state), p["B_norm"], eps)
+    C = rms_norm(C.reshape(b, L, rank, groups, d_state), p["C_norm"], eps)
+    A = np.minimum(-heavy_tail(dd_A), -a_floor)
+    DT = softplus(dd_dt + np.asarray(p["dt_bias"], np.float64))
+    ADT = (A * DT).transpose(0, 2, 1)
+    DT = DT.transpose(0, 2, 1)
+    trap = trap.transpose(0, 2, 1)
+    ang = np.broadcast_to(ang[:, :, None, :], (b, L, heads, n_angles))
+    cos, sin = oracle.angles_to_cos_sin(ang, DT, d_state // 2)
+    if "mimo_x" not in p:
+        y, _ = m3_siso_scan(C[:, :, 0], B[:, :, 0], x, ADT, DT, trap, p["C_bias"][:, 0],
+                            p["B_bias"][:, 0], cos, sin, D=p["D"], z=z)
+    else:
+        y, _ = m3_mimo_scan(C, B, x, ADT, DT, trap, p["C_bias"], p["B_bias"], p["mimo_x"],
+                            p["mimo_z"], p["mimo_o"], cos, sin, D=p["D"], z=z)
+    return y.reshape(b, L, d_inner) @ np.asarray(p["out_proj"], np.float64).T

@@ -1,0 +1,65 @@
+"""The Mamba-3 mixer's host side on the CPU: the checkpoint's parameter names and
+shapes (apps/mamba3_lm/block.py:24-31 lists them for the published SISO model), and
+the oracle's front-end pieces against closed forms."""
+
+import numpy as np
+import pytest
+
+from oracle import naive
+
+
+def test_mixer_parameters_match_the_checkpoint():
+    torch = pytest.importorskip("torch")
+    from armhackathon_amd.mamba3_block import Mamba3Mixer
+
+    m = Mamba3Mixer()
+    shapes = {k: tuple(v.shape) for k, v in m.state_dict().items()}
+    assert shapes == {
+        "in_proj.weight": (3432, 768), "out_proj.weight": (768, 1536), "dt_bias": (24,),
+        "D": (24,), "B_bias": (24, 1, 128), "C_bias": (24, 1, 128),
+        "B_norm.weight": (128,), "C_norm.weight": (128,)}
+    assert m.split_sizes == [1536, 1536, 128, 128, 24, 24, 24, 32]
+    mm = Mamba3Mixer(d_model=64, d_state=32, headdim=16, is_mimo=True, mimo_rank=4)
+    s = {k: tuple(v.shape) for k, v in mm.state_dict().items()}
+    assert s["mimo_x"] == s["mimo_z"] == s["mimo_o"] == (8, 4, 16)
+    assert s["B_bias"] == (8, 4, 32) and mm.split_sizes[2] == 4 * 32
+    assert Mamba3Mixer(d_state=128, rope_fraction=1.0).num_rope_angles == 64
+    with pytest.raises(ValueError):
+        Mamba3Mixer(rope_fraction=0.25)
+    del torch
+
+
+def test_heavy_tail_closed_forms():
+    """f(x) = 1 + x (x >= 0), 1 / (1 - x) (x < 0): values, continuity and slope 1 at 0,
+    positive everywhere (so -f is a decay)."""
+    x = np.array([0.0, 2.0, -1.0, -3.0, 1e-9, -1e-9])
+    np.testing.assert_allclose(naive.heavy_tail(x), [1.0, 3.0, 0.5, 0.25, 1.0, 1.0],
+                               rtol=1e-12, atol=1e-8)
+    h = 1e-6
+    slope = (naive.heavy_tail(h) - naive.heavy_tail(-h)) / (2 * h)
+    assert abs(slope - 1.0) < 1e-6
+    grid = np.linspace(-50, 50, 1001)
+    assert (naive.heavy_tail(grid) > 0).all()
+    assert (np.diff(naive.heavy_tail(grid)) > 0).all()
+
+
+def test_rms_norm_invariants():
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((5, 7, 32))
+    y = naive.rms_norm(x, np.ones(32), 0.0)
+    np.testing.assert_allclose(np.sqrt((y * y).mean(-1)), 1.0, rtol=1e-12)
+    np.testing.assert_allclose(naive.rms_norm(3.5 * x, np.ones(32), 0.0), y, rtol=1e-12)
+    w = rng.standard_normal(32)
+    np.testing.assert_allclose(naive.rms_norm(x, w, 0.0), y * w, rtol=1e-12)
+    # eps inside the square root: a zero row stays finite (and zero)
+    assert np.all(naive.rms_norm(np.zeros((1, 32)), w, 1e-5) == 0.0)
+
+
+def test_frontend_rejects_short_rows():
+    """The host check runs before any launch (fake, never dereferenced pointers)."""
+    from armhackathon_amd import _ffi
+
+    with pytest.raises(_ffi.ArmScanError) as e:
+        _ffi.block_frontend_raw(16, 1, 4, 10, 2, 4, 4, 1, 1, 2, 16, 1e-4, 16, 16, 1e-5, 16, 16,
+                                16, 16, 16)
+    assert e.value.code == 2 and "row_stride" in str(e.value)
