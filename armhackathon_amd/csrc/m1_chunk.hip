@@ -452,7 +452,7 @@ __device__ __forceinline__ void issue_tile(float* tile, const float* Bg, const f
     if (G::DMA % kWavesPerBlock == 0 || m < G::DMA) {
       const int k = m * (256 / G::CH) + lane / SPR;  // tile row of this lane
       const int n = n0 + (k % kTileStates);
-      if (n < N) {
+      if (n < N && (k < kTileStates || Cg != nullptr)) {  // Cg null: B rows only
         const float* src = (k < kTileStates ? Bg : Cg) + (long long)n * L + mem0 + 4 * piece;
         __builtin_amdgcn_global_load_lds(
             (const void*)src, (__attribute__((address_space(3))) void*)(tile + m * 256), 16, 0,
@@ -784,7 +784,6 @@ __device__ __forceinline__ void fold_rows(const M1Kern& p, long long blk, int se
   const float* urow = p.u + row * L;
   const float* drow = p.delta + row * L;
   const float* Bg = p.B + ((long long)bi * p.groups + g) * N * L;
-  const float* Cg = p.C + ((long long)bi * p.groups + g) * N * L;
   const float bias = p.bias ? p.bias[d] : 0.0f;
   float* sA = small + (wave * RPW + rw) * N;
   float* sB = small + (kWavesPerBlock * RPW + wave * RPW + rw) * N;
@@ -801,7 +800,8 @@ __device__ __forceinline__ void fold_rows(const M1Kern& p, long long blk, int se
   const int ng = (N + kTileStates - 1) / kTileStates;
   const long long ntiles = (ce - cb) * ng;
   auto mem0 = [&](long long c) { return REV ? L - (c + 1) * CH : c * CH; };
-  if (ntiles > 0) issue_tile<I>(tiles, Bg, Cg, L, mem0(cb), 0, N, wave, lane);
+  // the fold reads B only: the tiles' C rows are not fetched
+  if (ntiles > 0) issue_tile<I>(tiles, Bg, nullptr, L, mem0(cb), 0, N, wave, lane);
   long long k = 0;
   for (long long c = cb; c < ce; ++c) {
     const long long sb = c * CH + (long long)j * I;
@@ -828,7 +828,7 @@ __device__ __forceinline__ void fold_rows(const M1Kern& p, long long blk, int se
       if (k + 1 < ntiles) {
         const long long cn = cb + (k + 1) / ng;
         const int qn = (int)((k + 1) % ng);
-        issue_tile<I>(tiles + ((k + 1) & 1) * G::FLOATS, Bg, Cg, L, mem0(cn),
+        issue_tile<I>(tiles + ((k + 1) & 1) * G::FLOATS, Bg, nullptr, L, mem0(cn),
                       qn * kTileStates, N, wave, lane);
       }
       const float* tile = tiles + (k & 1) * G::FLOATS;

@@ -15,8 +15,9 @@
 // projection by their strides (the angles with head stride 0, one set shared by every
 // head as block.py:174 broadcasts them).
 //
-// A block takes kTok consecutive tokens of one batch row. The gates go through LDS so
-// that their head-major stores run along the sequence (kTok floats per head). The
+// A block takes kTok consecutive tokens of one batch row. The gates go through LDS, 32
+// heads at a time, so that their head-major stores run along the sequence (kTok floats
+// per head). The
 // normalised rows of B and C (d_state floats each) take one wave each.
 
 #include <hip/hip_runtime.h>
@@ -29,10 +30,11 @@ namespace armscan {
 namespace {
 
 constexpr int kTok = 32;
+constexpr int kHeadGroup = 32;  // heads per pass through LDS
 constexpr int kFrontThreads = 256;
 
 __global__ void __launch_bounds__(kFrontThreads) m3_frontend_kernel(M3Frontend p) {
-  extern __shared__ float gl[];  // [3][heads][kTok]: dt, adt, trap
+  __shared__ float gl[3 * kHeadGroup * kTok];  // [3][head in group][token]: dt, adt, trap
   const int H = p.heads, L = p.len, n = p.d_state, rows = p.rank * p.groups;
   const long long b = blockIdx.y;
   const int t0 = blockIdx.x * kTok;
@@ -40,23 +42,28 @@ __global__ void __launch_bounds__(kFrontThreads) m3_frontend_kernel(M3Frontend p
   const float* base = p.proj + (b * L + t0) * p.row_stride;
   const int col_b = 2 * H * p.headdim, col_c = col_b + rows * n, col_g = col_c + rows * n;
 
-  for (int e = threadIdx.x; e < ntok * H; e += kFrontThreads) {
-    const int j = e / H, h = e - j * H;
-    const float* g = base + (long long)j * p.row_stride + col_g;
-    const float dt = softplus(g[h] + p.dt_bias[h]);
-    const float x = g[H + h];
-    const float heavy = fmaxf(x, 0.0f) + 1.0f / (1.0f - fminf(x, 0.0f));
-    gl[h * kTok + j] = dt;
-    gl[(H + h) * kTok + j] = fminf(-heavy, -p.a_floor) * dt;
-    gl[(2 * H + h) * kTok + j] = g[2 * H + h];
-  }
-  __syncthreads();
-  for (int e = threadIdx.x; e < H * ntok; e += kFrontThreads) {
-    const int h = e / ntok, j = e - h * ntok;
-    const long long o = (b * H + h) * L + t0 + j;
-    p.dt[o] = gl[h * kTok + j];
-    p.adt[o] = gl[(H + h) * kTok + j];
-    p.trap[o] = gl[(2 * H + h) * kTok + j];
+  constexpr int G = kHeadGroup;
+  for (int h0 = 0; h0 < H; h0 += G) {  // block-uniform
+    const int nh = H - h0 < G ? H - h0 : G;
+    for (int e = threadIdx.x; e < ntok * nh; e += kFrontThreads) {
+      const int j = e / nh, hh = e - j * nh, h = h0 + hh;
+      const float* g = base + (long long)j * p.row_stride + col_g;
+      const float dt = softplus(g[h] + p.dt_bias[h]);
+      const float x = g[H + h];
+      const float heavy = fmaxf(x, 0.0f) + 1.0f / (1.0f - fminf(x, 0.0f));
+      gl[hh * kTok + j] = dt;
+      gl[(G + hh) * kTok + j] = fminf(-heavy, -p.a_floor) * dt;
+      gl[(2 * G + hh) * kTok + j] = g[2 * H + h];
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < nh * ntok; e += kFrontThreads) {
+      const int hh = e / ntok, j = e - hh * ntok;
+      const long long o = (b * H + h0 + hh) * L + t0 + j;
+      p.dt[o] = gl[hh * kTok + j];
+      p.adt[o] = gl[(G + hh) * kTok + j];
+      p.trap[o] = gl[(2 * G + hh) * kTok + j];
+    }
+    __syncthreads();  // gl is rewritten by the next group
   }
 
   // RMSNorm rows: (token j, B or C, row rr), one wave each
@@ -82,9 +89,7 @@ __global__ void __launch_bounds__(kFrontThreads) m3_frontend_kernel(M3Frontend p
 hipError_t m3_frontend(const M3Frontend& p, hipStream_t st) {
   if (p.len <= 0 || p.batch <= 0 || p.heads <= 0) return hipErrorInvalidValue;
   const dim3 grid((unsigned)((p.len + kTok - 1) / kTok), (unsigned)p.batch);
-  const size_t lds = (size_t)3 * p.heads * kTok * sizeof(float);
-  if (lds > 64 * 1024) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(m3_frontend_kernel, grid, dim3(kFrontThreads), lds, st, p);
+  hipLaunchKernelGGL(m3_frontend_kernel, grid, dim3(kFrontThreads), 0, st, p);
   return hipGetLastError();
 }
 

@@ -84,15 +84,16 @@ def test_mixer_forward(spec):
     assert rel_err(got, ref) <= TOL, name
 
 
-@pytest.mark.parametrize("rows", [(1, 1), (2, 2)], ids=["siso", "r2g2"])
+@pytest.mark.parametrize("rows", [(1, 1, 4), (2, 2, 4), (1, 1, 40)],
+                         ids=["siso", "r2g2", "h40"])
 def test_frontend_kernel(rows):
     import torch
 
     from armhackathon_amd import _ffi
 
-    rank, groups = rows
-    b, L, h, hd, n, nang = 2, 70, 4, 16, 32, 8
-    case(f"front-end kernel rank {rank} groups {groups}")
+    rank, groups, h = rows  # 40 heads: two passes of the 32-head LDS staging
+    b, L, hd, n, nang = 2, 70, 16, 32, 8
+    case(f"front-end kernel rank {rank} groups {groups} heads {h}")
     need = 2 * h * hd + 2 * rank * groups * n + 3 * h + nang
     rs = need + 5  # a row stride wider than the columns
     rng = np.random.default_rng(9)
