@@ -273,7 +273,9 @@ static int mamba3_call(const ArmMamba3Dims* dims, const float* q, const float* k
     if (n_angles == 0 || n_angles > d.dqk / 2)
       return fail(ARM_SCAN_ERR_INVALID_DIMS, "n_angles (%zu) must be 1 .. dqk/2", n_angles);
     const char* why = nullptr;
-    if (!armscan::m3_angles_supported(p, &why)) {
+    // with the unfused route at hand, MIMO takes it: its 16/rank-step chunks make the
+    // fused pre-pass lengthen every iteration of a latency-bound loop
+    if (!armscan::m3_angles_supported(p, &why) || (unfused_ok && mimo)) {
       if (!unfused_ok) return fail(ARM_SCAN_ERR_INVALID_DIMS, "%s", why);
       // the pre-pass kernels into scratch cos/sin, then the scan on them
       const size_t half = d.dqk / 2, n_cs = d.batch * d.len * d.heads * half;

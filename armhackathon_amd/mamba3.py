@@ -14,6 +14,11 @@ values the behaviour is the reference's):
   * `return_last_state=True` also returns the final state (b, h, dv, dqk)
     (and, for SISO, last_bx (b, h, dqk)); the reference rejects a MIMO carry.
 
+Forward calls from raw angles whose v, z or angles are views (slices of a mixer's
+projection, angles expanded over heads, as apps/mamba3_lm/block.py:150-174 passes
+them) are read in place through arm_scan_mamba3_scan_strided_f32 instead of being
+copied contiguous.
+
 Tensors are device tensors; the scan runs in the HIP kernels of
 libarm_scan_hip.so on the current stream.
 """
@@ -141,6 +146,93 @@ def _angles_fusable(angles, cos, sin, reverse, q, k, v, q_bias, k_bias, z, rank)
         return False
     return all(t.data_ptr() % 16 == 0 for t in (q, k, v, q_bias, k_bias, angles)
                if t is not None) and (z is None or z.data_ptr() % 16 == 0)
+
+
+def _inplace_strides(v, z, angles):
+    """Element strides under which arm_scan_mamba3_scan_strided_f32 reads v and z
+    ((batch, step), heads dv apart, unit channel stride) and the angles ((batch, step,
+    head), unit pair stride) where they lie, or None when a layout does not fit. The
+    reference's Mamba-3 block hands the scan exactly such views: x and z are slices of
+    its in_proj output and the angles an `expand` over heads
+    (apps/mamba3_lm/block.py:150-174)."""
+    def vz(t):
+        b, length, h, dv = t.shape
+        if (dv > 1 and t.stride(3) != 1) or (h > 1 and t.stride(2) != dv):
+            return None
+        return (t.stride(0), t.stride(1))
+
+    sv = vz(v)
+    sz = None if z is None else vz(z)
+    if sv is None or (z is not None and sz is None):
+        return None
+    if angles.shape[3] > 1 and angles.stride(3) != 1:
+        return None
+    return {"v": sv, "z": sz, "angles": (angles.stride(0), angles.stride(1), angles.stride(2))}
+
+
+def _strided_route(angles, cos, sin, reverse, want_state, v, z):
+    """Forward from raw angles, no carries, and v, z or the angles not contiguous."""
+    if angles is None or cos is not None or sin is not None or reverse or want_state:
+        return None
+    if angles.dim() != 4 or all(t is None or t.is_contiguous() for t in (v, z, angles)):
+        return None
+    if any(t is not None and t.dtype != torch.float32 for t in (v, z, angles)):
+        return None  # read as they lie, so they must already be float32
+    return _inplace_strides(v, z, angles)
+
+
+def _run_strided(q, k, v, adt, dt, trap, q_bias, k_bias, angles, d_skip, z, psi, zeta, phi):
+    dev = _device_of(q, k, v, adt, dt, trap, q_bias, k_bias, angles, d_skip, z, psi, zeta,
+                     phi)
+    strides = _inplace_strides(v, z, angles)
+    if strides is None:
+        raise ValueError("v, z or angles have a layout the strided scan cannot read")
+    mimo = psi is not None
+    if mimo:
+        b, length, rank, groups, dqk = q.shape
+    else:
+        b, length, groups, dqk = q.shape
+        rank = 1
+    h, dv = v.shape[2], v.shape[3]
+    dims = _ffi.ArmMamba3Dims(b, h, dv, dqk, length, rank, groups)
+    out = torch.empty((b, length, h, dv), dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        _ffi.mamba3_strided_raw(
+            dims,
+            [q.data_ptr(), k.data_ptr(), v.data_ptr(), adt.data_ptr(), dt.data_ptr(),
+             trap.data_ptr(), q_bias.data_ptr(), k_bias.data_ptr(), angles.data_ptr(),
+             _ptr(d_skip), _ptr(z), _ptr(psi), _ptr(zeta), _ptr(phi)],
+            strides, angles.shape[-1], _ffi.BACKENDS["auto"], _ffi.THREADING["auto"],
+            out.data_ptr(), stream=_stream(dev))
+    _CALLS["n"] += 1
+    return out
+
+
+@torch.library.custom_op("arm_scan::mamba3_scan_strided", mutates_args=())
+def _mamba3_scan_strided_op(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    adt: torch.Tensor,
+    dt: torch.Tensor,
+    trap: torch.Tensor,
+    q_bias: torch.Tensor,
+    k_bias: torch.Tensor,
+    angles: torch.Tensor,
+    d_skip: Optional[torch.Tensor],
+    z: Optional[torch.Tensor],
+    psi: Optional[torch.Tensor] = None,
+    zeta: Optional[torch.Tensor] = None,
+    phi: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    return _run_strided(q, k, v, adt, dt, trap, q_bias, k_bias, angles, d_skip, z, psi, zeta,
+                        phi)
+
+
+@_mamba3_scan_strided_op.register_fake
+def _(q, k, v, adt, dt, trap, q_bias, k_bias, angles, d_skip, z, psi=None, zeta=None,
+      phi=None):
+    return q.new_empty((q.shape[0], q.shape[1], v.shape[2], v.shape[3]))
 
 
 @torch.library.custom_op("arm_scan::mamba3_scan_angles", mutates_args=())
@@ -273,6 +365,13 @@ def mamba3_scan(q, k, v, adt, dt, trap, q_bias, k_bias, angles=None,
         q = q.unsqueeze(2)
     if k.dim() == 3:
         k = k.unsqueeze(2)
+    if (angles is not None and v.dim() == 4 and angles.dim() == 4
+            and _strided_route(angles, cos, sin, reverse, return_last_state, v, z)):
+        # v, z or the angles are views (e.g. of a mixer's projection): read in place
+        _check_shapes(q, k, v, adt, dt, trap, q_bias, k_bias, None, None, D, z, angles=angles)
+        return _mamba3_scan_strided_op(
+            _c(q), _c(k), v, _c(adt), _c(dt), _c(trap), _c(q_bias), _c(k_bias), angles,
+            None if D is None else _c(D), z)
     q, k, v = _c(q), _c(k), _c(v)
     q_bias, k_bias = _c(q_bias), _c(k_bias)
     z = None if z is None else _c(z)
@@ -324,6 +423,14 @@ def mamba3_mimo_scan(q, k, v, adt, dt, trap, q_bias, k_bias, psi, zeta, phi,
     if k.dim() == 4:
         k = k.unsqueeze(3)
     rank = q.shape[2]
+    if (angles is not None and v.dim() == 4 and angles.dim() == 4
+            and _strided_route(angles, cos, sin, reverse, return_last_state, v, z)):
+        # v, z or the angles are views: the pre-pass and the scan read them in place
+        _check_shapes(q, k, v, adt, dt, trap, q_bias, k_bias, None, None, D, z, rank=rank,
+                      psi=psi, zeta=zeta, phi=phi, angles=angles)
+        return _mamba3_scan_strided_op(
+            _c(q), _c(k), v, _c(adt), _c(dt), _c(trap), _c(q_bias), _c(k_bias), angles,
+            None if D is None else _c(D), z, _c(psi), _c(zeta), _c(phi))
     # From raw angles MIMO takes the HIP pre-pass and the scan on cos/sin: with
     # 16/rank-step chunks the fused pre-pass lengthens every iteration of a loop that
     # is latency-bound (arm_scan_mamba3_scan_angles_f32 still serves it).

@@ -125,3 +125,50 @@ def test_frontend_kernel(rows):
     assert rel_err(host(adt), ADT.transpose(0, 2, 1)) <= 1e-5
     assert np.array_equal(host(trap), proj[..., 2 * h * hd + 2 * bc + 2 * h:
                                            2 * h * hd + 2 * bc + 3 * h].transpose(0, 2, 1))
+
+
+@pytest.mark.parametrize("mimo", [False, True], ids=["siso", "mimo_r2"])
+def test_public_scan_reads_views_in_place(mimo):
+    """arm_scan.mamba3_scan / mamba3_mimo_scan handed the reference block's views (x
+    and z slices of one projection, angles expanded over heads) read them in place
+    (arm_scan_mamba3_scan_strided_f32) and give the bits of the contiguous call; a
+    layout the strided entry cannot read (heads not dv apart) is copied instead."""
+    import torch
+
+    import armhackathon_amd as arm_scan
+    from armhackathon_amd.op import kernel_calls
+
+    case(f"public scan on views, mimo={mimo}")
+    g = torch.Generator(device="cuda").manual_seed(11)
+    b, L, h, dv, n, nang, r = 2, 100, 4, 16, 32, 8, (2 if mimo else 1)
+    f = dict(device="cuda", generator=g)
+    proj = torch.randn(b, L, 2 * h * dv + 12 + nang, **f)  # [z | x | pad | angles]
+    z, x = proj[..., :h * dv].view(b, L, h, dv), proj[..., h * dv:2 * h * dv].view(b, L, h, dv)
+    ang = proj[..., -nang:].unsqueeze(-2).expand(-1, -1, h, -1)
+    q = torch.randn(b, L, r, 1, n, **f) / n ** 0.5
+    k = torch.randn(b, L, r, 1, n, **f) / n ** 0.5
+    dt = torch.nn.functional.softplus(torch.randn(b, h, L, **f) - 3.0)
+    adt = -dt * torch.rand(h, 1, **f)
+    trap = torch.randn(b, h, L, **f)
+    D = torch.randn(h, **f)
+    if mimo:
+        qb, kb = (torch.randn(h, r, n, **f) * 0.1 for _ in range(2))
+        pzp = [torch.randn(h, r, dv, **f) for _ in range(3)]
+
+        def run(xx, zz, aa):
+            return arm_scan.mamba3_mimo_scan(q, k, xx, adt, dt, trap, qb, kb, *pzp, angles=aa,
+                                             D=D, z=zz)
+    else:
+        qb, kb = (torch.randn(h, n, **f) * 0.1 for _ in range(2))
+
+        def run(xx, zz, aa):
+            return arm_scan.mamba3_scan(q[:, :, 0], k[:, :, 0], xx, adt, dt, trap, qb, kb,
+                                        angles=aa, D=D, z=zz)
+    assert not x.is_contiguous() and ang.stride(2) == 0
+    got = run(x, z, ang)
+    want = run(x.contiguous(), z.contiguous(), ang.contiguous())
+    assert torch.equal(got, want)
+    # heads not dv apart: the copy route, same bits
+    xt = x.transpose(1, 2).contiguous().transpose(1, 2)
+    assert torch.equal(run(xt, z, ang), want)
+    assert kernel_calls() > 0
