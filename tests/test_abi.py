@@ -101,6 +101,23 @@ def test_m3_noncausal_rejections():
     assert call(D(1, 2, 4, 5, 3, 1, 1)) == 2   # odd dqk
 
 
+def test_m3_strided_rejections():
+    L = _ffi.load()
+    D = _ffi.ArmMamba3Dims
+
+    def call(vs=(64, 16), zs=(64, 16), ang=(64, 16, 4), z=None, angles=FAKE):
+        arr = lambda t: (ctypes.c_int64 * len(t))(*t)  # noqa: E731
+        return L.arm_scan_mamba3_scan_strided_f32(
+            ctypes.byref(D(1, 2, 8, 8, 4, 1, 1)), FAKE, FAKE, FAKE, arr(vs), FAKE, FAKE, FAKE,
+            FAKE, FAKE, angles, 4, arr(ang), None, z, arr(zs) if zs else None, None, None,
+            None, 0, 0, FAKE, None)
+
+    assert call(angles=None) == 1                   # raw angles are required
+    assert call(z=FAKE, zs=None) == 1               # z without its strides
+    assert call(vs=(-64, 16)) == 2                  # negative strides
+    assert call(ang=(64, 16, -4)) == 2
+
+
 def test_ss2d_rejections():
     L = _ffi.load()
     d = _ffi.ArmSS2DDims(1, 2, 3, 3, 4)

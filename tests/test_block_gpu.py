@@ -172,3 +172,40 @@ def test_public_scan_reads_views_in_place(mimo):
     xt = x.transpose(1, 2).contiguous().transpose(1, 2)
     assert torch.equal(run(xt, z, ang), want)
     assert kernel_calls() > 0
+
+
+def test_mixer_full_size_against_composition():
+    """The published SISO mixer at B2 L4096, where the oracle does not finish in
+    seconds: Mamba3Mixer (front-end kernel, in-place strided scan) against the
+    reference's block composition (torch front-end, then the public op on copies)."""
+    import torch
+    import torch.nn.functional as F
+
+    import armhackathon_amd as arm_scan
+    from armhackathon_amd.mamba3_block import Mamba3Mixer
+
+    case("published mixer B2 L4096 vs the torch composition")
+    m = Mamba3Mixer()
+    _randomise(m, 4)
+    m = m.cuda()
+    u = torch.randn(2, 4096, m.d_model, device="cuda", generator=torch.Generator(
+        device="cuda").manual_seed(1))
+    with torch.no_grad():
+        got = m(u)
+        b, L, _ = u.shape
+        h, p, n = m.nheads, m.headdim, m.d_state
+        z, x, B, C, ddt, dda, tr, ang = torch.split(m.in_proj(u), m.split_sizes, dim=-1)
+        B = m.B_norm(B.reshape(b, L, 1, 1, n))
+        C = m.C_norm(C.reshape(b, L, 1, 1, n))
+        A = torch.clamp(-(dda.clamp_min(0) + torch.reciprocal(1 - dda.clamp_max(0))),
+                        max=-m.A_floor)
+        DT = F.softplus(ddt + m.dt_bias)
+        y = arm_scan.mamba3_scan(
+            C[:, :, 0].contiguous(), B[:, :, 0].contiguous(), x.reshape(b, L, h, p).contiguous(),
+            (A * DT).permute(0, 2, 1).contiguous(), DT.permute(0, 2, 1).contiguous(),
+            tr.permute(0, 2, 1).contiguous(), m.C_bias[:, 0].contiguous(),
+            m.B_bias[:, 0].contiguous(),
+            angles=ang.unsqueeze(-2).expand(-1, -1, h, -1).contiguous(), D=m.D,
+            z=z.reshape(b, L, h, p).contiguous())
+        want = m.out_proj(y.reshape(b, L, h * p))
+    assert rel_err(host(got), host(want)) <= 1e-5

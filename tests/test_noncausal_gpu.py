@@ -211,3 +211,25 @@ def test_ss2d_noncausal(grid):
             ref = ref if merge == "sum" else ref * 0.5
             assert isinstance(out, torch.Tensor)
             assert rel_err(host(out), ref) <= TOL
+
+
+def test_noncausal_full_size():
+    """Config 3's shapes (B4 L4096, 24 heads x 64, dqk 128), where the oracle does not
+    finish in seconds: the accumulating kernel route against the composition of the
+    reference (the pair of traversals, minus the same-step term taken in float64)."""
+    import torch
+
+    import armhackathon_amd as arm_scan
+    from armhackathon_amd import workloads
+
+    case("noncausal at config 3 shapes vs the pair route")
+    x = workloads.m3_siso(seed=3)
+    t = {k: torch.from_numpy(v).cuda() for k, v in x.items()}
+    args = [t[k] for k in KEYS]
+    nc = arm_scan.noncausal_scan(*args, cos=t["cos"], sin=t["sin"])
+    fwd, bwd = arm_scan.mamba3_scan_pair(*args, cos=t["cos"], sin=t["sin"])
+    qb, kb = t["q"].double() + t["q_bias"].double(), t["k"].double() + t["k_bias"].double()
+    gamma = (t["dt"].double() * torch.sigmoid(t["trap"].double())).permute(0, 2, 1)
+    diag = (gamma * (qb * kb).sum(-1)).unsqueeze(-1) * t["v"].double()
+    ref = fwd.double() + bwd.double() - diag
+    assert rel_err(host(nc), host(ref)) <= 1e-5
