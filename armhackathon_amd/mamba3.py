@@ -104,7 +104,13 @@ def _run(q, k, v, adt, dt, trap, q_bias, k_bias, cos, sin, d_skip, z, reverse, p
 def _run_angles(q, k, v, adt, dt, trap, q_bias, k_bias, angles, d_skip, z, psi, zeta, phi,
                 want_state):
     """Forward scan with the angle pre-pass fused into the kernel
-    (arm_scan_mamba3_scan_angles_f32): raw angles instead of cos/sin."""
+    (arm_scan_mamba3_scan_angles_f32): raw angles instead of cos/sin. Tensors that are
+    not 16-byte aligned (views at odd offsets) take the pre-pass kernels and the scan
+    on cos/sin instead: the same result, unfused."""
+    if not _aligned16(q, k, v, q_bias, k_bias, angles, z):
+        cos, sin = angles_to_cos_sin(angles, dt, q.shape[-1] // 2)
+        return _run(q, k, v, adt, dt, trap, q_bias, k_bias, cos, sin, d_skip, z, False, psi,
+                    zeta, phi, want_state)
     dev = _device_of(q, k, v, adt, dt, trap, q_bias, k_bias, angles, d_skip, z, psi, zeta,
                      phi)
     mimo = psi is not None
@@ -133,19 +139,22 @@ def _run_angles(q, k, v, adt, dt, trap, q_bias, k_bias, angles, d_skip, z, psi, 
 
 
 def _angles_fusable(angles, cos, sin, reverse, q, k, v, q_bias, k_bias, z, rank):
-    """Whether the fused pre-pass serves this call: the conditions
+    """Whether the fused pre-pass serves this call by its shapes: the conditions
     arm_scan_mamba3_scan_angles_f32 declares (forward; angle pairs a positive
-    multiple of 4 up to dqk/2; dv, dqk multiples of 16, dqk <= 128; rank 1, 2 or 4;
-    16-byte aligned tensors)."""
+    multiple of 4 up to dqk/2; dv, dqk multiples of 16, dqk <= 128; rank 1, 2 or 4).
+    Its last condition, 16-byte aligned tensors, is checked inside the op
+    (`_run_angles`), where the tensors have storage: under torch.compile this runs
+    on fake tensors, which have no data pointer."""
     if angles is None or cos is not None or sin is not None or reverse or angles.dim() != 4:
         return False
     dqk, dv, r = q.shape[-1], v.shape[-1], angles.shape[-1]
     if r == 0 or r % 4 or r > dqk // 2 or dv % 16 or dqk % 16 or dqk > 128:
         return False
-    if rank not in (1, 2, 4):
-        return False
-    return all(t.data_ptr() % 16 == 0 for t in (q, k, v, q_bias, k_bias, angles)
-               if t is not None) and (z is None or z.data_ptr() % 16 == 0)
+    return rank in (1, 2, 4)
+
+
+def _aligned16(*tensors):
+    return all(t is None or t.data_ptr() % 16 == 0 for t in tensors)
 
 
 def _inplace_strides(v, z, angles):
