@@ -63,3 +63,17 @@ def test_frontend_rejects_short_rows():
         _ffi.block_frontend_raw(16, 1, 4, 10, 2, 4, 4, 1, 1, 2, 16, 1e-4, 16, 16, 1e-5, 16, 16,
                                 16, 16, 16)
     assert e.value.code == 2 and "row_stride" in str(e.value)
+
+
+def test_grid_views_round_trip():
+    """grid -> (row-major, column-major) views -> grid is exact, and the two orderings
+    differ (a transpose that silently did nothing would pass the scan checks)."""
+    torch = pytest.importorskip("torch")
+    from armhackathon_amd.ss2d_mamba3 import grid_to_views_time_major, views_to_grid_time_major
+
+    g = torch.arange(2 * 3 * 5 * 4, dtype=torch.float32).reshape(2, 3, 5, 4)
+    views = grid_to_views_time_major(g)
+    assert views.shape == (4, 15, 4)
+    rows, cols = views_to_grid_time_major(views[:2], views[2:], 3, 5)
+    assert torch.equal(rows, g) and torch.equal(cols, g)
+    assert not torch.equal(views[:2], views[2:])
