@@ -77,3 +77,24 @@ def test_grid_views_round_trip():
     rows, cols = views_to_grid_time_major(views[:2], views[2:], 3, 5)
     assert torch.equal(rows, g) and torch.equal(cols, g)
     assert not torch.equal(views[:2], views[2:])
+
+
+def test_use_arm_scan_swaps_and_restores():
+    """use_arm_scan (python/arm_scan/ss2d.py:170-202): every block exposing scan_pair_fn
+    or scan_fn gets this package's function, the count is returned, and enable=False
+    puts the originals back."""
+    torch = pytest.importorskip("torch")
+    from armhackathon_amd import ss2d
+
+    class Block(torch.nn.Module):
+        def __init__(self, attr):
+            super().__init__()
+            setattr(self, attr, lambda *a, **k: "original")
+
+    root = torch.nn.Sequential(Block("scan_pair_fn"), Block("scan_fn"), torch.nn.Linear(2, 2))
+    assert ss2d.use_arm_scan(root) == 2
+    assert root[0].scan_pair_fn is ss2d.scan_pair_arm and root[1].scan_fn is ss2d.scan_fn_arm
+    assert ss2d.use_arm_scan(root) == 2  # idempotent: the originals stay remembered
+    assert ss2d.use_arm_scan(root, enable=False) == 2
+    assert root[0].scan_pair_fn() == "original" and root[1].scan_fn() == "original"
+    assert not hasattr(root[0], "_arm_scan_saved_scan_pair_fn")

@@ -338,3 +338,41 @@ def test_m1_decode_step_optional_absent():
     out = arm_scan.selective_state_update(t["h"], t["x"], t["dt"], t["A"], t["B"], t["C"])
     assert rel_err(host(out), ref[..., 0]) < TOL
     assert rel_err(host(t["h"]), ref_h) < TOL
+
+
+def test_numpy_api_and_scan_fn():
+    """selective_scan_numpy (numpy in and out, python/arm_scan/numpy_api.py:16-70) and
+    the SS2D single-direction seam scan_fn_arm against the oracle; the reference's CPU
+    backends are refused with code 3."""
+    import torch
+
+    import armhackathon_amd as arm_scan
+    from armhackathon_amd import _ffi
+    from armhackathon_amd.ss2d import scan_fn_arm
+
+    case("numpy API and scan_fn_arm")
+    rng = np.random.default_rng(41)
+    b, d, L, n = 2, 32, 300, 16
+    u = rng.standard_normal((b, d, L)).astype(np.float32)
+    dl = (rng.standard_normal((b, d, L)) * 0.5 - 3.0).astype(np.float32)
+    A = -np.exp(rng.normal(0, 0.5, (d, n))).astype(np.float32)
+    B = rng.standard_normal((b, n, L)).astype(np.float32)
+    C = rng.standard_normal((b, n, L)).astype(np.float32)
+    D = rng.standard_normal(d).astype(np.float32)
+    z = rng.standard_normal((b, d, L)).astype(np.float32)
+    bias = rng.uniform(-0.5, 0.5, d).astype(np.float32)
+    ref, ref_last = oracle.selective_scan(u, dl, A, B, C, D=D, z=z, delta_bias=bias,
+                                          delta_softplus=True, dtype=np.float64)
+    out, last = arm_scan.selective_scan_numpy(u, dl, A, B, C, D=D, z=z, delta_bias=bias,
+                                              delta_softplus=True, return_last_state=True)
+    assert isinstance(out, np.ndarray) and out.dtype == np.float32
+    assert rel_err(out, ref) <= 1e-4 and rel_err(last, ref_last) <= 1e-4
+    with pytest.raises(_ffi.ArmScanError) as e:
+        arm_scan.selective_scan_numpy(u, dl, A, B, C, backend="scalar")
+    assert e.value.code == 3
+    t = {k: torch.from_numpy(v).cuda() for k, v in
+         dict(u=u, dl=dl, A=A, B=B, C=C, D=D, bias=bias).items()}
+    got = scan_fn_arm(t["u"], t["dl"], t["A"], t["B"], t["C"], D=t["D"], delta_bias=t["bias"])
+    ref2, _ = oracle.selective_scan(u, dl, A, B, C, D=D, delta_bias=bias, delta_softplus=True,
+                                    dtype=np.float64)
+    assert rel_err(host(got), ref2) <= 1e-4
