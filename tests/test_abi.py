@@ -146,3 +146,25 @@ def test_host_tensor_is_an_error():
     with pytest.raises(ValueError, match="device tensors"):
         arm_scan.selective_scan(u, u, torch.zeros(2, 4), torch.zeros(1, 4, 8),
                                 torch.zeros(1, 4, 8))
+
+
+def test_last_error_is_per_thread():
+    """arm_scan_last_error() explains the calling thread's most recent failure
+    (the reference's call is reentrant across threads, arm-scan-ffi/src/lib.rs)."""
+    import threading
+
+    L = _ffi.load()
+    seen = {}
+    barrier = threading.Barrier(2)
+
+    def worker(name, dims):
+        rc = _m1(dims)
+        barrier.wait()  # both threads have failed before either reads its message
+        seen[name] = (rc, L.arm_scan_last_error().decode())
+
+    t1 = threading.Thread(target=worker, args=("zero", _ffi.ArmScanDims(0, 2, 2, 2, 1)))
+    t2 = threading.Thread(target=worker, args=("groups", _ffi.ArmScanDims(1, 3, 2, 2, 2)))
+    t1.start(); t2.start(); t1.join(); t2.join()
+    assert seen["zero"][0] == 2 and seen["groups"][0] == 2
+    assert seen["zero"][1] != seen["groups"][1]
+    assert "zero" in seen["zero"][1] and "groups" in seen["groups"][1]
