@@ -25,6 +25,7 @@ __all__ = [
     "selective_scan_bidirectional",
     "selective_scan_time_major",
     "selective_state_update",
+    "causal_conv1d",
     "bidirectional_scan",
     "ss2d_scan",
     "use_arm_scan",
@@ -48,6 +49,7 @@ _LAZY = {
     "selective_scan_bidirectional": ".op",
     "selective_scan_time_major": ".op",
     "selective_state_update": ".op",
+    "causal_conv1d": ".op",
     "kernel_calls": ".op",
     "bidirectional_scan": ".bidirectional",
     "ss2d_scan": ".ss2d",

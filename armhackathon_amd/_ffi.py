@@ -131,6 +131,11 @@ def _declare(lib):
                   _ci, _ci,              # backend threading
                   _vp, _vp, _vp,         # out last_state last_bx
                   _vp]                   # stream
+    f = lib.arm_scan_causal_conv1d_f32
+    f.restype = _ci
+    f.argtypes = [*([ctypes.c_size_t] * 4),   # batch dim len width
+                  _vp, _vp, _vp, _vp,         # x x_strides weight bias
+                  _ci, _vp, _vp]              # silu out stream
     f = lib.arm_scan_mamba3_scan_strided_f32
     f.restype = _ci
     f.argtypes = [ctypes.POINTER(ArmMamba3Dims),
@@ -328,6 +333,15 @@ def mamba3_strided_raw(dims, ptrs, strides, n_angles, backend, threading, ptr_ou
         _p(ang), int(n_angles), angs, _p(d_skip), _p(z), zs, _p(psi), _p(zeta), _p(phi),
         int(backend), int(threading), ptr_out, _p(stream))
     _check(name, code)
+
+
+def causal_conv1d_raw(batch, dim, length, width, ptr_x, x_strides, ptr_w, ptr_bias, silu,
+                      ptr_out, *, stream=0):
+    """Call arm_scan_causal_conv1d_f32 (x strides in elements: batch, dim, step)."""
+    code = load().arm_scan_causal_conv1d_f32(batch, dim, length, width, ptr_x,
+                                             _i64x(x_strides), ptr_w, _p(ptr_bias),
+                                             int(bool(silu)), ptr_out, _p(stream))
+    _check("arm_scan_causal_conv1d_f32", code)
 
 
 def block_frontend_raw(ptr_proj, batch, length, row_stride, heads, headdim, d_state, rank,

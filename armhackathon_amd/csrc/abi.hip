@@ -353,6 +353,28 @@ int arm_scan_mamba3_scan_strided_f32(
                      z ? z_strides : nullptr, angle_strides, true);
 }
 
+int arm_scan_causal_conv1d_f32(size_t batch, size_t dim, size_t len, size_t width,
+                               const float* x, const int64_t* x_strides, const float* weight,
+                               const float* bias, int silu, float* out, void* stream) {
+  if (!x || !x_strides || !weight || !out)
+    return fail(ARM_SCAN_ERR_NULL_POINTER, "a required pointer is null");
+  if (!batch || !dim || !len || !width)
+    return fail(ARM_SCAN_ERR_INVALID_DIMS, "a dimension is zero");
+  if (width > 8) return fail(ARM_SCAN_ERR_INVALID_DIMS, "width (%zu) above 8", width);
+  if (batch > 65535 || dim > (1u << 22) || len > (1ull << 40) || !prod_ok({batch, dim, len}))
+    return fail(ARM_SCAN_ERR_INVALID_DIMS, "problem too large for this build");
+  for (int i = 0; i < 3; ++i)
+    if (x_strides[i] < 0) return fail(ARM_SCAN_ERR_INVALID_DIMS, "strides must be non-negative");
+  if (silu != 0 && silu != 1) return fail(ARM_SCAN_ERR_BAD_ENUM, "silu must be 0 or 1");
+  armscan::CausalConv c{};
+  c.x = x;
+  for (int i = 0; i < 3; ++i) c.xs[i] = (long long)x_strides[i];
+  c.w = weight; c.bias = bias; c.out = out;
+  c.batch = (int)batch; c.dim = (int)dim; c.width = (int)width; c.silu = silu;
+  c.len = (long long)len;
+  return run(armscan::causal_conv1d(c, (hipStream_t)stream), "causal conv1d launch");
+}
+
 int arm_scan_mamba3_block_frontend_f32(
     const float* proj, size_t batch, size_t len, size_t row_stride, size_t heads,
     size_t headdim, size_t d_state, size_t rank, size_t groups, size_t n_angles,

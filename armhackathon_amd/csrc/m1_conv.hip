@@ -1,0 +1,90 @@
+// The Mamba-1 mixer's depthwise causal convolution on gfx950, the step before the scan
+// in Hugging Face's MambaMixer (transformers modeling_mamba.py causal_conv1d_fn; the
+// reference runs it upstream, python/arm_scan/patch.py patches only the scan):
+//
+//   y[b, d, t] = act(bias[d] + sum_{k < K} w[d, k] * x[b, d, t - (K-1) + k]),  x[t < 0] = 0
+//
+// x is any strided (batch, dim, len) view. The mixer hands over the first half of its
+// in_proj output, (batch, len, 2*dim) storage, so channels are the contiguous axis.
+// y is written (batch, dim, len) contiguous, the layout F.conv1d returns. The
+// convolution is a transpose as well: a block stages a tile of kConvT + K - 1 steps x
+// kConvD channels through LDS. It reads the tile along channels, the contiguous axis of
+// such views, and writes along time.
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "scan_common.h"
+#include "scan_launch.h"
+
+namespace armscan {
+
+namespace {
+
+constexpr int kConvD = 64;        // channels per tile
+constexpr int kConvT = 64;        // steps per tile
+constexpr int kConvMaxK = 8;      // widest filter served
+constexpr int kConvThreads = 256;
+
+__global__ void __launch_bounds__(kConvThreads) causal_conv_kernel(CausalConv p) {
+  __shared__ float tile[(kConvT + kConvMaxK - 1) * (kConvD + 1)];  // [step][channel], padded
+  const int K = p.width;
+  const long long b = blockIdx.z;
+  const int d0 = blockIdx.y * kConvD;
+  const long long t0 = (long long)blockIdx.x * kConvT;
+  const int rows = kConvT + K - 1;  // steps t0-(K-1) .. t0+kConvT-1
+  const float* xb = p.x + b * p.xs[0];
+  if (p.vec) {
+    // unit channel stride, 16-byte aligned rows: four channels per load
+    for (int e = threadIdx.x; e < rows * (kConvD / 4); e += kConvThreads) {
+      const int r = e / (kConvD / 4), c = 4 * (e - r * (kConvD / 4));
+      const long long t = t0 - (K - 1) + r;
+      const int d = d0 + c;
+      float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      if (t >= 0 && t < p.len && d < p.dim)  // dim % 4 == 0: the piece is whole
+        v = *reinterpret_cast<const float4*>(xb + d + t * p.xs[2]);
+      float* row = tile + r * (kConvD + 1) + c;
+      row[0] = v.x; row[1] = v.y; row[2] = v.z; row[3] = v.w;
+    }
+  } else {
+    for (int e = threadIdx.x; e < rows * kConvD; e += kConvThreads) {
+      const int r = e / kConvD, c = e - r * kConvD;
+      const long long t = t0 - (K - 1) + r;
+      const int d = d0 + c;
+      float v = 0.0f;
+      if (t >= 0 && t < p.len && d < p.dim) v = xb[(long long)d * p.xs[1] + t * p.xs[2]];
+      tile[r * (kConvD + 1) + c] = v;
+    }
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < kConvD * kConvT; e += kConvThreads) {
+    const int c = e / kConvT, r = e - c * kConvT;
+    const int d = d0 + c;
+    const long long t = t0 + r;
+    if (d >= p.dim || t >= p.len) continue;
+    const float* w = p.w + (long long)d * K;
+    float acc = p.bias ? p.bias[d] : 0.0f;
+    for (int k = 0; k < K; ++k) acc = fmaf(w[k], tile[(r + k) * (kConvD + 1) + c], acc);
+    if (p.silu) acc = silu_fast(acc);
+    p.out[(b * p.dim + d) * p.len + t] = acc;
+  }
+}
+
+}  // namespace
+
+hipError_t causal_conv1d(const CausalConv& p, hipStream_t st) {
+  if (p.width < 1 || p.width > kConvMaxK || p.batch < 1 || p.dim < 1 || p.len < 1)
+    return hipErrorInvalidValue;
+  const long long tb = (p.len + kConvT - 1) / kConvT;
+  if (tb > 0x7fffffffLL || p.batch > 65535 || (p.dim + kConvD - 1) / kConvD > 65535)
+    return hipErrorInvalidValue;
+  const dim3 grid((unsigned)tb, (unsigned)((p.dim + kConvD - 1) / kConvD), (unsigned)p.batch);
+  CausalConv k = p;
+  k.vec = p.xs[1] == 1 && p.dim % 4 == 0 && p.xs[0] % 4 == 0 && p.xs[2] % 4 == 0 &&
+          ((uintptr_t)p.x & 15u) == 0;
+  hipLaunchKernelGGL(causal_conv_kernel, grid, dim3(kConvThreads), 0, st, k);
+  return hipGetLastError();
+}
+
+}  // namespace armscan

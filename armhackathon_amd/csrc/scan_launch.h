@@ -120,6 +120,20 @@ hipError_t m3_angles_to_cos_sin(const float* angles, const float* dt, size_t bat
                                 size_t len, size_t heads, size_t r, size_t half, float* cos,
                                 float* sin, hipStream_t st,
                                 const long long* ang_strides = nullptr);
+// The Mamba-1 mixer's depthwise causal convolution (m1_conv.hip): x any strided
+// (batch, dim, len) view, weight (dim, width), bias (dim) or null, silu or identity;
+// out (batch, dim, len) contiguous.
+struct CausalConv {
+  const float* x;
+  long long xs[3];  // element strides of x: batch, dim, step
+  const float *w, *bias;
+  float* out;
+  int batch, dim, width, silu;
+  long long len;
+  int vec;  // set by causal_conv1d: 16-byte channel pieces
+};
+hipError_t causal_conv1d(const CausalConv& p, hipStream_t st);
+
 // The Mamba-3 mixer's front-end (m3_block.hip, apps/mamba3_lm/block.py:146-178): from
 // the in_proj output, the head-major gates and the RMS-normalised q (C) and k (B).
 struct M3Frontend {

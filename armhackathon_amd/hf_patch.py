@@ -16,6 +16,11 @@ reference leaves to upstream (README.md:320-322). It is patched here as well, wi
 the same fallback rule: the fast path runs the step as one kernel instead of the
 dozen small torch kernels upstream launches per layer and token.
 
+The mixer's depthwise causal convolution (`causal_conv1d_fn`, the step before the
+scan) is patched under the same rule. Upstream's fallback copies the mixer's
+time-major projection contiguous, runs a depthwise conv and then a silu pass; here
+one kernel reads the view in place and fuses the bias and the silu.
+
 The mixer hands the gate z as a (batch, dim, len) view of its time-major
 in_proj output and transposes the scan output back for out_proj. The wrapper
 reads z in place and writes the output time-major (returned as a (batch, dim,
@@ -27,10 +32,30 @@ len) view), so neither side copies; the reference's op copies z
 
 import torch
 
-from .op import kernel_calls, selective_scan_time_major, selective_state_update
+from .op import causal_conv1d, kernel_calls, selective_scan_time_major, selective_state_update
 
-_STATE = {"orig": None, "orig_step": None, "target": None, "fast_calls": 0,
-          "fallback_calls": 0, "step_calls": 0, "step_fallback_calls": 0}
+_STATE = {"orig": None, "orig_step": None, "orig_conv": None, "target": None,
+          "fast_calls": 0, "fallback_calls": 0, "step_calls": 0, "step_fallback_calls": 0,
+          "conv_calls": 0, "conv_fallback_calls": 0}
+
+
+def _patch_conv_fn(modeling_mamba):
+    orig = modeling_mamba.causal_conv1d_fn
+
+    def causal_conv1d_fn(hidden_states, weight, bias=None, activation=None, **kwargs):
+        tensors = (hidden_states, weight) + (() if bias is None else (bias,))
+        needs_grad = torch.is_grad_enabled() and any(t.requires_grad for t in tensors)
+        if (needs_grad or activation not in (None, "silu", "swish")
+                or any(t.device.type != "cuda" or t.dtype != torch.float32 for t in tensors)
+                or hidden_states.dim() != 3 or weight.dim() != 2 or weight.shape[1] > 8):
+            _STATE["conv_fallback_calls"] += 1
+            return orig(hidden_states, weight, bias=bias, activation=activation, **kwargs)
+        _STATE["conv_calls"] += 1
+        # the mixer's input is a (b, D, L) view of time-major storage: read in place
+        return causal_conv1d(hidden_states, weight, bias=bias, activation=activation)
+
+    modeling_mamba.causal_conv1d_fn = causal_conv1d_fn
+    _STATE["orig_conv"] = orig
 
 
 def _patch_step_fn(modeling_mamba):
@@ -92,6 +117,9 @@ def _patch_scan_fn(modeling_mamba):
     if hasattr(modeling_mamba, "mamba_selective_state_update"):
         _patch_step_fn(modeling_mamba)
         done.append("transformers mamba_selective_state_update (decode step)")
+    if hasattr(modeling_mamba, "causal_conv1d_fn"):
+        _patch_conv_fn(modeling_mamba)
+        done.append("transformers causal_conv1d_fn (the mixer's causal convolution)")
     return done
 
 
@@ -123,8 +151,11 @@ def unpatch():
     modeling_mamba.mamba_selective_scan = _STATE["orig"]
     if _STATE["orig_step"] is not None:
         modeling_mamba.mamba_selective_state_update = _STATE["orig_step"]
+    if _STATE["orig_conv"] is not None:
+        modeling_mamba.causal_conv1d_fn = _STATE["orig_conv"]
     _STATE["orig"] = None
     _STATE["orig_step"] = None
+    _STATE["orig_conv"] = None
     _STATE["target"] = None
     return True
 
@@ -136,6 +167,8 @@ def stats():
         "fallback_calls": _STATE["fallback_calls"],
         "step_calls": _STATE["step_calls"],
         "step_fallback_calls": _STATE["step_fallback_calls"],
+        "conv_calls": _STATE["conv_calls"],
+        "conv_fallback_calls": _STATE["conv_fallback_calls"],
         "kernel_calls": kernel_calls(),
         "patched": _STATE["orig"] is not None,
         "api": "selective_scan_fn" if _STATE["orig"] is not None else None,

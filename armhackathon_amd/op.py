@@ -359,6 +359,43 @@ def selective_scan_bidirectional_with_state(u, delta, A, B, C, D=None, z=None,
     return of, ob, lf, lb
 
 
+@torch.library.custom_op("arm_scan::causal_conv1d", mutates_args=())
+def _causal_conv1d_op(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor],
+                      silu: bool) -> torch.Tensor:
+    dev = _device_of(x, weight, bias)
+    batch, dim, length = x.shape
+    out = torch.empty((batch, dim, length), dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        _ffi.causal_conv1d_raw(batch, dim, length, weight.shape[1], x.data_ptr(), x.stride(),
+                               weight.data_ptr(), _ptr(bias), silu, out.data_ptr(),
+                               stream=_stream(dev))
+    _CALLS["n"] += 1
+    return out
+
+
+@_causal_conv1d_op.register_fake
+def _(x, weight, bias, silu):
+    return x.new_empty(x.shape, dtype=torch.float32).contiguous()
+
+
+def causal_conv1d(x, weight, bias=None, activation=None):
+    """The Mamba-1 mixer's depthwise causal convolution (transformers modeling_mamba.py
+    causal_conv1d_fn; the reference leaves it upstream): x (batch, dim, len), any
+    strides (read in place), weight (dim, width <= 8), bias (dim,) or None, activation
+    None or "silu" -> (batch, dim, len) contiguous, float32."""
+    if activation not in (None, "silu", "swish"):
+        raise ValueError(f"activation must be None or 'silu', got {activation!r}")
+    if x.dim() != 3 or weight.dim() != 2 or weight.shape[0] != x.shape[1]:
+        raise ValueError(f"x (batch, dim, len) and weight (dim, width) expected, got "
+                         f"{tuple(x.shape)} and {tuple(weight.shape)}")
+    if bias is not None and tuple(bias.shape) != (x.shape[1],):
+        raise ValueError(f"bias must be ({x.shape[1]},), got {tuple(bias.shape)}")
+    if x.dtype != torch.float32:
+        x = x.float()
+    return _causal_conv1d_op(x, _c(weight), None if bias is None else _c(bias),
+                             activation is not None)
+
+
 def kernel_calls() -> int:
     """How many times the native library has been invoked (engagement check,
     python/arm_scan/op.py:163-166)."""

@@ -442,6 +442,7 @@ def bench_prefill(args, dev):
                         generator=torch.Generator(device=dev).manual_seed(0))
     arm_scan.patch()
     calls0 = arm_scan.stats()["fast_calls"]
+    conv0 = arm_scan.stats()["conv_calls"]
     with torch.no_grad():
         for _ in range(1):
             model(ids, use_cache=False, logits_to_keep=1)
@@ -455,7 +456,9 @@ def bench_prefill(args, dev):
     arm_scan.unpatch()
     return dict(tokens_per_s=8 * 2048 / dt, ms_per_forward=dt * 1e3,
                 scan_calls_per_forward=(st["fast_calls"] - calls0) / (1 + args.prefill_steps),
-                fallback_calls=st["fallback_calls"], batch=8, seq_len=2048,
+                conv_calls_per_forward=(st["conv_calls"] - conv0) / (1 + args.prefill_steps),
+                fallback_calls=st["fallback_calls"] + st["conv_fallback_calls"], batch=8,
+                seq_len=2048,
                 logits="last position only (logits_to_keep=1)")
 
 

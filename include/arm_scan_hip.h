@@ -18,7 +18,8 @@
  *     variants for callers' layouts and the fused Mamba-3 angle pre-pass
  *     (arm_scan_selective_scan_strided_f32, arm_scan_mamba3_scan_time_major_f32,
  *     arm_scan_mamba3_scan_angles_f32, arm_scan_mamba3_angles_f32), the decode
- *     step arm_scan_selective_state_update_f32, the non-causal Mamba-3 sum
+ *     step arm_scan_selective_state_update_f32 and the mixer's causal convolution
+ *     arm_scan_causal_conv1d_f32, the non-causal Mamba-3 sum
  *     arm_scan_mamba3_noncausal_f32, and the Mamba-3 mixer's front-end and strided
  *     scan (arm_scan_mamba3_block_frontend_f32, arm_scan_mamba3_scan_strided_f32),
  *     each described at its declaration;
@@ -197,6 +198,19 @@ int arm_scan_mamba3_scan_strided_f32(
     const int64_t* angle_strides, const float* d_skip, const float* z, const int64_t* z_strides,
     const float* mimo_psi, const float* mimo_zeta, const float* mimo_phi, int backend,
     int threading, float* out, void* stream);
+
+/* No reference counterpart: the Mamba-1 mixer's depthwise causal convolution, the step
+ * before the scan in Hugging Face's MambaMixer (transformers modeling_mamba.py
+ * causal_conv1d_fn), which the reference leaves to upstream (its patch replaces only
+ * the scan, python/arm_scan/patch.py:119-180):
+ *   out[b, d, t] = act(bias[d] + sum_{k < width} weight[d, k] x[b, d, t - width + 1 + k])
+ * with x[t < 0] = 0 and act silu (silu = 1) or the identity (silu = 0). x is any strided
+ * (batch, dim, len) view given by x_strides (batch, dim, step) in elements; the mixer
+ * passes the time-major half of its in_proj output. weight (dim, width), bias (dim) or
+ * NULL; out (batch, dim, len) contiguous. width <= 8. */
+int arm_scan_causal_conv1d_f32(size_t batch, size_t dim, size_t len, size_t width,
+                               const float* x, const int64_t* x_strides, const float* weight,
+                               const float* bias, int silu, float* out, void* stream);
 
 /* No reference counterpart: the Mamba-3 mixer's front-end, which the reference runs as
  * torch ops (apps/mamba3_lm/block.py:146-178), in one kernel. proj (batch, len,

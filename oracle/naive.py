@@ -297,6 +297,22 @@ def m3_mimo_scan(q, k, v, adt, dt, trap, q_bias, k_bias, psi, zeta, phi, cos, si
     return np.ascontiguousarray(out), S
 
 
+def causal_conv1d(x, w, bias=None, silu_act=False):
+    """Depthwise causal convolution (transformers modeling_mamba.py causal_conv1d_fn) in
+    float64: y[b, d, t] = bias[d] + sum_k w[d, k] x[b, d, t - K + 1 + k], x[t < 0] = 0,
+    through numpy's full convolution per row."""
+    x = np.asarray(x, np.float64)
+    w = np.asarray(w, np.float64)
+    b, d, L = x.shape
+    y = np.empty((b, d, L))
+    for j in range(d):
+        for i in range(b):
+            y[i, j] = np.convolve(x[i, j], w[j, ::-1])[:L]
+    if bias is not None:
+        y = y + np.asarray(bias, np.float64)[None, :, None]
+    return silu(y) if silu_act else y
+
+
 def heavy_tail(x):
     """1 + x for x >= 0, 1 / (1 - x) below (apps/mamba3_lm/block.py:52-62)."""
     x = np.asarray(x, np.float64)

@@ -98,3 +98,23 @@ def test_use_arm_scan_swaps_and_restores():
     assert ss2d.use_arm_scan(root, enable=False) == 2
     assert root[0].scan_pair_fn() == "original" and root[1].scan_fn() == "original"
     assert not hasattr(root[0], "_arm_scan_saved_scan_pair_fn")
+
+
+def test_causal_conv1d_oracle_closed_forms():
+    """The oracle's causal convolution: an impulse at t returns the taps in order
+    (w[d, K-1] at t, w[d, K-2] at t+1, ...), nothing before t (causality); width 1 is a
+    per-channel scale; linear in x."""
+    rng = np.random.default_rng(0)
+    w = rng.standard_normal((3, 4))
+    x = np.zeros((1, 3, 10))
+    x[0, :, 5] = 1.0
+    y = naive.causal_conv1d(x, w)
+    assert np.all(y[0, :, :5] == 0.0)
+    np.testing.assert_allclose(y[0, :, 5:9], w[:, ::-1], rtol=0, atol=0)
+    x2 = rng.standard_normal((2, 3, 10))
+    np.testing.assert_allclose(naive.causal_conv1d(x2, w[:, :1]), x2 * w[None, :, :1],
+                               rtol=1e-15)
+    x3 = rng.standard_normal((2, 3, 10))
+    np.testing.assert_allclose(naive.causal_conv1d(2 * x2 - x3, w),
+                               2 * naive.causal_conv1d(x2, w) - naive.causal_conv1d(x3, w),
+                               rtol=1e-12, atol=1e-12)

@@ -376,3 +376,44 @@ def test_numpy_api_and_scan_fn():
     ref2, _ = oracle.selective_scan(u, dl, A, B, C, D=D, delta_bias=bias, delta_softplus=True,
                                     dtype=np.float64)
     assert rel_err(host(got), ref2) <= 1e-4
+
+
+CONV = [  # (batch, dim, len, width, bias, silu, time-major view)
+    (2, 64, 300, 4, True, True, True),
+    (1, 100, 70, 4, False, True, True),
+    (3, 37, 5, 4, True, False, False),
+    (1, 16, 1, 2, True, True, True),
+    (2, 130, 257, 8, True, True, False),
+    (1, 64, 64, 1, False, False, True),
+]
+
+
+@pytest.mark.parametrize("shape", CONV, ids=lambda s: "x".join(map(str, s)))
+def test_causal_conv1d(shape):
+    """The mixer's causal convolution against numpy's full convolution per row, on the
+    HF mixer's layout (a (b, D, L) view of (b, L, 2D) storage) and on contiguous
+    input; widths 1 .. 8, lengths shorter than the filter, ragged tiles."""
+    import torch
+
+    import armhackathon_amd as arm_scan
+    from oracle import naive
+
+    b, d, L, K, with_bias, act, tm = shape
+    case(f"causal conv1d {shape}")
+    rng = np.random.default_rng(43)
+    x = rng.standard_normal((b, d, L)).astype(np.float32)
+    w = rng.standard_normal((d, K)).astype(np.float32)
+    bias = rng.standard_normal(d).astype(np.float32) if with_bias else None
+    ref = naive.causal_conv1d(x, w, bias, silu_act=act)
+    if tm:
+        store = torch.zeros((b, L, 2 * d), device="cuda")
+        store[..., :d] = torch.from_numpy(x).cuda().transpose(1, 2)
+        xt = store[..., :d].transpose(1, 2)
+        assert not xt.is_contiguous() or L == 1  # one step: torch counts it contiguous
+    else:
+        xt = torch.from_numpy(x).cuda()
+    out = arm_scan.causal_conv1d(xt, torch.from_numpy(w).cuda(),
+                                 None if bias is None else torch.from_numpy(bias).cuda(),
+                                 activation="silu" if act else None)
+    assert out.is_contiguous() and out.shape == (b, d, L)
+    assert rel_err(host(out), ref) <= 1e-5

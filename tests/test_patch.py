@@ -15,6 +15,7 @@ def test_patch_falls_back_on_host_tensors():
 
     orig = modeling_mamba.mamba_selective_scan
     orig_step = modeling_mamba.mamba_selective_state_update
+    orig_conv = modeling_mamba.causal_conv1d_fn
     cfg = MambaConfig(vocab_size=64, hidden_size=16, state_size=4, num_hidden_layers=2,
                       expand=2, conv_kernel=4, time_step_rank=2)
     torch.manual_seed(0)
@@ -27,6 +28,8 @@ def test_patch_falls_back_on_host_tensors():
             assert targets and "mamba_selective_scan" in targets[0]
             assert any("mamba_selective_state_update" in t for t in targets)
             assert modeling_mamba.mamba_selective_state_update is not orig_step
+            assert any("causal_conv1d_fn" in t for t in targets)
+            assert modeling_mamba.causal_conv1d_fn is not orig_conv
             assert arm_scan.patch() == ["transformers mamba_selective_scan (already patched)"]
             assert modeling_mamba.mamba_selective_scan is not orig
             before = arm_scan.stats()
@@ -36,8 +39,11 @@ def test_patch_falls_back_on_host_tensors():
             assert arm_scan.unpatch()
     assert modeling_mamba.mamba_selective_scan is orig
     assert modeling_mamba.mamba_selective_state_update is orig_step
+    assert modeling_mamba.causal_conv1d_fn is orig_conv
     assert not arm_scan.unpatch()
     assert after["fallback_calls"] - before["fallback_calls"] == 2
     assert after["fast_calls"] == before["fast_calls"]
+    assert after["conv_fallback_calls"] - before["conv_fallback_calls"] == 2
+    assert after["conv_calls"] == before["conv_calls"]
     assert torch.equal(ref, got)
     assert transformers is not None

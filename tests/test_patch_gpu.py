@@ -48,6 +48,8 @@ def test_patch_logits_and_engagement(length):
             arm_scan.unpatch()
     assert s1["fast_calls"] - s0["fast_calls"] == 3
     assert s1["fallback_calls"] == s0["fallback_calls"]
+    assert s1["conv_calls"] - s0["conv_calls"] == 3
+    assert s1["conv_fallback_calls"] == s0["conv_fallback_calls"]
     scale = max(1.0, ref.abs().max().item())
     assert (got - ref).abs().max().item() < 1e-4 * scale
     assert not arm_scan.stats()["patched"]
