@@ -26,6 +26,7 @@ __all__ = [
     "selective_scan_time_major",
     "selective_state_update",
     "causal_conv1d",
+    "causal_conv1d_update",
     "bidirectional_scan",
     "ss2d_scan",
     "use_arm_scan",
@@ -50,6 +51,7 @@ _LAZY = {
     "selective_scan_time_major": ".op",
     "selective_state_update": ".op",
     "causal_conv1d": ".op",
+    "causal_conv1d_update": ".op",
     "kernel_calls": ".op",
     "bidirectional_scan": ".bidirectional",
     "ss2d_scan": ".ss2d",

@@ -136,6 +136,11 @@ def _declare(lib):
     f.argtypes = [*([ctypes.c_size_t] * 4),   # batch dim len width
                   _vp, _vp, _vp, _vp,         # x x_strides weight bias
                   _ci, _vp, _vp]              # silu out stream
+    f = lib.arm_scan_causal_conv1d_update_f32
+    f.restype = _ci
+    f.argtypes = [*([ctypes.c_size_t] * 3),   # batch dim width
+                  _vp, _vp, _vp, _vp, _vp,    # x x_strides conv_state weight bias
+                  _ci, _vp, _vp]              # silu out stream
     f = lib.arm_scan_mamba3_scan_strided_f32
     f.restype = _ci
     f.argtypes = [ctypes.POINTER(ArmMamba3Dims),
@@ -342,6 +347,15 @@ def causal_conv1d_raw(batch, dim, length, width, ptr_x, x_strides, ptr_w, ptr_bi
                                              _i64x(x_strides), ptr_w, _p(ptr_bias),
                                              int(bool(silu)), ptr_out, _p(stream))
     _check("arm_scan_causal_conv1d_f32", code)
+
+
+def causal_conv1d_update_raw(batch, dim, width, ptr_x, x_strides, ptr_state, ptr_w, ptr_bias,
+                             silu, ptr_out, *, stream=0):
+    """Call arm_scan_causal_conv1d_update_f32 (x strides in elements: batch, dim)."""
+    code = load().arm_scan_causal_conv1d_update_f32(batch, dim, width, ptr_x, _i64x(x_strides),
+                                                    ptr_state, ptr_w, _p(ptr_bias),
+                                                    int(bool(silu)), ptr_out, _p(stream))
+    _check("arm_scan_causal_conv1d_update_f32", code)
 
 
 def block_frontend_raw(ptr_proj, batch, length, row_stride, heads, headdim, d_state, rank,

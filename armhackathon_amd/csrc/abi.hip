@@ -375,6 +375,25 @@ int arm_scan_causal_conv1d_f32(size_t batch, size_t dim, size_t len, size_t widt
   return run(armscan::causal_conv1d(c, (hipStream_t)stream), "causal conv1d launch");
 }
 
+int arm_scan_causal_conv1d_update_f32(size_t batch, size_t dim, size_t width,
+                                      const float* x, const int64_t* x_strides,
+                                      float* conv_state, const float* weight,
+                                      const float* bias, int silu, float* out, void* stream) {
+  if (!x || !x_strides || !conv_state || !weight || !out)
+    return fail(ARM_SCAN_ERR_NULL_POINTER, "a required pointer is null");
+  if (!batch || !dim || !width) return fail(ARM_SCAN_ERR_INVALID_DIMS, "a dimension is zero");
+  if (width > 64 || batch > (1u << 30) || dim > (1u << 30) || !prod_ok({batch, dim, width}))
+    return fail(ARM_SCAN_ERR_INVALID_DIMS, "problem too large for this build");
+  if (x_strides[0] < 0 || x_strides[1] < 0)
+    return fail(ARM_SCAN_ERR_INVALID_DIMS, "strides must be non-negative");
+  if (silu != 0 && silu != 1) return fail(ARM_SCAN_ERR_BAD_ENUM, "silu must be 0 or 1");
+  armscan::CausalConvStep c{};
+  c.x = x; c.xs[0] = (long long)x_strides[0]; c.xs[1] = (long long)x_strides[1];
+  c.state = conv_state; c.w = weight; c.bias = bias; c.out = out;
+  c.batch = (int)batch; c.dim = (int)dim; c.width = (int)width; c.silu = silu;
+  return run(armscan::causal_conv1d_step(c, (hipStream_t)stream), "causal conv1d step launch");
+}
+
 int arm_scan_mamba3_block_frontend_f32(
     const float* proj, size_t batch, size_t len, size_t row_stride, size_t heads,
     size_t headdim, size_t d_state, size_t rank, size_t groups, size_t n_angles,

@@ -71,7 +71,35 @@ __global__ void __launch_bounds__(kConvThreads) causal_conv_kernel(CausalConv p)
   }
 }
 
+// One decode step: thread (b, d) shifts its window of the conv state left by one,
+// appends the new input and writes act(bias + w . window).
+__global__ void __launch_bounds__(kConvThreads) causal_conv_step_kernel(CausalConvStep p) {
+  const long long i = (long long)blockIdx.x * kConvThreads + threadIdx.x;  // b * dim + d
+  if (i >= (long long)p.batch * p.dim) return;
+  const long long b = i / p.dim, d = i - b * p.dim;
+  float* s = p.state + i * p.width;
+  const float* w = p.w + d * p.width;
+  const float x = p.x[b * p.xs[0] + d * p.xs[1]];
+  float acc = p.bias ? p.bias[d] : 0.0f;
+  for (int k = 0; k < p.width; ++k) {
+    const float v = k + 1 < p.width ? s[k + 1] : x;
+    s[k] = v;
+    acc = fmaf(w[k], v, acc);
+  }
+  if (p.silu) acc = silu(acc);
+  p.out[i] = acc;
+}
+
 }  // namespace
+
+hipError_t causal_conv1d_step(const CausalConvStep& p, hipStream_t st) {
+  const long long rows = (long long)p.batch * p.dim;
+  const long long blocks = (rows + kConvThreads - 1) / kConvThreads;
+  if (blocks <= 0 || blocks > 0x7fffffffLL || p.width < 1) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(causal_conv_step_kernel, dim3((unsigned)blocks), dim3(kConvThreads), 0,
+                     st, p);
+  return hipGetLastError();
+}
 
 hipError_t causal_conv1d(const CausalConv& p, hipStream_t st) {
   if (p.width < 1 || p.width > kConvMaxK || p.batch < 1 || p.dim < 1 || p.len < 1)

@@ -133,6 +133,18 @@ struct CausalConv {
   int vec;  // set by causal_conv1d: 16-byte channel pieces
 };
 hipError_t causal_conv1d(const CausalConv& p, hipStream_t st);
+// One decode step of it: state (batch, dim, width) contiguous, the window of the last
+// width inputs, shifted left in place with x (batch, dim; strides xs) appended; out
+// (batch, dim) = act(bias + sum_k w[d, k] state[b, d, k]) after the shift.
+struct CausalConvStep {
+  const float* x;
+  long long xs[2];  // element strides of x: batch, dim
+  float* state;
+  const float *w, *bias;
+  float* out;
+  int batch, dim, width, silu;
+};
+hipError_t causal_conv1d_step(const CausalConvStep& p, hipStream_t st);
 
 // The Mamba-3 mixer's front-end (m3_block.hip, apps/mamba3_lm/block.py:146-178): from
 // the in_proj output, the head-major gates and the RMS-normalised q (C) and k (B).

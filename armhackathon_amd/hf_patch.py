@@ -32,9 +32,11 @@ len) view), so neither side copies; the reference's op copies z
 
 import torch
 
-from .op import causal_conv1d, kernel_calls, selective_scan_time_major, selective_state_update
+from .op import (causal_conv1d, causal_conv1d_update, kernel_calls, selective_scan_time_major,
+                 selective_state_update)
 
-_STATE = {"orig": None, "orig_step": None, "orig_conv": None, "target": None,
+_STATE = {"orig": None, "orig_step": None, "orig_conv": None, "orig_conv_step": None,
+          "target": None,
           "fast_calls": 0, "fallback_calls": 0, "step_calls": 0, "step_fallback_calls": 0,
           "conv_calls": 0, "conv_fallback_calls": 0}
 
@@ -56,6 +58,26 @@ def _patch_conv_fn(modeling_mamba):
 
     modeling_mamba.causal_conv1d_fn = causal_conv1d_fn
     _STATE["orig_conv"] = orig
+    if not hasattr(modeling_mamba, "causal_conv1d_update"):
+        return
+    orig_step = modeling_mamba.causal_conv1d_update
+
+    def causal_conv1d_update_(hidden_states, conv_state, weight, bias=None, activation=None):
+        tensors = (hidden_states, conv_state, weight) + (() if bias is None else (bias,))
+        needs_grad = torch.is_grad_enabled() and any(t.requires_grad for t in tensors)
+        if (needs_grad or activation not in (None, "silu", "swish")
+                or any(t.device.type != "cuda" or t.dtype != torch.float32 for t in tensors)
+                or hidden_states.dim() != 3 or hidden_states.shape[-1] != 1
+                or weight.dim() != 2 or not conv_state.is_contiguous()
+                or tuple(conv_state.shape) != (*hidden_states.shape[:2], weight.shape[1])):
+            _STATE["conv_fallback_calls"] += 1
+            return orig_step(hidden_states, conv_state, weight, bias=bias, activation=activation)
+        _STATE["conv_calls"] += 1
+        return causal_conv1d_update(hidden_states[..., 0], conv_state, weight, bias=bias,
+                                    activation=activation).unsqueeze(-1)
+
+    modeling_mamba.causal_conv1d_update = causal_conv1d_update_
+    _STATE["orig_conv_step"] = orig_step
 
 
 def _patch_step_fn(modeling_mamba):
@@ -153,6 +175,9 @@ def unpatch():
         modeling_mamba.mamba_selective_state_update = _STATE["orig_step"]
     if _STATE["orig_conv"] is not None:
         modeling_mamba.causal_conv1d_fn = _STATE["orig_conv"]
+    if _STATE["orig_conv_step"] is not None:
+        modeling_mamba.causal_conv1d_update = _STATE["orig_conv_step"]
+    _STATE["orig_conv_step"] = None
     _STATE["orig"] = None
     _STATE["orig_step"] = None
     _STATE["orig_conv"] = None

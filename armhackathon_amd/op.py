@@ -396,6 +396,44 @@ def causal_conv1d(x, weight, bias=None, activation=None):
                              activation is not None)
 
 
+@torch.library.custom_op("arm_scan::causal_conv1d_update", mutates_args=("conv_state",))
+def _causal_conv1d_update_op(x: torch.Tensor, conv_state: torch.Tensor, weight: torch.Tensor,
+                             bias: Optional[torch.Tensor], silu: bool) -> torch.Tensor:
+    dev = _device_of(x, conv_state, weight, bias)
+    batch, dim = x.shape
+    out = torch.empty((batch, dim), dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        _ffi.causal_conv1d_update_raw(batch, dim, weight.shape[1], x.data_ptr(), x.stride(),
+                                      conv_state.data_ptr(), weight.data_ptr(), _ptr(bias),
+                                      silu, out.data_ptr(), stream=_stream(dev))
+    _CALLS["n"] += 1
+    return out
+
+
+@_causal_conv1d_update_op.register_fake
+def _(x, conv_state, weight, bias, silu):
+    return x.new_empty(x.shape, dtype=torch.float32)
+
+
+def causal_conv1d_update(x, conv_state, weight, bias=None, activation=None):
+    """One decode step of `causal_conv1d` (transformers modeling_mamba.py
+    causal_conv1d_update): conv_state (batch, dim, width), contiguous float32, holds the
+    last width inputs and is shifted in place with x (batch, dim) appended (any strides,
+    read in place); returns (batch, dim) = act(bias + weight . window)."""
+    if activation not in (None, "silu", "swish"):
+        raise ValueError(f"activation must be None or 'silu', got {activation!r}")
+    if x.dim() != 2 or weight.dim() != 2 or weight.shape[0] != x.shape[1]:
+        raise ValueError(f"x (batch, dim) and weight (dim, width) expected, got "
+                         f"{tuple(x.shape)} and {tuple(weight.shape)}")
+    if (tuple(conv_state.shape) != (x.shape[0], x.shape[1], weight.shape[1])
+            or not conv_state.is_contiguous() or conv_state.dtype != torch.float32):
+        raise ValueError("conv_state must be a contiguous float32 (batch, dim, width) tensor")
+    if x.dtype != torch.float32:
+        x = x.float()
+    return _causal_conv1d_update_op(x, conv_state, _c(weight),
+                                    None if bias is None else _c(bias), activation is not None)
+
+
 def kernel_calls() -> int:
     """How many times the native library has been invoked (engagement check,
     python/arm_scan/op.py:163-166)."""

@@ -464,8 +464,8 @@ def bench_prefill(args, dev):
 
 def bench_decode(dev, new_tokens=64, prompt=128):
     """Greedy generation with the cache (Mamba-130M architecture, random init, batch 1):
-    ms per new token unpatched, with the scan patched only, and with the decode step
-    patched too (transformers' mamba_selective_state_update)."""
+    ms per new token unpatched; patched but with upstream's two decode-step functions
+    (mamba_selective_state_update, causal_conv1d_update); and fully patched."""
     import torch
     from transformers import MambaConfig, MambaForCausalLM
     from transformers.models.mamba import modeling_mamba
@@ -502,9 +502,12 @@ def bench_decode(dev, new_tokens=64, prompt=128):
     arm_scan.patch()
     try:
         step = modeling_mamba.mamba_selective_state_update
+        conv_step = modeling_mamba.causal_conv1d_update
         modeling_mamba.mamba_selective_state_update = hf_patch._STATE["orig_step"]
-        r["scan_patched_ms_per_token"], _ = ms_per_token()
+        modeling_mamba.causal_conv1d_update = hf_patch._STATE["orig_conv_step"]
+        r["upstream_decode_steps_ms_per_token"], _ = ms_per_token()
         modeling_mamba.mamba_selective_state_update = step
+        modeling_mamba.causal_conv1d_update = conv_step
         r["ms_per_token"], got = ms_per_token()
     finally:
         arm_scan.unpatch()

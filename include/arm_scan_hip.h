@@ -19,7 +19,8 @@
  *     (arm_scan_selective_scan_strided_f32, arm_scan_mamba3_scan_time_major_f32,
  *     arm_scan_mamba3_scan_angles_f32, arm_scan_mamba3_angles_f32), the decode
  *     step arm_scan_selective_state_update_f32 and the mixer's causal convolution
- *     arm_scan_causal_conv1d_f32, the non-causal Mamba-3 sum
+ *     (arm_scan_causal_conv1d_f32, arm_scan_causal_conv1d_update_f32), the non-causal
+ *     Mamba-3 sum
  *     arm_scan_mamba3_noncausal_f32, and the Mamba-3 mixer's front-end and strided
  *     scan (arm_scan_mamba3_block_frontend_f32, arm_scan_mamba3_scan_strided_f32),
  *     each described at its declaration;
@@ -211,6 +212,16 @@ int arm_scan_mamba3_scan_strided_f32(
 int arm_scan_causal_conv1d_f32(size_t batch, size_t dim, size_t len, size_t width,
                                const float* x, const int64_t* x_strides, const float* weight,
                                const float* bias, int silu, float* out, void* stream);
+
+/* No reference counterpart: one decode step of arm_scan_causal_conv1d_f32, transformers'
+ * causal_conv1d_update: conv_state (batch, dim, width) contiguous holds the last width
+ * inputs; it is shifted left in place with x (batch, dim; strides x_strides) appended,
+ * and out (batch, dim) = act(bias + sum_k weight[d, k] conv_state[b, d, k]) after the
+ * shift. width <= 64. */
+int arm_scan_causal_conv1d_update_f32(size_t batch, size_t dim, size_t width,
+                                      const float* x, const int64_t* x_strides,
+                                      float* conv_state, const float* weight,
+                                      const float* bias, int silu, float* out, void* stream);
 
 /* No reference counterpart: the Mamba-3 mixer's front-end, which the reference runs as
  * torch ops (apps/mamba3_lm/block.py:146-178), in one kernel. proj (batch, len,

@@ -417,3 +417,33 @@ def test_causal_conv1d(shape):
                                  activation="silu" if act else None)
     assert out.is_contiguous() and out.shape == (b, d, L)
     assert rel_err(host(out), ref) <= 1e-5
+
+
+@pytest.mark.parametrize("width", [4, 2, 1])
+def test_causal_conv1d_update_token_by_token(width):
+    """The decode step, run token by token from a zero state, gives the full causal
+    convolution of the sequence (the oracle's), and leaves the last `width` inputs in
+    the state; x read from a strided (b, D) view as the mixer passes it."""
+    import torch
+
+    import armhackathon_amd as arm_scan
+    from oracle import naive
+
+    b, d, L = 2, 40, 9
+    case(f"causal conv1d update width {width}")
+    rng = np.random.default_rng(47)
+    x = rng.standard_normal((b, d, L)).astype(np.float32)
+    w = rng.standard_normal((d, width)).astype(np.float32)
+    bias = rng.standard_normal(d).astype(np.float32)
+    ref = naive.causal_conv1d(x, w, bias, silu_act=True)
+    store = torch.zeros((b, L, 2 * d), device="cuda")
+    store[..., d:] = torch.from_numpy(x).cuda().transpose(1, 2)
+    state = torch.zeros((b, d, width), device="cuda")
+    wt, bt = torch.from_numpy(w).cuda(), torch.from_numpy(bias).cuda()
+    outs = []
+    for t in range(L):
+        xt = store[:, t, d:]  # (b, D) view, channels contiguous
+        outs.append(host(arm_scan.causal_conv1d_update(xt, state, wt, bt, activation="silu")))
+    got = np.stack(outs, axis=-1)
+    assert rel_err(got, ref) <= 1e-5
+    np.testing.assert_array_equal(host(state), x[:, :, L - width:])

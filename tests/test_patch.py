@@ -16,6 +16,7 @@ def test_patch_falls_back_on_host_tensors():
     orig = modeling_mamba.mamba_selective_scan
     orig_step = modeling_mamba.mamba_selective_state_update
     orig_conv = modeling_mamba.causal_conv1d_fn
+    orig_conv_step = modeling_mamba.causal_conv1d_update
     cfg = MambaConfig(vocab_size=64, hidden_size=16, state_size=4, num_hidden_layers=2,
                       expand=2, conv_kernel=4, time_step_rank=2)
     torch.manual_seed(0)
@@ -30,6 +31,7 @@ def test_patch_falls_back_on_host_tensors():
             assert modeling_mamba.mamba_selective_state_update is not orig_step
             assert any("causal_conv1d_fn" in t for t in targets)
             assert modeling_mamba.causal_conv1d_fn is not orig_conv
+            assert modeling_mamba.causal_conv1d_update is not orig_conv_step
             assert arm_scan.patch() == ["transformers mamba_selective_scan (already patched)"]
             assert modeling_mamba.mamba_selective_scan is not orig
             before = arm_scan.stats()
@@ -40,6 +42,7 @@ def test_patch_falls_back_on_host_tensors():
     assert modeling_mamba.mamba_selective_scan is orig
     assert modeling_mamba.mamba_selective_state_update is orig_step
     assert modeling_mamba.causal_conv1d_fn is orig_conv
+    assert modeling_mamba.causal_conv1d_update is orig_conv_step
     assert not arm_scan.unpatch()
     assert after["fallback_calls"] - before["fallback_calls"] == 2
     assert after["fast_calls"] == before["fast_calls"]

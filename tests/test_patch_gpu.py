@@ -74,4 +74,5 @@ def test_patch_cached_generation():
             arm_scan.unpatch()
     assert st["fast_calls"] >= 3  # the prefill went through the kernel
     assert st["step_calls"] >= 3 * 11 and st["step_fallback_calls"] == 0  # and the decode
+    assert st["conv_calls"] >= 3 * 12 and st["conv_fallback_calls"] == 0  # prefill + steps
     assert torch.equal(ref, got)
