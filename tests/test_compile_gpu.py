@@ -50,6 +50,15 @@ def _cases():
     zv = proj[..., :h * dv].view(b, Lm, h, dv)
     angv = proj[..., -8:].unsqueeze(-2).expand(-1, -1, h, -1)
 
+    xc = _rand(b, L, 2 * d, seed=25)[..., :d].transpose(1, 2)  # the mixer's conv input
+    wc, bc = _rand(d, 4, seed=26), _rand(d, seed=27)
+    cst = _rand(b, d, 4, seed=28)
+
+    def conv_step():
+        s = cst.clone()
+        y = arm_scan.causal_conv1d_update(xc[..., 0], s, wc, bc, activation="silu")
+        return y, s
+
     mixer = Mamba3Mixer(d_model=32, d_state=32, headdim=16).cuda()
     uin = _rand(b, Lm, 32, seed=24)
 
@@ -84,10 +93,14 @@ def _cases():
          lambda: arm_scan.noncausal_scan(*m3, cos=cos, sin=sin, D=Dm, z=zz),
          ops.mamba3_noncausal.default, (*m3, cos, sin, Dm, zz)),
         ("Mamba3Mixer", lambda: mixer(uin), None, None),
+        ("causal_conv1d",
+         lambda: arm_scan.causal_conv1d(xc, wc, bc, activation="silu"),
+         ops.causal_conv1d.default, (xc, wc, bc, True)),
+        ("causal_conv1d_update", conv_step, None, None),
     ]
 
 
-@pytest.mark.parametrize("idx", range(9))
+@pytest.mark.parametrize("idx", range(11))
 def test_compile_fullgraph(idx):
     import torch
 
