@@ -14,16 +14,18 @@
  *   - ArmMamba3Dims gains `groups` (q/k carry a groups axis, head h reads group
  *     h / (heads / groups); groups == 1 is the reference layout);
  *   - Mamba-3 MIMO may write `last_state` (the reference rejects any MIMO carry);
- *   - new entry points: arm_scan_ss2d_f32 (the fused four-direction 2D scan), and
- *     variants for callers' layouts and the fused Mamba-3 angle pre-pass
- *     (arm_scan_selective_scan_strided_f32, arm_scan_mamba3_scan_time_major_f32,
- *     arm_scan_mamba3_scan_angles_f32, arm_scan_mamba3_angles_f32), the decode
- *     step arm_scan_selective_state_update_f32 and the mixer's causal convolution
- *     (arm_scan_causal_conv1d_f32, arm_scan_causal_conv1d_update_f32), the non-causal
- *     Mamba-3 sum
- *     arm_scan_mamba3_noncausal_f32, and the Mamba-3 mixer's front-end and strided
- *     scan (arm_scan_mamba3_block_frontend_f32, arm_scan_mamba3_scan_strided_f32),
- *     each described at its declaration;
+ *   - new entry points, each described at its declaration:
+ *       arm_scan_ss2d_f32, the fused four-direction 2D scan;
+ *       arm_scan_selective_scan_strided_f32 and arm_scan_mamba3_scan_time_major_f32,
+ *         variants for callers' layouts;
+ *       arm_scan_mamba3_scan_angles_f32 and arm_scan_mamba3_angles_f32, the Mamba-3
+ *         angle pre-pass fused into the scan and alone;
+ *       arm_scan_selective_state_update_f32, the Mamba-1 decode step;
+ *       arm_scan_causal_conv1d_f32 and arm_scan_causal_conv1d_update_f32, the Mamba-1
+ *         mixer's causal convolution and its decode step;
+ *       arm_scan_mamba3_noncausal_f32, the non-causal Mamba-3 sum;
+ *       arm_scan_mamba3_block_frontend_f32 and arm_scan_mamba3_scan_strided_f32, the
+ *         Mamba-3 mixer's front-end and the scan reading its projection in place;
  *   - code 6 reports a HIP launch / device error; arm_scan_last_error() explains
  *     the most recent nonzero code on the calling thread.
  *
@@ -173,12 +175,6 @@ int arm_scan_mamba3_scan_angles_f32(
     const float* mimo_psi, const float* mimo_zeta, const float* mimo_phi, int backend,
     int threading, float* out, float* last_state, float* last_bx, void* stream);
 
-/* No reference counterpart: the RoPE angle pre-pass the reference runs in Python
- * (python/arm_scan/mamba3.py:41-89) as one kernel. angles (batch, len, heads,
- * n_angles) raw, dt (batch, heads, len) post-softplus -> cos, sin (batch, len, heads,
- * half) with theta = cumsum_len(tanh(angle) * pi * dt); pairs n_angles .. half-1 get
- * cos 1, sin 0. Feeds arm_scan_mamba3_scan[_time_major]_f32 where the fused entry
- * point does not apply (reverse, MIMO, n_angles not a multiple of 4). */
 /* No reference counterpart: the forward Mamba-3 scan from raw angles with v, z and the
  * angles given by element strides, as the Mamba-3 mixer holds them: views into its
  * in_proj output, the angles shared by every head (apps/mamba3_lm/block.py:150-174
@@ -254,6 +250,13 @@ int arm_scan_mamba3_noncausal_f32(const ArmMamba3Dims* dims, const float* q, con
                                   const float* z, int backend, int threading, float* out,
                                   void* stream);
 
+/* No reference counterpart: the RoPE angle pre-pass the reference runs in Python
+ * (python/arm_scan/mamba3.py:41-89), as two kernels (the sums of sequence segments,
+ * then cos/sin from them). angles (batch, len, heads, n_angles) raw, dt (batch, heads,
+ * len) post-softplus -> cos, sin (batch, len, heads, half) with
+ * theta = cumsum_len(tanh(angle) * pi * dt); pairs n_angles .. half-1 get cos 1,
+ * sin 0. Feeds arm_scan_mamba3_scan[_time_major]_f32 where the fused entry point does
+ * not apply (reverse, MIMO, n_angles not a multiple of 4). */
 int arm_scan_mamba3_angles_f32(const float* angles, const float* dt, size_t batch, size_t len,
                                size_t heads, size_t n_angles, size_t half, float* cos,
                                float* sin, void* stream);
