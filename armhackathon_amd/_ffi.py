@@ -2,10 +2,12 @@
 
 Mirrors the reference loader (python/arm_scan/_ffi.py:1-224): the same search
 order idea, the same ABI-version check, the same argtypes and the same
-error-code -> exception mapping. What differs is what ABI 8 differs in
+error-code -> exception mapping. What differs is what ABI 9 differs in
 (include/arm_scan_hip.h): every tensor pointer is a device pointer, every entry
-point takes a trailing hipStream_t, ArmMamba3Dims carries `groups`, and there is
-one more entry point, arm_scan_ss2d_f32.
+point takes a trailing hipStream_t, ArmMamba3Dims carries `groups`, and there are
+new entry points (the fused 2D scan, the time-major, strided, raw-angle and
+non-causal Mamba-3 scans, the Mamba-3 mixer front-end, the strided Mamba-1 scan,
+its decode step and the mixer's causal convolution); the header lists them.
 
 Library search order:
   1. the ARM_SCAN_LIB environment variable (full path to the library);
@@ -19,7 +21,7 @@ import ctypes
 import os
 from pathlib import Path
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 LIB_NAME = "libarm_scan_hip.so"
 
@@ -40,18 +42,18 @@ SS2D_MERGES = {"none": 0, "sum": 1, "mean": 2}
 
 
 class ArmScanDims(ctypes.Structure):
-    # arm-scan-ffi/src/lib.rs:43-50 (unchanged in ABI 8)
+    # arm-scan-ffi/src/lib.rs:43-50 (unchanged in ABI 9)
     _fields_ = [(n, ctypes.c_size_t) for n in ("batch", "dim", "len", "state", "groups")]
 
 
 class ArmMamba3Dims(ctypes.Structure):
-    # arm-scan-ffi/src/lib.rs:362-373 plus `groups` (ABI 8)
+    # arm-scan-ffi/src/lib.rs:362-373 plus `groups` (ABI 9)
     _fields_ = [(n, ctypes.c_size_t)
                 for n in ("batch", "heads", "dv", "dqk", "len", "rank", "groups")]
 
 
 class ArmSS2DDims(ctypes.Structure):
-    # ABI 8: the fused four-direction 2D scan
+    # ABI 9: the fused four-direction 2D scan
     _fields_ = [(n, ctypes.c_size_t) for n in ("batch", "dim", "height", "width", "state")]
 
 
@@ -94,7 +96,8 @@ def _declare(lib):
     f = lib.arm_scan_selective_scan_strided_f32
     f.restype = _ci
     f.argtypes = [ctypes.POINTER(ArmScanDims),
-                  *([_vp] * 7),          # u delta a b c d_skip z
+                  _vp, _vp,              # u u_strides
+                  *([_vp] * 6),          # delta a b c d_skip z
                   _vp, _vp,              # z_strides delta_bias
                   _ci, _ci,              # delta_softplus reverse
                   _vp, _vp,              # out out_strides
@@ -135,7 +138,7 @@ def _declare(lib):
     f.restype = _ci
     f.argtypes = [*([ctypes.c_size_t] * 4),   # batch dim len width
                   _vp, _vp, _vp, _vp,         # x x_strides weight bias
-                  _ci, _vp, _vp]              # silu out stream
+                  _ci, _ci, _vp, _vp]         # silu out_time_major out stream
     f = lib.arm_scan_causal_conv1d_update_f32
     f.restype = _ci
     f.argtypes = [*([ctypes.c_size_t] * 3),   # batch dim width
@@ -236,14 +239,14 @@ def scan_raw(dims, ptr_u, ptr_delta, ptr_a, ptr_b, ptr_c, ptr_d_skip, ptr_z,
 
 def scan_strided_raw(dims, ptr_u, ptr_delta, ptr_a, ptr_b, ptr_c, ptr_d_skip, ptr_z,
                      z_strides, ptr_delta_bias, delta_softplus, ptr_out, out_strides,
-                     ptr_last=0, ptr_h0=0, *, reverse=False, stream=0):
-    """Call arm_scan_selective_scan_strided_f32: z and out given by element
+                     ptr_last=0, ptr_h0=0, *, reverse=False, stream=0, u_strides=None):
+    """Call arm_scan_selective_scan_strided_f32: u, z and out given by element
     strides (batch, dim, step); None = contiguous (batch, dim, len)."""
     def arr(s):
         return None if s is None else (ctypes.c_longlong * 3)(*[int(x) for x in s])
-    zs, os_ = arr(z_strides), arr(out_strides)
+    zs, os_, us = arr(z_strides), arr(out_strides), arr(u_strides)
     code = load().arm_scan_selective_scan_strided_f32(
-        ctypes.byref(dims), ptr_u, ptr_delta, ptr_a, ptr_b, ptr_c, _p(ptr_d_skip), _p(ptr_z),
+        ctypes.byref(dims), ptr_u, us, ptr_delta, ptr_a, ptr_b, ptr_c, _p(ptr_d_skip), _p(ptr_z),
         zs, _p(ptr_delta_bias), int(bool(delta_softplus)), int(bool(reverse)), ptr_out, os_,
         _p(ptr_last), _p(ptr_h0), _p(stream))
     _check("arm_scan_selective_scan_strided_f32", code)
@@ -341,11 +344,13 @@ def mamba3_strided_raw(dims, ptrs, strides, n_angles, backend, threading, ptr_ou
 
 
 def causal_conv1d_raw(batch, dim, length, width, ptr_x, x_strides, ptr_w, ptr_bias, silu,
-                      ptr_out, *, stream=0):
-    """Call arm_scan_causal_conv1d_f32 (x strides in elements: batch, dim, step)."""
+                      ptr_out, *, stream=0, time_major=False):
+    """Call arm_scan_causal_conv1d_f32 (x strides in elements: batch, dim, step; out
+    (batch, dim, len) contiguous, or (batch, len, dim) storage with time_major)."""
     code = load().arm_scan_causal_conv1d_f32(batch, dim, length, width, ptr_x,
                                              _i64x(x_strides), ptr_w, _p(ptr_bias),
-                                             int(bool(silu)), ptr_out, _p(stream))
+                                             int(bool(silu)), int(bool(time_major)), ptr_out,
+                                             _p(stream))
     _check("arm_scan_causal_conv1d_f32", code)
 
 

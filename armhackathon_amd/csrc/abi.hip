@@ -126,6 +126,7 @@ int arm_scan_selective_scan_f32(const ArmScanDims* dims, const float* u, const f
 }
 
 int arm_scan_selective_scan_strided_f32(const ArmScanDims* dims, const float* u,
+                                        const long long* u_strides,
                                         const float* delta, const float* a, const float* b,
                                         const float* c, const float* d_skip, const float* z,
                                         const long long* z_strides, const float* delta_bias,
@@ -144,6 +145,7 @@ int arm_scan_selective_scan_strided_f32(const ArmScanDims* dims, const float* u,
   for (int i = 0; i < 3; ++i) {
     p.z_stride[i] = z_strides ? z_strides[i] : 0;
     p.out_stride[i] = out_strides ? out_strides[i] : 0;
+    p.u_stride[i] = u_strides ? u_strides[i] : 0;
   }
   const char* why = nullptr;
   if (armscan::m1_strided_io(p) && !armscan::m1_strided_supported(p, &why))
@@ -355,7 +357,8 @@ int arm_scan_mamba3_scan_strided_f32(
 
 int arm_scan_causal_conv1d_f32(size_t batch, size_t dim, size_t len, size_t width,
                                const float* x, const int64_t* x_strides, const float* weight,
-                               const float* bias, int silu, float* out, void* stream) {
+                               const float* bias, int silu, int out_time_major, float* out,
+                               void* stream) {
   if (!x || !x_strides || !weight || !out)
     return fail(ARM_SCAN_ERR_NULL_POINTER, "a required pointer is null");
   if (!batch || !dim || !len || !width)
@@ -366,7 +369,10 @@ int arm_scan_causal_conv1d_f32(size_t batch, size_t dim, size_t len, size_t widt
   for (int i = 0; i < 3; ++i)
     if (x_strides[i] < 0) return fail(ARM_SCAN_ERR_INVALID_DIMS, "strides must be non-negative");
   if (silu != 0 && silu != 1) return fail(ARM_SCAN_ERR_BAD_ENUM, "silu must be 0 or 1");
+  if (out_time_major != 0 && out_time_major != 1)
+    return fail(ARM_SCAN_ERR_BAD_ENUM, "out_time_major must be 0 or 1");
   armscan::CausalConv c{};
+  c.out_tm = out_time_major;
   c.x = x;
   for (int i = 0; i < 3; ++i) c.xs[i] = (long long)x_strides[i];
   c.w = weight; c.bias = bias; c.out = out;

@@ -46,6 +46,10 @@ struct M1Kern {
   // step, and the bytes of one batch's slab (every offset inside it fits 32 bits)
   long long zs_b, zs_d, zs_t, os_b, os_d, os_t;
   unsigned z_bytes, o_bytes;
+  // strided u (m1_tile_kernel<.., SIO != 0>): per-lane buffer loads, as z's in SIO 1
+  long long us_b, us_d, us_t;
+  unsigned u_bytes;
+  int u_strided;
   int z_dma;  // strided z and out staged through LDS (m1_tile_kernel<.., 2>)
   // Rows cut into `segs` segments of `seg_chunks` chunks when there are too few rows
   // to fill the chip: segmap[row][s][n] = (A, B), the affine map of segment s < segs-1
@@ -282,7 +286,8 @@ __device__ __forceinline__ void chunk(const M1Kern& p, long long sb, int j, bool
                                       const float* Bg, const float* Cg, const float* a2s,
                                       float bias, float dskip, float* carry, float (&dn)[I],
                                       float (&un)[I], bool have, long long pre_sb,
-                                      long long zts = 1, long long ots = 1) {
+                                      long long zts = 1, long long ots = 1,
+                                      long long uts = 1) {
   constexpr bool V = VEC && FULL;
   const long long L = p.L;
   const int N = p.N;
@@ -291,7 +296,7 @@ __device__ __forceinline__ void chunk(const M1Kern& p, long long sb, int j, bool
   float sdt = 0.0f;
   if (!have) {
     load_block<I, REV, V>(drow, Lv, sb, 0.0f, dn, L);
-    load_block<I, REV, V>(urow, Lv, sb, 0.0f, un, L);
+    load_block<I, REV, V>(urow, Lv, sb, 0.0f, un, L, uts);  // uts != 1 only with !V
   }
 #pragma unroll
   for (int i = 0; i < I; ++i) {
@@ -622,7 +627,8 @@ __device__ __forceinline__ void tile_rows(const M1Kern& p, long long blk, int se
   const int N = p.N;
   const int bi = (int)(row / p.dim), d = (int)(row - (long long)bi * p.dim);
   const int g = d / p.group_size;
-  const float* urow = p.u + row * L;
+  const bool ustr = SIO && p.u_strided;  // u read by strides (wave-uniform)
+  const float* urow = ustr ? p.u + bi * p.us_b + d * p.us_d : p.u + row * L;
   const float* drow = p.delta + row * L;
   const float* zrow =
       p.z ? (SIO ? p.z + bi * p.zs_b + d * p.zs_d : p.z + row * L) : nullptr;
@@ -696,7 +702,13 @@ __device__ __forceinline__ void tile_rows(const M1Kern& p, long long blk, int se
     {
       float dd[I], uu[I];
       load_block<I, REV, true>(drow, L, sb, 0.0f, dd, L);
-      load_block<I, REV, true>(urow, L, sb, 0.0f, uu, L);
+      if (ustr) {
+        const long long tlo = REV ? L - sb - I : sb;  // the block's lowest memory step
+        load_block_strided<I, REV>(slab_rsrc(p.u + bib * p.us_b, p.u_bytes),
+                                   (unsigned)((d * p.us_d + tlo * p.us_t) * 4), p.us_t, uu);
+      } else {
+        load_block<I, REV, true>(urow, L, sb, 0.0f, uu, L);
+      }
 #pragma unroll
       for (int i = 0; i < I; ++i) {
         float x = dd[i] + bias;
@@ -755,7 +767,8 @@ __device__ __forceinline__ void tile_rows(const M1Kern& p, long long blk, int se
     float dn[I], un[I];
     chunk<LPR, I, REV, true, false>(p, nfull * CH + (long long)j * I, j, true, true, row, urow,
                                     drow, zrow, orow, Bg, Cg, a2s, bias, dskip, carry, dn, un,
-                                    false, -1, SIO ? p.zs_t : 1, SIO ? p.os_t : 1);
+                                    false, -1, SIO ? p.zs_t : 1, SIO ? p.os_t : 1,
+                                    ustr ? p.us_t : 1);
   }
 }
 
@@ -783,6 +796,8 @@ __device__ __forceinline__ void fold_rows(const M1Kern& p, long long blk, int se
   const int g = d / p.group_size;
   const float* urow = p.u + row * L;
   const float* drow = p.delta + row * L;
+  // strided u (the seam kernels): the block's 16 rows share one batch, wave-uniform
+  const long long bib = blk * (kWavesPerBlock * RPW) / p.dim;
   const float* Bg = p.B + ((long long)bi * p.groups + g) * N * L;
   const float bias = p.bias ? p.bias[d] : 0.0f;
   float* sA = small + (wave * RPW + rw) * N;
@@ -810,7 +825,13 @@ __device__ __forceinline__ void fold_rows(const M1Kern& p, long long blk, int se
     {
       float dd[I], uu[I];
       load_block<I, REV, true>(drow, L, sb, 0.0f, dd, L);
-      load_block<I, REV, true>(urow, L, sb, 0.0f, uu, L);
+      if (p.u_strided) {
+        const long long tlo = REV ? L - sb - I : sb;  // the block's lowest memory step
+        load_block_strided<I, REV>(slab_rsrc(p.u + bib * p.us_b, p.u_bytes),
+                                   (unsigned)((d * p.us_d + tlo * p.us_t) * 4), p.us_t, uu);
+      } else {
+        load_block<I, REV, true>(urow, L, sb, 0.0f, uu, L);
+      }
 #pragma unroll
       for (int i = 0; i < I; ++i) {
         float x = dd[i] + bias;
@@ -1035,7 +1056,8 @@ hipError_t run_tile(M1Kern& k, bool rev, hipStream_t st) {
 }  // namespace
 
 bool m1_strided_io(const M1Problem& pr) {
-  return (pr.z && !contiguous_strides(pr.z_stride, pr)) || !contiguous_strides(pr.out_stride, pr);
+  return (pr.z && !contiguous_strides(pr.z_stride, pr)) ||
+         !contiguous_strides(pr.out_stride, pr) || !contiguous_strides(pr.u_stride, pr);
 }
 
 bool m1_strided_supported(const M1Problem& pr, const char** why) {
@@ -1043,19 +1065,20 @@ bool m1_strided_supported(const M1Problem& pr, const char** why) {
     if (why) *why = w;
     return false;
   };
-  if (pr.len % 4 != 0 || !aligned16(pr.u) || !aligned16(pr.delta) || !aligned16(pr.B) ||
-      !aligned16(pr.C))
+  const bool u_cont = contiguous_strides(pr.u_stride, pr);
+  if (pr.len % 4 != 0 || (u_cont && !aligned16(pr.u)) || !aligned16(pr.delta) ||
+      !aligned16(pr.B) || !aligned16(pr.C))
     return no("strided z/out need len % 4 == 0 and 16-byte aligned u, delta, B, C");
   if (pr.dim % 16 != 0 || (pr.dim / pr.groups) % 16 != 0)
     return no("strided z/out need dim and dim/groups multiples of 16");
-  for (int t = 0; t < 2; ++t) {
-    const long long(&s)[3] = t ? pr.out_stride : pr.z_stride;
+  for (int t = 0; t < 3; ++t) {
+    const long long(&s)[3] = t == 2 ? pr.u_stride : t ? pr.out_stride : pr.z_stride;
     if (t == 0 && !pr.z) continue;
     if (contiguous_strides(s, pr)) continue;
-    if (s[0] < 0 || s[1] < 0 || s[2] < 0) return no("negative z/out strides");
+    if (s[0] < 0 || s[1] < 0 || s[2] < 0) return no("negative z/out/u strides");
     if (t == 1 && (s[1] == 0 || s[2] == 0)) return no("out strides must not be zero");
     if (slab_bytes(s, pr) >= (1LL << 32) || 4LL * (M1_TILE_I - 1) * s[2] >= (1LL << 31))
-      return no("a batch of strided z/out must span less than 4 GiB");
+      return no("a batch of strided z/out/u must span less than 4 GiB");
   }
   return true;
 }
@@ -1087,6 +1110,11 @@ hipError_t m1_scan_chunked(const M1Problem& pr, hipStream_t st) {
                          pr.state > kTileStates)) &&
               M1_TILE_I == 16;
     k.o_bytes = (unsigned)slab_bytes(os, pr);
+    if (!contiguous_strides(pr.u_stride, pr)) {
+      k.u_strided = 1;
+      k.us_b = pr.u_stride[0]; k.us_d = pr.u_stride[1]; k.us_t = pr.u_stride[2];
+      k.u_bytes = (unsigned)slab_bytes(pr.u_stride, pr);
+    }
     return k.z_dma ? run_tile<2>(k, rev, st) : run_tile<1>(k, rev, st);
   }
   // the tiled path needs every 16-row block inside one batch/group and 16-byte rows

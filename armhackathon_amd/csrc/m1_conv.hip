@@ -58,14 +58,43 @@ __global__ void __launch_bounds__(kConvThreads) causal_conv_kernel(CausalConv p)
     }
   }
   __syncthreads();
-  for (int e = threadIdx.x; e < kConvD * kConvT; e += kConvThreads) {
-    const int c = e / kConvT, r = e - c * kConvT;
+  if (p.out_tm) {
+    // (batch, len, dim) storage: consecutive lanes take consecutive channels, and a
+    // thread keeps one channel (kConvThreads is a multiple of kConvD), whose taps and
+    // bias it loads once
+    static_assert(kConvThreads % kConvD == 0, "a thread keeps its channel");
+    const int c = threadIdx.x % kConvD;
     const int d = d0 + c;
-    const long long t = t0 + r;
-    if (d >= p.dim || t >= p.len) continue;
-    const float* w = p.w + (long long)d * K;
+    if (d >= p.dim) return;  // no barrier follows
+    float wr[kConvMaxK];
+#pragma unroll
+    for (int k = 0; k < kConvMaxK; ++k) wr[k] = k < K ? p.w[(long long)d * K + k] : 0.0f;
+    const float bv = p.bias ? p.bias[d] : 0.0f;
+    for (int r = threadIdx.x / kConvD; r < kConvT; r += kConvThreads / kConvD) {
+      const long long t = t0 + r;
+      if (t >= p.len) break;
+      float acc = bv;
+#pragma unroll
+      for (int k = 0; k < kConvMaxK; ++k)
+        if (k < K) acc = fmaf(wr[k], tile[(r + k) * (kConvD + 1) + c], acc);
+      if (p.silu) acc = silu_fast(acc);
+      p.out[(b * p.len + t) * p.dim + d] = acc;
+    }
+    return;
+  }
+  // (batch, dim, len): a thread keeps one step (kConvThreads is a multiple of kConvT)
+  // and walks the channels, each wave on one channel, so taps and bias are uniform
+  static_assert(kConvThreads % kConvT == 0, "a thread keeps its step");
+  const int r = threadIdx.x % kConvT;
+  const long long t = t0 + r;
+  if (t >= p.len) return;  // no barrier follows
+  for (int c = threadIdx.x / kConvT; c < kConvD; c += kConvThreads / kConvT) {
+    const int d = d0 + c;
+    if (d >= p.dim) break;
     float acc = p.bias ? p.bias[d] : 0.0f;
-    for (int k = 0; k < K; ++k) acc = fmaf(w[k], tile[(r + k) * (kConvD + 1) + c], acc);
+#pragma unroll
+    for (int k = 0; k < kConvMaxK; ++k)
+      if (k < K) acc = fmaf(p.w[(long long)d * K + k], tile[(r + k) * (kConvD + 1) + c], acc);
     if (p.silu) acc = silu_fast(acc);
     p.out[(b * p.dim + d) * p.len + t] = acc;
   }

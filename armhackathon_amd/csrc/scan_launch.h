@@ -16,8 +16,8 @@ struct M1Problem {
   float *out2, *last2;  // bidirectional outputs
   int softplus, reverse;
   int merge;  // bidirectional: write out = fwd + bwd instead of two outputs
-  // element strides (batch, dim, step) of z and out; all zero = (dim*len, len, 1)
-  long long z_stride[3], out_stride[3];
+  // element strides (batch, dim, step) of z, out and u; all zero = (dim*len, len, 1)
+  long long z_stride[3], out_stride[3], u_stride[3];
 };
 
 hipError_t m1_scan(const M1Problem& p, hipStream_t st);
@@ -130,7 +130,8 @@ struct CausalConv {
   float* out;
   int batch, dim, width, silu;
   long long len;
-  int vec;  // set by causal_conv1d: 16-byte channel pieces
+  int vec;     // set by causal_conv1d: 16-byte channel pieces
+  int out_tm;  // out as (batch, len, dim) storage instead of (batch, dim, len)
 };
 hipError_t causal_conv1d(const CausalConv& p, hipStream_t st);
 // One decode step of it: state (batch, dim, width) contiguous, the window of the last

@@ -53,8 +53,11 @@ def _patch_conv_fn(modeling_mamba):
             _STATE["conv_fallback_calls"] += 1
             return orig(hidden_states, weight, bias=bias, activation=activation, **kwargs)
         _STATE["conv_calls"] += 1
-        # the mixer's input is a (b, D, L) view of time-major storage: read in place
-        return causal_conv1d(hidden_states, weight, bias=bias, activation=activation)
+        # the mixer's input is a (b, D, L) view of time-major storage: read in place;
+        # the output goes back time-major, so the mixer's x_proj (which reads its
+        # transpose) and the scan (which reads it as u, in place) need no copy
+        return causal_conv1d(hidden_states, weight, bias=bias, activation=activation,
+                             time_major=True)
 
     modeling_mamba.causal_conv1d_fn = causal_conv1d_fn
     _STATE["orig_conv"] = orig

@@ -146,9 +146,11 @@ def _strided_ok(u, delta, b, c, z, dim, length, groups):
     conditions its declaration states)."""
     if length % 4 or dim % 16 or (dim // groups) % 16:
         return False
-    if any(t.data_ptr() % 16 for t in (u, delta, b, c)):
+    if any(t.data_ptr() % 16 for t in (delta, b, c)):
         return False
-    for t in (z, None):
+    if u.is_contiguous() and u.data_ptr() % 16:
+        return False
+    for t in (z, None, u):
         st = (length * dim, 1, dim) if t is None else t.stride()
         if min(st) < 0 or 4 * ((dim - 1) * st[1] + (length - 1) * st[2] + 1) >= 1 << 32:
             return False
@@ -181,11 +183,13 @@ def _selective_scan_tm_op(
                                   None if z is None else z.stride(), _ptr(delta_bias),
                                   delta_softplus, out.data_ptr(), out.stride(),
                                   last_state.data_ptr(), _ptr(h0), reverse=reverse,
-                                  stream=_stream(dev))
+                                  stream=_stream(dev),
+                                  u_strides=None if u.is_contiguous() else u.stride())
         else:
             # a shape the strided kernel does not serve: the contiguous scan, then
             # the output laid out time-major
             zc = None if z is None else z.contiguous()
+            u = u.contiguous()
             tmp = torch.empty_like(u)
             _ffi.scan_raw(dims, u.data_ptr(), delta.data_ptr(), a.data_ptr(), b.data_ptr(),
                           c.data_ptr(), _ptr(d_skip), _ptr(zc), _ptr(delta_bias),
@@ -221,8 +225,11 @@ def selective_scan_time_major(u, delta, A, B, C, D=None, z=None, delta_bias=None
     C = _bc4(C, batch, state, length)
     if z is not None and z.dtype != torch.float32:
         z = z.float()
+    # u, like z, may be a view of time-major storage (the mixer's convolution output
+    # laid out for its x_proj): read in place
+    u = u.float() if u.dtype != torch.float32 else u
     out, last_state = _selective_scan_tm_op(
-        _c(u), _c(delta), _c(A), _c(B), _c(C),
+        u, _c(delta), _c(A), _c(B), _c(C),
         None if D is None else _c(D),
         z,
         None if delta_bias is None else _c(delta_bias),
@@ -361,28 +368,37 @@ def selective_scan_bidirectional_with_state(u, delta, A, B, C, D=None, z=None,
 
 @torch.library.custom_op("arm_scan::causal_conv1d", mutates_args=())
 def _causal_conv1d_op(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor],
-                      silu: bool) -> torch.Tensor:
+                      silu: bool, time_major: bool) -> torch.Tensor:
     dev = _device_of(x, weight, bias)
     batch, dim, length = x.shape
-    out = torch.empty((batch, dim, length), dtype=torch.float32, device=dev)
+    if time_major:
+        out = torch.empty((batch, length, dim), dtype=torch.float32,
+                          device=dev).transpose(1, 2)
+    else:
+        out = torch.empty((batch, dim, length), dtype=torch.float32, device=dev)
     with torch.cuda.device(dev):
         _ffi.causal_conv1d_raw(batch, dim, length, weight.shape[1], x.data_ptr(), x.stride(),
                                weight.data_ptr(), _ptr(bias), silu, out.data_ptr(),
-                               stream=_stream(dev))
+                               stream=_stream(dev), time_major=time_major)
     _CALLS["n"] += 1
     return out
 
 
 @_causal_conv1d_op.register_fake
-def _(x, weight, bias, silu):
-    return x.new_empty(x.shape, dtype=torch.float32).contiguous()
+def _(x, weight, bias, silu, time_major):
+    b, d, length = x.shape
+    if time_major:
+        return x.new_empty((b, length, d), dtype=torch.float32).transpose(1, 2)
+    return x.new_empty((b, d, length), dtype=torch.float32)
 
 
-def causal_conv1d(x, weight, bias=None, activation=None):
+def causal_conv1d(x, weight, bias=None, activation=None, time_major=False):
     """The Mamba-1 mixer's depthwise causal convolution (transformers modeling_mamba.py
     causal_conv1d_fn; the reference leaves it upstream): x (batch, dim, len), any
     strides (read in place), weight (dim, width <= 8), bias (dim,) or None, activation
-    None or "silu" -> (batch, dim, len) contiguous, float32."""
+    None or "silu" -> (batch, dim, len) float32, contiguous; or, with time_major, a view
+    of (batch, len, dim) storage, the layout the mixer's x_proj reads after its
+    transpose (and the scan reads in place)."""
     if activation not in (None, "silu", "swish"):
         raise ValueError(f"activation must be None or 'silu', got {activation!r}")
     if x.dim() != 3 or weight.dim() != 2 or weight.shape[0] != x.shape[1]:
@@ -393,7 +409,7 @@ def causal_conv1d(x, weight, bias=None, activation=None):
     if x.dtype != torch.float32:
         x = x.float()
     return _causal_conv1d_op(x, _c(weight), None if bias is None else _c(bias),
-                             activation is not None)
+                             activation is not None, bool(time_major))
 
 
 @torch.library.custom_op("arm_scan::causal_conv1d_update", mutates_args=("conv_state",))

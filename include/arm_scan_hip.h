@@ -49,7 +49,7 @@
 extern "C" {
 #endif
 
-#define ARM_SCAN_ABI_VERSION 8u
+#define ARM_SCAN_ABI_VERSION 9u
 
 /* Return codes: arm-scan-ffi/src/lib.rs:53-58, plus 6. */
 #define ARM_SCAN_OK 0
@@ -70,17 +70,17 @@ typedef struct ArmScanDims {
   size_t batch, dim, len, state, groups;
 } ArmScanDims;
 
-/* arm-scan-ffi/src/lib.rs:362-373 plus `groups` (ABI 8). */
+/* arm-scan-ffi/src/lib.rs:362-373 plus `groups` (ABI 9). */
 typedef struct ArmMamba3Dims {
   size_t batch, heads, dv, dqk, len, rank, groups;
 } ArmMamba3Dims;
 
-/* New in ABI 8: the 2D cross-scan over a (height, width) token grid. */
+/* New in ABI 9: the 2D cross-scan over a (height, width) token grid. */
 typedef struct ArmSS2DDims {
   size_t batch, dim, height, width, state;
 } ArmSS2DDims;
 
-/* Replaces arm_scan_abi_version (arm-scan-ffi/src/lib.rs:37-40); returns 8. */
+/* Replaces arm_scan_abi_version (arm-scan-ffi/src/lib.rs:37-40); returns 9. */
 uint32_t arm_scan_abi_version(void);
 
 /* Replaces arm_scan_selective_scan_f32 (arm-scan-ffi/src/lib.rs:99-216).
@@ -93,17 +93,20 @@ int arm_scan_selective_scan_f32(const ArmScanDims* dims, const float* u, const f
                                 int delta_softplus, int reverse, int backend, int threading,
                                 float* out, float* last_state, const float* h0, void* stream);
 
-/* No reference counterpart: arm_scan_selective_scan_f32 with z and out given by
+/* No reference counterpart: arm_scan_selective_scan_f32 with u, z and out given by
  * element strides (batch, dim, step) instead of as contiguous (batch, dim, len).
  * It serves the Hugging Face seam, which hands the gate z as a (batch, dim, len)
  * view of time-major (batch, len, 2*dim) storage (transformers modeling_mamba.py
  * MambaMixer.forward -> mamba_selective_scan(..., z=gate)); the reference copies it
  * (python/arm_scan/op.py:19-20). Writing out time-major likewise lets the caller's
- * out_proj read it without a copy. A null stride array means contiguous. Needs
- * len % 4 == 0, dim and dim/groups multiples of 16, 16-byte aligned u/delta/B/C and
- * each batch of z/out inside 4 GiB; otherwise ARM_SCAN_ERR_INVALID_DIMS, and the
- * caller makes z/out contiguous and calls arm_scan_selective_scan_f32. */
+ * out_proj read it without a copy, and u may be a time-major view too (the mixer's
+ * convolution output laid out for its x_proj). A null stride array means contiguous.
+ * Needs len % 4 == 0, dim and dim/groups multiples of 16, 16-byte aligned delta/B/C
+ * (and u when contiguous) and each batch of u/z/out inside 4 GiB; otherwise
+ * ARM_SCAN_ERR_INVALID_DIMS, and the caller makes them contiguous and calls
+ * arm_scan_selective_scan_f32. */
 int arm_scan_selective_scan_strided_f32(const ArmScanDims* dims, const float* u,
+                                        const long long* u_strides,
                                         const float* delta, const float* a, const float* b,
                                         const float* c, const float* d_skip, const float* z,
                                         const long long* z_strides, const float* delta_bias,
@@ -147,7 +150,7 @@ int arm_scan_mamba3_scan_f32(const ArmMamba3Dims* dims, const float* q, const fl
                              const float* mimo_phi, int reverse, int backend, int threading,
                              float* out, float* last_state, float* last_bx, void* stream);
 
-/* New in ABI 8 (no counterpart in the reference): arm_scan_mamba3_scan_f32 with out
+/* New in ABI 9 (no counterpart in the reference): arm_scan_mamba3_scan_f32 with out
  * written time-major (batch, len, heads, dv), the layout python/arm_scan/mamba3.py:142
  * produces from the head-major result with a permute and a copy. Same arguments,
  * checks and codes. */
@@ -204,10 +207,12 @@ int arm_scan_mamba3_scan_strided_f32(
  * with x[t < 0] = 0 and act silu (silu = 1) or the identity (silu = 0). x is any strided
  * (batch, dim, len) view given by x_strides (batch, dim, step) in elements; the mixer
  * passes the time-major half of its in_proj output. weight (dim, width), bias (dim) or
- * NULL; out (batch, dim, len) contiguous. width <= 8. */
+ * NULL; out (batch, dim, len) contiguous, or with out_time_major = 1 (batch, len, dim)
+ * storage, the layout the mixer's x_proj reads. width <= 8. */
 int arm_scan_causal_conv1d_f32(size_t batch, size_t dim, size_t len, size_t width,
                                const float* x, const int64_t* x_strides, const float* weight,
-                               const float* bias, int silu, float* out, void* stream);
+                               const float* bias, int silu, int out_time_major, float* out,
+                               void* stream);
 
 /* No reference counterpart: one decode step of arm_scan_causal_conv1d_f32, transformers'
  * causal_conv1d_update: conv_state (batch, dim, width) contiguous holds the last width
@@ -261,7 +266,7 @@ int arm_scan_mamba3_angles_f32(const float* angles, const float* dt, size_t batc
                                size_t heads, size_t n_angles, size_t half, float* cos,
                                float* sin, void* stream);
 
-/* New in ABI 8 (no single reference symbol: it fuses python/arm_scan/ss2d.py:277-342,
+/* New in ABI 9 (no single reference symbol: it fuses python/arm_scan/ss2d.py:277-342,
  * which composes two bidirectional calls). Four directions over a (H, W) grid:
  * row_fwd, row_bwd over the row-major flattening t = i*W + j, col_fwd, col_bwd over the
  * column-major one t = j*H + i; backward = reverse index mode.

@@ -1,7 +1,7 @@
 """The C ABI of libarm_scan_hip.so, host side only (no GPU needed).
 
 * every function declared in include/arm_scan_hip.h is exported by the library;
-* the ABI version is 8 and the loader checks it;
+* the ABI version is 9 and the loader checks it;
 * the reference's rejection codes (arm-scan-ffi/src/lib.rs:53-58, :117-158,
   :461-487) come back before any launch: null pointers -> 1, bad dims -> 2,
   CPU backends -> 3, bad enums -> 4. These calls never touch the device, so
@@ -34,7 +34,7 @@ def test_header_symbols_exported():
 
 
 def test_abi_version():
-    assert _ffi.load().arm_scan_abi_version() == 8 == _ffi.ABI_VERSION
+    assert _ffi.load().arm_scan_abi_version() == 9 == _ffi.ABI_VERSION
 
 
 def _m1(dims, u=FAKE, backend=0, threading=0, last=None, h0=None):

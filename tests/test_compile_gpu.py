@@ -95,7 +95,7 @@ def _cases():
         ("Mamba3Mixer", lambda: mixer(uin), None, None),
         ("causal_conv1d",
          lambda: arm_scan.causal_conv1d(xc, wc, bc, activation="silu"),
-         ops.causal_conv1d.default, (xc, wc, bc, True)),
+         ops.causal_conv1d.default, (xc, wc, bc, True, True)),
         ("causal_conv1d_update", conv_step, None, None),
     ]
 

@@ -447,3 +447,55 @@ def test_causal_conv1d_update_token_by_token(width):
     got = np.stack(outs, axis=-1)
     assert rel_err(got, ref) <= 1e-5
     np.testing.assert_array_equal(host(state), x[:, :, L - width:])
+
+
+@pytest.mark.parametrize("shape", [(2, 64, 512, False), (1, 32, 300, False), (2, 64, 512, True),
+                                   (8, 1536, 2048, False)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_time_major_u(shape):
+    """u, z and out all views of time-major storage (the HF mixer's convolution output
+    laid out for its x_proj): bit-identical to the contiguous call. Few rows take the
+    segmented scan (its fold reads u by strides too); L = 300 has a tail chunk."""
+    import torch
+
+    import armhackathon_amd as arm_scan
+
+    b, d, L, rev = shape
+    case(f"time-major u {shape}")
+    g = torch.Generator(device="cuda").manual_seed(5)
+    f = dict(device="cuda", generator=g)
+    u_tm = torch.randn(b, L, d, **f).transpose(1, 2)
+    z_tm = torch.randn(b, L, 2 * d, **f)[..., d:].transpose(1, 2)
+    dl = torch.randn(b, d, L, **f) * 0.5 - 3.0
+    A = -torch.exp(torch.randn(d, 16, **f) * 0.5)
+    B, C = torch.randn(b, 16, L, **f), torch.randn(b, 16, L, **f)
+    D, bias = torch.randn(d, **f), torch.rand(d, **f) - 0.5
+    kw = dict(D=D, delta_bias=bias, delta_softplus=True, return_last_state=True, reverse=rev)
+    got, last = arm_scan.selective_scan_time_major(u_tm, dl, A, B, C, z=z_tm, **kw)
+    want, wlast = arm_scan.selective_scan(u_tm.contiguous(), dl, A, B, C, z=z_tm.contiguous(),
+                                          **kw)
+    assert torch.equal(got, want) and torch.equal(last, wlast)
+
+
+@pytest.mark.parametrize("width,dim,length", [(4, 96, 300), (1, 30, 5), (8, 64, 3),
+                                              (3, 130, 129), (2, 1536, 2048)])
+def test_causal_conv1d_time_major_out(width, dim, length):
+    """The convolution written as (b, L, D) storage, returned as a (b, D, L) view, has
+    the bits of the contiguous output (itself checked against numpy above): a partial
+    channel tile (96, 130), channels not in 16-byte pieces (30, 130), lengths shorter
+    than the filter and than one tile."""
+    import torch
+
+    import armhackathon_amd as arm_scan
+
+    case(f"causal conv1d time-major out K{width} D{dim} L{length}")
+    g = torch.Generator(device="cuda").manual_seed(6 + width)
+    store = torch.randn(2, length, 2 * dim, device="cuda", generator=g)
+    x = store[..., :dim].transpose(1, 2)
+    w = torch.randn(dim, width, device="cuda", generator=g)
+    bias = torch.randn(dim, device="cuda", generator=g)
+    for act in ("silu", None):
+        a = arm_scan.causal_conv1d(x, w, bias, activation=act)
+        t = arm_scan.causal_conv1d(x, w, bias, activation=act, time_major=True)
+        assert t.stride() == (length * dim, 1, dim) and a.is_contiguous()
+        assert torch.equal(a, t)
