@@ -51,6 +51,7 @@ struct M1Kern {
   unsigned u_bytes;
   int u_strided;
   int z_dma;  // strided z and out staged through LDS (m1_tile_kernel<.., 2>)
+  int u_dma;  // with z_dma: strided u (unit channel stride) through the same stage
   // Rows cut into `segs` segments of `seg_chunks` chunks when there are too few rows
   // to fill the chip: segmap[row][s][n] = (A, B), the affine map of segment s < segs-1
   // (h_end = A h_start + B), from m1_seg_fold_kernel. segs <= 1: whole rows.
@@ -692,7 +693,9 @@ __device__ __forceinline__ void tile_rows(const M1Kern& p, long long blk, int se
   auto z_stage = [&](long long c) {
     issue_z_stage<REV>(zbuf, p.z + bib * p.zs_b, p.zs_t, L, c * CH, d0, wave, lane);
   };
-  if (SIO == 2 && p.z && ce > cb) z_stage(cb);
+  // u through the stage too: per chunk, u's DMA, its read, then z's DMA
+  const bool ustage = SIO == 2 && p.u_dma;
+  if (SIO == 2 && p.z && ce > cb && !ustage) z_stage(cb);
 
   long long k = 0;  // tile counter
   for (long long c = cb; c < ce; ++c) {
@@ -702,7 +705,18 @@ __device__ __forceinline__ void tile_rows(const M1Kern& p, long long blk, int se
     {
       float dd[I], uu[I];
       load_block<I, REV, true>(drow, L, sb, 0.0f, dd, L);
-      if (ustr) {
+      if (ustage) {
+        if constexpr (SIO == 2) {
+          // the block's 16 channels of u, 64-byte runs, land with delta's loads; the
+          // stage is free (the previous chunk's outputs have left it) and z's DMA
+          // follows once every lane has read its u
+          issue_z_stage<REV>(zbuf, p.u + bib * p.us_b, p.us_t, L, c * CH, d0, wave, lane);
+          tile_sync();
+          read_z_stage(zbuf, j, wave, rw, uu);
+          lds_barrier();
+          if (p.z) z_stage(c);
+        }
+      } else if (ustr) {
         const long long tlo = REV ? L - sb - I : sb;  // the block's lowest memory step
         load_block_strided<I, REV>(slab_rsrc(p.u + bib * p.us_b, p.u_bytes),
                                    (unsigned)((d * p.us_d + tlo * p.us_t) * 4), p.us_t, uu);
@@ -757,7 +771,7 @@ __device__ __forceinline__ void tile_rows(const M1Kern& p, long long blk, int se
       lds_barrier();
       store_out_stage<REV>(zbuf, p.out + bib * p.os_b, p.os_t, L, c * CH, d0, wave, lane);
       lds_barrier();  // every lane has read its outputs before the next z stage lands
-      if (p.z && c + 1 < ce) z_stage(c + 1);
+      if (p.z && c + 1 < ce && !ustage) z_stage(c + 1);
     } else {
       store_out(sb, y);
     }
@@ -1114,6 +1128,8 @@ hipError_t m1_scan_chunked(const M1Problem& pr, hipStream_t st) {
       k.u_strided = 1;
       k.us_b = pr.u_stride[0]; k.us_d = pr.u_stride[1]; k.us_t = pr.u_stride[2];
       k.u_bytes = (unsigned)slab_bytes(pr.u_stride, pr);
+      k.u_dma = k.z_dma && k.us_d == 1 && k.us_t % 4 == 0 && k.us_b % 4 == 0 &&
+                aligned16(pr.u);
     }
     return k.z_dma ? run_tile<2>(k, rev, st) : run_tile<1>(k, rev, st);
   }

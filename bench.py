@@ -139,6 +139,8 @@ def config_inputs(name, dev):
         proj = torch.empty((b, L, 2 * d), device=dev)  # the mixer's in_proj output
         proj[..., d:] = t["z"].transpose(1, 2)
         t["z"] = proj.transpose(1, 2)[:, d:]
+        # u: the causal convolution's output, stored (b, L, D) for the mixer's x_proj
+        t["u"] = t["u"].transpose(1, 2).contiguous().transpose(1, 2)
         return t, workloads.m1_bytes(b, d, L, n, z=True, D=True, bias=True, last_state=True)
     if name in ("m3_siso_angles", "m3_mimo_angles"):
         base = workloads.m3_siso(seed=3) if name == "m3_siso_angles" else \
@@ -180,8 +182,8 @@ CONFIG_NAMES = {
     "m1_b1": "config 1: Mamba-1 selective_scan B1 D1536 L2048 N16, z and D, final state "
              "(8 input sets rotated: one set fits in the 256 MB MALL)",
     "m1_seam": "config 2 scan at the Hugging Face seam: B8 D1536 L2048 N16, bias+softplus, "
-               "D, z read in place from the mixer's (b, L, 2D) projection, out written "
-               "time-major",
+               "D, z read in place from the mixer's (b, L, 2D) projection, u from the "
+               "convolution's (b, L, D) output, out written time-major",
     "m3_siso": "config 3: Mamba-3 SISO B4 L4096 24 heads x 64, dqk 128 (final states too)",
     "m3_siso_angles": "config 3 from raw angles (b, l, h, 32): the angle pre-pass fused",
     "m3_mimo_angles": "config 4 from raw angles (b, l, h, 32): the angle pre-pass fused",

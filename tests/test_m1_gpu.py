@@ -450,18 +450,22 @@ def test_causal_conv1d_update_token_by_token(width):
 
 
 @pytest.mark.parametrize("shape", [(2, 64, 512, False), (1, 32, 300, False), (2, 64, 512, True),
-                                   (8, 1536, 2048, False)],
+                                   (8, 1024, 512, True), (8, 1536, 2048, False)],
                          ids=lambda s: "x".join(map(str, s)))
-def test_time_major_u(shape):
-    """u, z and out all views of time-major storage (the HF mixer's convolution output
-    laid out for its x_proj): bit-identical to the contiguous call. Few rows take the
-    segmented scan (its fold reads u by strides too); L = 300 has a tail chunk."""
+@pytest.mark.parametrize("gate", [True, False], ids=["z", "noz"])
+@pytest.mark.parametrize("utm", [True, False], ids=["utm", "ucont"])
+def test_time_major_u(shape, gate, utm):
+    """z and out views of time-major storage, and u one too (the HF mixer's convolution
+    output laid out for its x_proj) or contiguous: bit-identical to the contiguous
+    call. Time-major u goes through the block's LDS stage, with z or without it. Few
+    rows take the segmented scan (its fold reads u by strides too); L = 300 has a tail
+    chunk."""
     import torch
 
     import armhackathon_amd as arm_scan
 
     b, d, L, rev = shape
-    case(f"time-major u {shape}")
+    case(f"time-major inputs {shape} gate={gate} u tm={utm}")
     g = torch.Generator(device="cuda").manual_seed(5)
     f = dict(device="cuda", generator=g)
     u_tm = torch.randn(b, L, d, **f).transpose(1, 2)
@@ -471,9 +475,12 @@ def test_time_major_u(shape):
     B, C = torch.randn(b, 16, L, **f), torch.randn(b, 16, L, **f)
     D, bias = torch.randn(d, **f), torch.rand(d, **f) - 0.5
     kw = dict(D=D, delta_bias=bias, delta_softplus=True, return_last_state=True, reverse=rev)
-    got, last = arm_scan.selective_scan_time_major(u_tm, dl, A, B, C, z=z_tm, **kw)
-    want, wlast = arm_scan.selective_scan(u_tm.contiguous(), dl, A, B, C, z=z_tm.contiguous(),
-                                          **kw)
+    if not gate:
+        z_tm = None
+    u_in = u_tm if utm else u_tm.contiguous()
+    got, last = arm_scan.selective_scan_time_major(u_in, dl, A, B, C, z=z_tm, **kw)
+    want, wlast = arm_scan.selective_scan(u_tm.contiguous(), dl, A, B, C,
+                                          z=None if z_tm is None else z_tm.contiguous(), **kw)
     assert torch.equal(got, want) and torch.equal(last, wlast)
 
 
