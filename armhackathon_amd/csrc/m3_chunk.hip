@@ -78,6 +78,7 @@ struct M3K {
   int heads, dv, dqk, len, groups, nparts, nchunks, steps_per_chunk, nseq;
   int out_tm;  // out (b, l, h, dv) instead of (b, h, l, dv)
   int ptiles, nstages;
+  int zown;  // z's step stride differs from v's (m3_chunk_kernel<.., ZOWN>)
   // DMA instructions (1 KB each) per stage: q and k take one per n-tile
   int n_cs, n_v, n_z;  // cos (and again sin), v, z
   int n_ins;           // all sections, + 2 for the gate record
@@ -413,7 +414,12 @@ struct Stash {
 // Waves 0 .. WN-1 compute the partials of n-tile `wave` for every slice of the
 // block; waves WN .. WN+PT-1 finish slice wave-WN of the previous chunk. Both kinds
 // pass one barrier per chunk.
-template <int R, bool MIMO, bool REV, int PT, bool ANG>
+// ACC: an accumulating traversal (p.accum; SISO without angles), a template parameter
+// so that the other kernels carry none of its epilogue work. ZOWN: z's step stride
+// differs from v's; otherwise z's DMA pieces share v's per-chunk step, one scalar
+// fewer per piece in a kernel whose scalar registers already spill (measured 6%
+// slower at config 3 with the two strides kept apart).
+template <int R, bool MIMO, bool REV, int PT, bool ANG, bool ACC = false, bool ZOWN = false>
 __global__ void __launch_bounds__(64 * (kMaxWaves + 2)) m3_chunk_kernel(M3K p) {
   extern __shared__ __attribute__((aligned(16))) float sm[];
   const int WN = p.dqk / 16;
@@ -464,7 +470,7 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 2)) m3_chunk_kernel(M3K p) {
 
   if (ewave) {
     // ================= epilogue wave: slice ej =================
-    const float dskip = p.D && !p.accum ? p.D[h] : 0.0f;
+    const float dskip = p.D && !ACC ? p.D[h] : 0.0f;
     const int pcol = p0 + ej * 16 + li;
     float psi[4], zeta[4], phi[4];
 #pragma unroll
@@ -482,13 +488,13 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 2)) m3_chunk_kernel(M3K p) {
                                 : (((long long)bi * H + h) * L + t0) * dv);
     Stash st = {};
     auto epilogue = [&](int ch) {
-      float* orow = out_lane + (REV ? -(long long)ch : (long long)ch) * T * ostep;
       // the other traversal's output, under accumulation (loaded first, used last)
       float prev[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-      if (p.accum) {
+      if constexpr (ACC) {
+        const float* prow = out_lane + (REV ? -(long long)ch : (long long)ch) * T * ostep;
 #pragma unroll
         for (int r = 0; r < 4; r += R)
-          if (ch * T + (4 * lj + r) / R < L) prev[r] = orow[(REV ? -(r / R) : r / R) * ostep];
+          if (ch * T + (4 * lj + r) / R < L) prev[r] = prow[(REV ? -(r / R) : r / R) * ostep];
       }
       const float* gb = gbuf + (ch & 1) * kMaxWaves * 256;
       const float* yb = ybuf + ((ch & 1) * PT + ej) * kMaxWaves * 256;
@@ -509,6 +515,7 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 2)) m3_chunk_kernel(M3K p) {
       f4 Y = ys[0] * st.ec;  // lane holds Y[row = 4lj + r][p], the inter-chunk part
 #pragma unroll
       for (int m = 0; m < 4; ++m) Y = mfma(G[m], st.x[m], Y);
+      float* orow = out_lane + (REV ? -(long long)ch : (long long)ch) * T * ostep;
 #pragma unroll
       for (int r = 0; r < 4; r += R) {
         if (ch * T + (4 * lj + r) / R < L) {
@@ -557,7 +564,7 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 2)) m3_chunk_kernel(M3K p) {
   in.csstride = H * half;
   in.angstride = p.at;
   in.vstride = p.vt;
-  in.zstride = p.zt;
+  in.zstride = ZOWN ? p.zt : p.vt;
 
   // biases of the lane's columns (row li has rank li % R)
   f4 bq, bk, bqp = {0.0f, 0.0f, 0.0f, 0.0f}, bkp = bqp;
@@ -724,29 +731,43 @@ size_t chunk_lds_bytes(const M3K& k, int pt, int ns) {
                           (size_t)2 * pt * kMaxWaves * 256 + (size_t)WN * 16 * kKtStride);
 }
 
-template <int R, bool MIMO, int PT>
+template <int R, bool MIMO, int PT, bool ZOWN>
 hipError_t launch_chunk(const M3K& k, bool rev, hipStream_t st) {
   const int WN = k.dqk / 16;
   const long long blocks = 8LL * (k.nparts / PT) * ((k.nseq + 7) / 8);
   const size_t lds = chunk_lds_bytes(k, PT, k.nstages);
   if (k.ang) {  // forward only: theta is a forward cumsum
     if (rev) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((m3_chunk_kernel<R, MIMO, false, PT, true>), dim3((unsigned)blocks),
-                       dim3(64 * (WN + PT)), lds, st, k);
+    hipLaunchKernelGGL((m3_chunk_kernel<R, MIMO, false, PT, true, false, ZOWN>),
+                       dim3((unsigned)blocks), dim3(64 * (WN + PT)), lds, st, k);
+  } else if (k.accum) {
+    if constexpr (R == 1 && !MIMO) {
+      if (rev)
+        hipLaunchKernelGGL((m3_chunk_kernel<1, false, true, PT, false, true, ZOWN>),
+                           dim3((unsigned)blocks), dim3(64 * (WN + PT)), lds, st, k);
+      else
+        hipLaunchKernelGGL((m3_chunk_kernel<1, false, false, PT, false, true, ZOWN>),
+                           dim3((unsigned)blocks), dim3(64 * (WN + PT)), lds, st, k);
+    } else {
+      return hipErrorInvalidValue;  // accumulation is SISO only (m3_scan checks it)
+    }
   } else if (rev) {
-    hipLaunchKernelGGL((m3_chunk_kernel<R, MIMO, true, PT, false>), dim3((unsigned)blocks),
-                       dim3(64 * (WN + PT)), lds, st, k);
+    hipLaunchKernelGGL((m3_chunk_kernel<R, MIMO, true, PT, false, false, ZOWN>),
+                       dim3((unsigned)blocks), dim3(64 * (WN + PT)), lds, st, k);
   } else {
-    hipLaunchKernelGGL((m3_chunk_kernel<R, MIMO, false, PT, false>), dim3((unsigned)blocks),
-                       dim3(64 * (WN + PT)), lds, st, k);
+    hipLaunchKernelGGL((m3_chunk_kernel<R, MIMO, false, PT, false, false, ZOWN>),
+                       dim3((unsigned)blocks), dim3(64 * (WN + PT)), lds, st, k);
   }
   return hipGetLastError();
 }
 
 template <int R, bool MIMO>
 hipError_t launch_chunk_pt(const M3K& k, bool rev, hipStream_t st) {
-  return k.ptiles == 2 ? launch_chunk<R, MIMO, 2>(k, rev, st)
-                       : launch_chunk<R, MIMO, 1>(k, rev, st);
+  if (k.zown)
+    return k.ptiles == 2 ? launch_chunk<R, MIMO, 2, true>(k, rev, st)
+                         : launch_chunk<R, MIMO, 1, true>(k, rev, st);
+  return k.ptiles == 2 ? launch_chunk<R, MIMO, 2, false>(k, rev, st)
+                       : launch_chunk<R, MIMO, 1, false>(k, rev, st);
 }
 
 }  // namespace
@@ -788,6 +809,7 @@ hipError_t m3_scan_chunked(const M3Problem& pr, hipStream_t st) {
   k.nang = (int)pr.n_angles;
   k.vb = pr.v_strides[0]; k.vt = (int)pr.v_strides[1];
   k.zb = pr.z_strides[0]; k.zt = (int)pr.z_strides[1];
+  k.zown = pr.z != nullptr && k.zt != k.vt;
   k.ab = pr.ang_strides[0]; k.at = (int)pr.ang_strides[1]; k.ah = pr.ang_strides[2];
   k.rec_floats = pr.angles ? kRecFloatsAng : kRecFloats;
   auto plan = [&]() {

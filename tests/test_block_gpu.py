@@ -132,7 +132,8 @@ def test_public_scan_reads_views_in_place(mimo):
     """arm_scan.mamba3_scan / mamba3_mimo_scan handed the reference block's views (x
     and z slices of one projection, angles expanded over heads) read them in place
     (arm_scan_mamba3_scan_strided_f32) and give the bits of the contiguous call; a
-    layout the strided entry cannot read (heads not dv apart) is copied instead."""
+    layout the strided entry cannot read (heads not dv apart) is copied instead. x and
+    z with different step strides take the kernel's separate z stride."""
     import torch
 
     import armhackathon_amd as arm_scan
@@ -171,6 +172,9 @@ def test_public_scan_reads_views_in_place(mimo):
     # heads not dv apart: the copy route, same bits
     xt = x.transpose(1, 2).contiguous().transpose(1, 2)
     assert torch.equal(run(xt, z, ang), want)
+    # x and z a step apart by different strides (the kernel's separate z stride)
+    assert torch.equal(run(x, z.contiguous(), ang), want)
+    assert torch.equal(run(x.contiguous(), z, ang), want)
     assert kernel_calls() > 0
 
 
