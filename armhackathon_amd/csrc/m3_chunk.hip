@@ -41,6 +41,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <type_traits>
 
 #include "scan_common.h"
 #include "scan_launch.h"
@@ -264,24 +265,30 @@ __device__ __forceinline__ void dma16(const float* src, float* lds) {
 
 // The DMA instructions of one wave, resolved once. For a chunk wholly inside the
 // sequence the lane's source is base[k] + ch * delta[k] + off[k] (floats; base and
-// delta are wave-uniform); the last, partial chunk goes through dma_clamped.
+// delta are wave-uniform); the last, partial chunk goes through dma_clamped. A plan
+// holds MD instructions: kNarrowDma when a stage needs no more than that per partial
+// wave (dqk 128 at configs 3 and 4), else kMaxDma. The plan's scalars stay live
+// through the chunk loop, in a kernel whose scalar registers spill: the narrow plan
+// spills 222 SGPRs instead of 588 and runs configs 3 and 4 about 4% faster.
 constexpr int kMaxDma = 8;
+constexpr int kNarrowDma = 4;
+template <int MD>
 struct DmaPlan {
-  const float* base[kMaxDma];
-  int delta[kMaxDma];
-  int off[kMaxDma];
-  bool on[kMaxDma];
-  int ins[kMaxDma];
+  const float* base[MD];
+  int delta[MD];
+  int off[MD];
+  bool on[MD];
+  int ins[MD];
   int count;
 };
 
-template <int R, bool REV>
+template <int R, bool REV, int MD>
 __device__ __forceinline__ void dma_plan(const M3K& p, const SeqIn& s, int first, int step_ins,
-                                         int lane, DmaPlan& d) {
+                                         int lane, DmaPlan<MD>& d) {
   const int T = p.steps_per_chunk, L = p.len;
   d.count = 0;
 #pragma unroll
-  for (int k = 0; k < kMaxDma; ++k) {
+  for (int k = 0; k < MD; ++k) {
     const int ins = first + k * step_ins;
     d.ins[k] = ins;
     d.on[k] = false;
@@ -311,21 +318,22 @@ __device__ __forceinline__ void dma_plan(const M3K& p, const SeqIn& s, int first
 
 // Instructions k0 .. k1-1 of the plan (a wave spreads a stage over its iteration so
 // that the block's DMA does not reach the address unit in one burst).
-__device__ __forceinline__ void dma_fast(const DmaPlan& d, int ch, float* stage, int k0 = 0,
-                                         int k1 = kMaxDma) {
+template <int MD>
+__device__ __forceinline__ void dma_fast(const DmaPlan<MD>& d, int ch, float* stage, int k0 = 0,
+                                         int k1 = MD) {
 #pragma unroll
-  for (int k = 0; k < kMaxDma; ++k)
+  for (int k = 0; k < MD; ++k)
     if (k >= k0 && k < k1 && k < d.count && d.on[k])
       dma16(d.base[k] + ((long long)ch * d.delta[k] + d.off[k]), stage + d.ins[k] * 256);
 }
 
 // Any chunk, with the rows past the end clamped to the last step.
-template <int R, bool REV>
-__device__ __forceinline__ void dma_clamped(const M3K& p, const SeqIn& s, const DmaPlan& d,
+template <int R, bool REV, int MD>
+__device__ __forceinline__ void dma_clamped(const M3K& p, const SeqIn& s, const DmaPlan<MD>& d,
                                             int ch, float* stage, int lane) {
   const int T = p.steps_per_chunk, L = p.len;
 #pragma unroll
-  for (int k = 0; k < kMaxDma; ++k) {
+  for (int k = 0; k < MD; ++k) {
     if (k >= d.count) break;
     const DmaPiece pc = dma_decode<R>(p, s, d.ins[k], lane);
     if (!pc.on) continue;
@@ -338,17 +346,18 @@ __device__ __forceinline__ void dma_clamped(const M3K& p, const SeqIn& s, const 
   }
 }
 
-template <int R, bool REV>
-__device__ __forceinline__ void dma_stage(const M3K& p, const SeqIn& s, const DmaPlan& d, int ch,
-                                          float* stage, int lane) {
+template <int R, bool REV, int MD>
+__device__ __forceinline__ void dma_stage(const M3K& p, const SeqIn& s, const DmaPlan<MD>& d,
+                                          int ch, float* stage, int lane) {
   if ((ch + 1) * p.steps_per_chunk <= p.len) dma_fast(d, ch, stage);
   else dma_clamped<R, REV>(p, s, d, ch, stage, lane);
 }
 
 // Part k0 .. k1-1 of dma_stage; the partial, last chunk goes whole with part 0.
-template <int R, bool REV>
-__device__ __forceinline__ void dma_stage_part(const M3K& p, const SeqIn& s, const DmaPlan& d,
-                                               int ch, float* stage, int lane, int k0, int k1) {
+template <int R, bool REV, int MD>
+__device__ __forceinline__ void dma_stage_part(const M3K& p, const SeqIn& s,
+                                               const DmaPlan<MD>& d, int ch, float* stage,
+                                               int lane, int k0, int k1) {
   if ((ch + 1) * p.steps_per_chunk <= p.len) dma_fast(d, ch, stage, k0, k1);
   else if (k0 == 0) dma_clamped<R, REV>(p, s, d, ch, stage, lane);
 }
@@ -419,7 +428,8 @@ struct Stash {
 // differs from v's; otherwise z's DMA pieces share v's per-chunk step, one scalar
 // fewer per piece in a kernel whose scalar registers already spill (measured 6%
 // slower at config 3 with the two strides kept apart).
-template <int R, bool MIMO, bool REV, int PT, bool ANG, bool ACC = false, bool ZOWN = false>
+template <int R, bool MIMO, bool REV, int PT, bool ANG, bool ACC = false, bool ZOWN = false,
+          int MD = kMaxDma>
 __global__ void __launch_bounds__(64 * (kMaxWaves + 2)) m3_chunk_kernel(M3K p) {
   extern __shared__ __attribute__((aligned(16))) float sm[];
   const int WN = p.dqk / 16;
@@ -588,10 +598,10 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 2)) m3_chunk_kernel(M3K p) {
 
   // The DMA instructions of this wave; the partial waves issue no other vector
   // memory operation inside the loop.
-  DmaPlan dp;
+  DmaPlan<MD> dp;
   dma_plan<R, REV>(p, in, nt, WN, lane, dp);
   for (int c = 0; c < NS - 1 && c < p.nchunks; ++c)
-    dma_stage<R, REV>(p, in, dp, c, stages + c * p.stage_floats, lane);
+    dma_stage<R, REV, MD>(p, in, dp, c, stages + c * p.stage_floats, lane);
 
   f4 S[PT];
 #pragma unroll
@@ -609,7 +619,7 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 2)) m3_chunk_kernel(M3K p) {
     // this iteration's DMA, one instruction per phase
     const bool dma_now = ch + NS - 1 < p.nchunks;
     float* dstage = stages + ((ch + NS - 1) % NS) * p.stage_floats;
-    if (dma_now) dma_stage_part<R, REV>(p, in, dp, ch + NS - 1, dstage, lane, 0, 1);
+    if (dma_now) dma_stage_part<R, REV, MD>(p, in, dp, ch + NS - 1, dstage, lane, 0, 1);
 
     const float* sg = stages + (ch % NS) * p.stage_floats;
     // ---- rotated q/k rows of this n-tile
@@ -669,7 +679,7 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 2)) m3_chunk_kernel(M3K p) {
     const f4 qr = rope<MIMO>(q, qp, bq, bqp, cs, sn, lo);
     const f4 kr = rope<MIMO>(k, kp, bk, bkp, cs, sn, lo);
     kr_last = kr;
-    if (dma_now) dma_stage_part<R, REV>(p, in, dp, ch + NS - 1, dstage, lane, 1, 2);
+    if (dma_now) dma_stage_part<R, REV, MD>(p, in, dp, ch + NS - 1, dstage, lane, 1, 2);
     // ---- partial G^T, and partial Q S0^T per slice
     {
       f4 gp = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -677,7 +687,7 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 2)) m3_chunk_kernel(M3K p) {
       for (int r = 0; r < 4; ++r) gp = mfma(kr[r], qr[r], gp);
       *reinterpret_cast<f4*>(gbuf + (ch & 1) * kMaxWaves * 256 + (nt * 64 + lane) * 4) = gp;
     }
-    if (dma_now) dma_stage_part<R, REV>(p, in, dp, ch + NS - 1, dstage, lane, 2, 3);
+    if (dma_now) dma_stage_part<R, REV, MD>(p, in, dp, ch + NS - 1, dstage, lane, 2, 3);
 #pragma unroll
     for (int j = 0; j < PT; ++j) {
       f4 yp = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -686,7 +696,7 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 2)) m3_chunk_kernel(M3K p) {
       *reinterpret_cast<f4*>(ybuf + (((ch & 1) * PT + j) * kMaxWaves + nt) * 256 + lane * 4) =
           yp;
     }
-    if (dma_now) dma_stage_part<R, REV>(p, in, dp, ch + NS - 1, dstage, lane, 3, 4);
+    if (dma_now) dma_stage_part<R, REV, MD>(p, in, dp, ch + NS - 1, dstage, lane, 3, 4);
     // ---- K transpose, then S = e^{c_last} S + K^T diag(w) X per slice
     *reinterpret_cast<f4*>(kt + li * kKtStride + 4 * lj) = kr;
     float kc[4];
@@ -704,7 +714,7 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 2)) m3_chunk_kernel(M3K p) {
       }
       S[j] = acc;
     }
-    if (dma_now) dma_stage_part<R, REV>(p, in, dp, ch + NS - 1, dstage, lane, 4, kMaxDma);
+    if (dma_now) dma_stage_part<R, REV, MD>(p, in, dp, ch + NS - 1, dstage, lane, 4, MD);
   }
   lds_barrier();
 
@@ -731,31 +741,31 @@ size_t chunk_lds_bytes(const M3K& k, int pt, int ns) {
                           (size_t)2 * pt * kMaxWaves * 256 + (size_t)WN * 16 * kKtStride);
 }
 
-template <int R, bool MIMO, int PT, bool ZOWN>
+template <int R, bool MIMO, int PT, bool ZOWN, int MD>
 hipError_t launch_chunk(const M3K& k, bool rev, hipStream_t st) {
   const int WN = k.dqk / 16;
   const long long blocks = 8LL * (k.nparts / PT) * ((k.nseq + 7) / 8);
   const size_t lds = chunk_lds_bytes(k, PT, k.nstages);
   if (k.ang) {  // forward only: theta is a forward cumsum
     if (rev) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((m3_chunk_kernel<R, MIMO, false, PT, true, false, ZOWN>),
+    hipLaunchKernelGGL((m3_chunk_kernel<R, MIMO, false, PT, true, false, ZOWN, MD>),
                        dim3((unsigned)blocks), dim3(64 * (WN + PT)), lds, st, k);
   } else if (k.accum) {
     if constexpr (R == 1 && !MIMO) {
       if (rev)
-        hipLaunchKernelGGL((m3_chunk_kernel<1, false, true, PT, false, true, ZOWN>),
+        hipLaunchKernelGGL((m3_chunk_kernel<1, false, true, PT, false, true, ZOWN, MD>),
                            dim3((unsigned)blocks), dim3(64 * (WN + PT)), lds, st, k);
       else
-        hipLaunchKernelGGL((m3_chunk_kernel<1, false, false, PT, false, true, ZOWN>),
+        hipLaunchKernelGGL((m3_chunk_kernel<1, false, false, PT, false, true, ZOWN, MD>),
                            dim3((unsigned)blocks), dim3(64 * (WN + PT)), lds, st, k);
     } else {
       return hipErrorInvalidValue;  // accumulation is SISO only (m3_scan checks it)
     }
   } else if (rev) {
-    hipLaunchKernelGGL((m3_chunk_kernel<R, MIMO, true, PT, false, false, ZOWN>),
+    hipLaunchKernelGGL((m3_chunk_kernel<R, MIMO, true, PT, false, false, ZOWN, MD>),
                        dim3((unsigned)blocks), dim3(64 * (WN + PT)), lds, st, k);
   } else {
-    hipLaunchKernelGGL((m3_chunk_kernel<R, MIMO, false, PT, false, false, ZOWN>),
+    hipLaunchKernelGGL((m3_chunk_kernel<R, MIMO, false, PT, false, false, ZOWN, MD>),
                        dim3((unsigned)blocks), dim3(64 * (WN + PT)), lds, st, k);
   }
   return hipGetLastError();
@@ -763,11 +773,19 @@ hipError_t launch_chunk(const M3K& k, bool rev, hipStream_t st) {
 
 template <int R, bool MIMO>
 hipError_t launch_chunk_pt(const M3K& k, bool rev, hipStream_t st) {
-  if (k.zown)
-    return k.ptiles == 2 ? launch_chunk<R, MIMO, 2, true>(k, rev, st)
-                         : launch_chunk<R, MIMO, 1, true>(k, rev, st);
-  return k.ptiles == 2 ? launch_chunk<R, MIMO, 2, false>(k, rev, st)
-                       : launch_chunk<R, MIMO, 1, false>(k, rev, st);
+  const bool narrow = k.n_ins <= kNarrowDma * (k.dqk / 16);
+  auto go = [&](auto zown, auto md) {
+    constexpr bool Z = decltype(zown)::value;
+    constexpr int M = decltype(md)::value;
+    return k.ptiles == 2 ? launch_chunk<R, MIMO, 2, Z, M>(k, rev, st)
+                         : launch_chunk<R, MIMO, 1, Z, M>(k, rev, st);
+  };
+  using T = std::true_type;
+  using F = std::false_type;
+  using Nd = std::integral_constant<int, kNarrowDma>;
+  using Wd = std::integral_constant<int, kMaxDma>;
+  if (k.zown) return narrow ? go(T{}, Nd{}) : go(T{}, Wd{});
+  return narrow ? go(F{}, Nd{}) : go(F{}, Wd{});
 }
 
 }  // namespace
