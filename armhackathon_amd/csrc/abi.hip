@@ -142,10 +142,14 @@ int arm_scan_selective_scan_strided_f32(const ArmScanDims* dims, const float* u,
   p.u = u; p.delta = delta; p.A = a; p.B = b; p.C = c; p.D = d_skip; p.z = z;
   p.bias = delta_bias; p.h0 = h0; p.out = out; p.last = last_state;
   p.softplus = delta_softplus != 0; p.reverse = reverse != 0;
+  // a null stride array is the contiguous (batch, dim, len) layout; given strides are
+  // taken as they are (a 0 is a broadcast view, read in place)
+  const long long cont[3] = {(long long)(dims->dim * dims->len), (long long)dims->len, 1};
+  p.has_strides = 1;
   for (int i = 0; i < 3; ++i) {
-    p.z_stride[i] = z_strides ? z_strides[i] : 0;
-    p.out_stride[i] = out_strides ? out_strides[i] : 0;
-    p.u_stride[i] = u_strides ? u_strides[i] : 0;
+    p.z_stride[i] = z_strides ? z_strides[i] : cont[i];
+    p.out_stride[i] = out_strides ? out_strides[i] : cont[i];
+    p.u_stride[i] = u_strides ? u_strides[i] : cont[i];
   }
   const char* why = nullptr;
   if (armscan::m1_strided_io(p) && !armscan::m1_strided_supported(p, &why))
@@ -260,6 +264,7 @@ static int mamba3_call(const ArmMamba3Dims* dims, const float* q, const float* k
   p.accumulate = accumulate ? 1 : 0;
   if (accumulate && (mimo || d.rank != 1))
     return fail(ARM_SCAN_ERR_INVALID_DIMS, "the non-causal sum is SISO (rank 1)");
+  armscan::m3_contiguous_strides(p);  // then the caller's strides, as given
   for (int i = 0; i < 3; ++i) {
     if ((i < 2 && v_strides && v_strides[i] < 0) || (i < 2 && z_strides && z_strides[i] < 0) ||
         (angle_strides && angle_strides[i] < 0))
@@ -268,7 +273,6 @@ static int mamba3_call(const ArmMamba3Dims* dims, const float* q, const float* k
     if (i < 2 && z_strides) p.z_strides[i] = (long long)z_strides[i];
     if (angle_strides) p.ang_strides[i] = (long long)angle_strides[i];
   }
-  armscan::m3_fill_strides(p);
   if (angles) {
     if (!prod_ok({d.batch, d.len, d.heads, n_angles}))
       return fail(ARM_SCAN_ERR_INVALID_DIMS, "dims overflow size_t");
@@ -500,6 +504,7 @@ int arm_scan_ss2d_f32(const ArmSS2DDims* dims, const float* u, const float* delt
   {
     armscan::M1Problem q = p;
     q.u = u; q.delta = delta; q.z = z;
+    q.B = b4; q.C = c4; q.out = out;  // for the alignment check (the planes keep it: L % 4 == 0)
     if (armscan::m1_jobs_supported(q)) {
       // One launch for the four directions. The column directions scan column-major
       // copies of u, delta, z and of their B/C (one batched transpose) and write

@@ -992,7 +992,9 @@ bool aligned16(const void* q) { return q == nullptr || ((uintptr_t)q & 15u) == 0
 }  // namespace
 
 bool m1_jobs_supported(const M1Problem& pr) {
-  return pr.len % 4 == 0 && pr.dim % 16 == 0 && pr.groups == 1 && pr.h0 == nullptr;
+  return pr.len % 4 == 0 && pr.dim % 16 == 0 && pr.groups == 1 && pr.h0 == nullptr &&
+         aligned16(pr.u) && aligned16(pr.delta) && aligned16(pr.z) && aligned16(pr.B) &&
+         aligned16(pr.C) && aligned16(pr.out);
 }
 
 hipError_t m1_scan_jobs(const M1Problem& pr, const M1JobSpec* spec, int n, hipStream_t st) {
@@ -1021,9 +1023,11 @@ hipError_t m1_scan_jobs(const M1Problem& pr, const M1JobSpec* spec, int n, hipSt
 }
 
 namespace {
+// Strides are meaningful only with has_strides (the strided entry point writes the
+// contiguous ones for a null array); without it every tensor is contiguous.
 bool contiguous_strides(const long long (&s)[3], const M1Problem& pr) {
   const long long L = (long long)pr.len, D = (long long)pr.dim;
-  return (s[0] == 0 && s[1] == 0 && s[2] == 0) || (s[0] == D * L && s[1] == L && s[2] == 1);
+  return !pr.has_strides || (s[0] == D * L && s[1] == L && s[2] == 1);
 }
 // bytes of one batch's slab of a strided (batch, dim, len) tensor
 long long slab_bytes(const long long (&s)[3], const M1Problem& pr) {

@@ -16,7 +16,10 @@ struct M1Problem {
   float *out2, *last2;  // bidirectional outputs
   int softplus, reverse;
   int merge;  // bidirectional: write out = fwd + bwd instead of two outputs
-  // element strides (batch, dim, step) of z, out and u; all zero = (dim*len, len, 1)
+  // Element strides (batch, dim, step) of z, out and u, read only when has_strides is
+  // set (the strided entry point, which writes the contiguous (dim*len, len, 1) for a
+  // null stride array). Every value is taken as given: a stride of 0 is a broadcast.
+  int has_strides;
   long long z_stride[3], out_stride[3], u_stride[3];
 };
 
@@ -87,26 +90,19 @@ struct M3Problem {
   int accumulate;
   // Element strides of v and z (batch, step) and of the raw angles (batch, step,
   // head). Within a step the heads of v and z lie dv apart; the angles' head stride
-  // may be 0 (one set shared by every head). All zero = the contiguous layouts;
-  // m3_fill_strides writes those in.
+  // may be 0 (one set shared by every head). m3_contiguous_strides writes the
+  // contiguous layouts; the strided entry point then puts the caller's strides in,
+  // each taken as given (0 is a broadcast).
   long long v_strides[2], z_strides[2], ang_strides[3];
 };
 
-inline void m3_fill_strides(M3Problem& p) {
+inline void m3_contiguous_strides(M3Problem& p) {
   const long long L = (long long)p.len, H = (long long)p.heads;
-  if (p.v_strides[0] == 0 && p.v_strides[1] == 0) {
-    p.v_strides[0] = L * H * (long long)p.dv;
-    p.v_strides[1] = H * (long long)p.dv;
-  }
-  if (p.z_strides[0] == 0 && p.z_strides[1] == 0) {
-    p.z_strides[0] = L * H * (long long)p.dv;
-    p.z_strides[1] = H * (long long)p.dv;
-  }
-  if (p.ang_strides[0] == 0 && p.ang_strides[1] == 0 && p.ang_strides[2] == 0) {
-    p.ang_strides[0] = L * H * (long long)p.n_angles;
-    p.ang_strides[1] = H * (long long)p.n_angles;
-    p.ang_strides[2] = (long long)p.n_angles;
-  }
+  p.v_strides[0] = p.z_strides[0] = L * H * (long long)p.dv;
+  p.v_strides[1] = p.z_strides[1] = H * (long long)p.dv;
+  p.ang_strides[0] = L * H * (long long)p.n_angles;
+  p.ang_strides[1] = H * (long long)p.n_angles;
+  p.ang_strides[2] = (long long)p.n_angles;
 }
 
 // Largest dv * dqk the Mamba-3 kernel holds on chip.

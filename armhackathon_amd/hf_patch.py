@@ -16,10 +16,12 @@ reference leaves to upstream (README.md:320-322). It is patched here as well, wi
 the same fallback rule: the fast path runs the step as one kernel instead of the
 dozen small torch kernels upstream launches per layer and token.
 
-The mixer's depthwise causal convolution (`causal_conv1d_fn`, the step before the
-scan) is patched under the same rule. Upstream's fallback copies the mixer's
-time-major projection contiguous, runs a depthwise conv and then a silu pass; here
-one kernel reads the view in place and fuses the bias and the silu.
+`patch(conv=True)` also routes the mixer's depthwise causal convolution
+(`causal_conv1d_fn`, the step before the scan, and its decode step) under the same
+rule; the default leaves it upstream's, as the reference's patch does. Upstream's
+fallback copies the mixer's time-major projection contiguous, runs a depthwise conv
+and then a silu pass; the kernel reads the view in place and fuses the bias and the
+silu.
 
 The mixer hands the gate z as a (batch, dim, len) view of its time-major
 in_proj output and transposes the scan output back for out_proj. The wrapper
@@ -107,7 +109,7 @@ def _patch_step_fn(modeling_mamba):
     _STATE["orig_step"] = orig
 
 
-def _patch_scan_fn(modeling_mamba):
+def _patch_scan_fn(modeling_mamba, conv):
     orig = modeling_mamba.mamba_selective_scan
 
     def mamba_selective_scan(hidden_states, dt, A, B, C, D=None, z=None,
@@ -142,17 +144,21 @@ def _patch_scan_fn(modeling_mamba):
     if hasattr(modeling_mamba, "mamba_selective_state_update"):
         _patch_step_fn(modeling_mamba)
         done.append("transformers mamba_selective_state_update (decode step)")
-    if hasattr(modeling_mamba, "causal_conv1d_fn"):
+    if conv and hasattr(modeling_mamba, "causal_conv1d_fn"):
         _patch_conv_fn(modeling_mamba)
         done.append("transformers causal_conv1d_fn (the mixer's causal convolution)")
     return done
 
 
-def patch():
-    """Route HF Mamba's selective scan on device tensors through the HIP kernel.
+def patch(conv=False):
+    """Route HF Mamba's selective scan on device tensors through the HIP kernel
+    (and its decode step through the single-step kernel), as the reference's
+    `patch()` routes the scan (python/arm_scan/patch.py:119-180). With
+    `conv=True` the mixer's causal convolution moves to its kernel too.
 
     Returns the list of patched targets ([] if this transformers version has
-    no `mamba_selective_scan` seam). Idempotent.
+    no `mamba_selective_scan` seam). Idempotent: a second call while patched
+    changes nothing (unpatch() first to change `conv`).
     """
     if _STATE["orig"] is not None:
         return ["transformers mamba_selective_scan (already patched)"]
@@ -164,7 +170,7 @@ def patch():
         warnings.warn("armhackathon_amd.patch(): this transformers version has no "
                       "mamba_selective_scan; leaving it unpatched")
         return []
-    return _patch_scan_fn(modeling_mamba)
+    return _patch_scan_fn(modeling_mamba, conv)
 
 
 def unpatch():

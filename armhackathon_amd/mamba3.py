@@ -164,18 +164,23 @@ def _inplace_strides(v, z, angles):
     reference's Mamba-3 block hands the scan exactly such views: x and z are slices of
     its in_proj output and the angles an `expand` over heads
     (apps/mamba3_lm/block.py:150-174)."""
+    def broadcast(t, axes):
+        return any(t.stride(a) == 0 and t.shape[a] > 1 for a in axes)
+
     def vz(t):
         b, length, h, dv = t.shape
         if (dv > 1 and t.stride(3) != 1) or (h > 1 and t.stride(2) != dv):
             return None
+        if broadcast(t, (0, 1)):
+            return None  # broadcast over batch or steps: the contiguous route
         return (t.stride(0), t.stride(1))
 
     sv = vz(v)
     sz = None if z is None else vz(z)
     if sv is None or (z is not None and sz is None):
         return None
-    if angles.shape[3] > 1 and angles.stride(3) != 1:
-        return None
+    if (angles.shape[3] > 1 and angles.stride(3) != 1) or broadcast(angles, (0, 1)):
+        return None  # the head stride alone may be 0 (one set of angles per step)
     return {"v": sv, "z": sz, "angles": (angles.stride(0), angles.stride(1), angles.stride(2))}
 
 

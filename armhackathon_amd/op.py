@@ -154,6 +154,10 @@ def _strided_ok(u, delta, b, c, z, dim, length, groups):
         st = (length * dim, 1, dim) if t is None else t.stride()
         if min(st) < 0 or 4 * ((dim - 1) * st[1] + (length - 1) * st[2] + 1) >= 1 << 32:
             return False
+        # a broadcast view (stride 0 over an axis longer than 1) takes the contiguous
+        # route, which materialises it
+        if t is not None and any(s == 0 and n > 1 for s, n in zip(st, t.shape)):
+            return False
     return True
 
 

@@ -8,6 +8,8 @@ oracle. The distributions are the ones the configurations name:
   m1_op      Mamba-1 selective_scan: u ~ N(0,1); delta = softplus(0.5 N(0,1) - 4)
              (passed with delta_softplus off); A = -[1..N] per channel; B, C ~ N(0,1)
              shared by all channels (groups = 1); D ~ N(0,1); z ~ N(0,1).
+  m1_layer   the bench step (one Mamba-130M prefill layer's scan): m1_op with a raw
+             delta 0.5 N(0,1) - 4 and delta_bias ~ U(-0.5, 0.5), softplus in the scan.
   m3_siso    Mamba-3 SISO: dt = softplus(N(0,1) - 4); trap ~ N(0,1) (pre-sigmoid);
              A_h = -exp(N(0, 0.5)); adt = A_h dt; theta = cumsum_L(U(-pi, pi) dt) per
              rotation pair (float64), cos/sin float32; q, k ~ N(0,1)/sqrt(dqk) per head
@@ -39,6 +41,18 @@ def m1_op(batch=1, dim=1536, length=2048, state=16, seed=0, z=True, D=True):
     out["D"] = rng.standard_normal(dim, dtype=F32) if D else None
     out["z"] = rng.standard_normal((batch, dim, length), dtype=F32) if z else None
     return out
+
+
+def m1_layer(batch=8, dim=1536, length=2048, state=16, seed=0):
+    """One Mamba-130M prefill layer's scan (config 2's scan shape, the bench step):
+    m1_op's u, A, B, C, D, z, with delta the raw dt_proj output 0.5 N(0,1) - 4 and a
+    delta_bias ~ U(-0.5, 0.5), to be scanned with delta_softplus on, as the Hugging
+    Face mixer calls it (modeling_mamba.py: softplus inside the scan)."""
+    x = m1_op(batch=batch, dim=dim, length=length, state=state, seed=seed)
+    rng = np.random.default_rng(seed + 100)
+    x["delta"] = (rng.standard_normal(x["u"].shape, dtype=F32) * F32(0.5) - F32(4.0))
+    x["delta_bias"] = rng.uniform(-0.5, 0.5, dim).astype(F32)
+    return x
 
 
 def _m3_common(rng, batch, length, heads, dqk):

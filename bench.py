@@ -70,17 +70,12 @@ def parse():
 
 
 def scan_inputs(seed, dev):
-    import numpy as np
     import torch
 
     from armhackathon_amd import workloads
 
-    x = workloads.m1_op(seed=seed, **SHAPE)
     # the HF layer passes the raw dt_proj output with its bias and asks for softplus
-    rng = np.random.default_rng(seed + 100)
-    x["delta"] = (rng.standard_normal(x["u"].shape, dtype=np.float32) * np.float32(0.5)
-                  - np.float32(4.0))
-    x["delta_bias"] = rng.uniform(-0.5, 0.5, SHAPE["dim"]).astype(np.float32)
+    x = workloads.m1_layer(seed=seed, **SHAPE)
     return {k: torch.from_numpy(v).to(dev) for k, v in x.items()}
 
 
@@ -369,13 +364,10 @@ def bench_config_cpu(name, seconds):
     configs 1 and 3-5, over a bounded sample of the config (config 1 whole, batch 1 of
     4 for Mamba-3, 2 of 16 for SS2D), repeated until `seconds` of wall time have
     passed."""
-    import numpy as np
-
     import oracle
     from armhackathon_amd import workloads
 
-    threads = min(16, os.cpu_count() or 1)
-    oracle.set_threads(threads)
+    host_oracle()
     K = ("q", "k", "v", "adt", "dt", "trap", "q_bias", "k_bias")
     if name == "m1_b1":
         x = workloads.m1_op(batch=1, dim=1536, length=2048, state=16, seed=100)
@@ -418,19 +410,78 @@ def bench_config_cpu(name, seconds):
             planes, _ = oracle.ss2d(x["u"], x["delta"], x["A"], x["B4"], x["C4"], D=x["D"],
                                     z=x["z"], want_state=True)
             planes.sum(axis=0)
-    reps, t0 = 0, time.perf_counter()
-    while True:
-        call()
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= seconds or reps >= 50:
-            break
-    return dict(value=round(nbytes * reps / el / 1e9, 3), unit="GB/s", cores=threads,
-                kind="port", sample=f"{reps} passes of {sample} in {el:.1f} s, {threads} threads")
+    return cpu_rates(call, nbytes, sample, seconds, 50)
+
+
+def host_oracle():
+    """Build the C++ restatement of the reference's x86 path on this host (g++, the
+    committed oracle/Makefile: -O3 -march=x86-64, no fast-math or contraction, as
+    cargo's portable release build) into a temporary directory, and load it. Once per
+    process; returns the build record."""
+    import tempfile
+
+    import oracle
+
+    if "build" in _HOST:
+        return _HOST["build"]
+    out = Path(tempfile.mkdtemp(prefix="arm_scan_oracle_")) / "libarm_scan_cpu.so"
+    t0 = time.perf_counter()
+    oracle.build(out=out)
+    oracle.use(out)
+    oracle.lib()
+    model = "unknown"
+    try:
+        for ln in Path("/proc/cpuinfo").read_text().splitlines():
+            if ln.startswith("model name"):
+                model = ln.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    _HOST["build"] = dict(built_on_host=True, build_s=round(time.perf_counter() - t0, 1),
+                          compiler="g++ -O3 -march=x86-64 -ffp-contract=off (oracle/Makefile)",
+                          nproc=os.cpu_count(), cpu_model=model)
+    return _HOST["build"]
+
+
+_HOST = {}
+# the box's CPU share for one GPU: all-thread figures use this many (nproc may show more)
+CPU_SHARE = 16
+
+
+def cpu_rates(call, nbytes, sample, seconds, max_reps):
+    """Time `call` (one pass over `nbytes` algorithmic bytes) on all of the host share's
+    threads and on one thread, each until `seconds` of wall time or `max_reps` passes."""
+    import oracle
+
+    def rate(threads, budget):
+        oracle.set_threads(threads)
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            call()
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= budget or reps >= max_reps:
+                return nbytes * reps / el / 1e9, reps, el
+
+    threads = min(CPU_SHARE, os.cpu_count() or 1)
+    v, reps, el = rate(threads, seconds)
+    v1, reps1, el1 = rate(1, seconds / 2)
+    oracle.set_threads(threads)
+    return dict(value=round(v, 3), unit="GB/s", cores=threads, kind="port",
+                sample=f"{reps} passes of {sample} in {el:.1f} s, {threads} threads",
+                one_thread=dict(value=round(v1, 3), unit="GB/s", cores=1,
+                                sample=f"{reps1} passes of {sample} in {el1:.1f} s, 1 thread"),
+                **host_oracle())
 
 
 def bench_prefill(args, dev):
-    """random-init Mamba-130M architecture, batch 8 x 2048."""
+    """random-init Mamba-130M architecture, batch 8 x 2048, fp32.
+    Timed three ways in one process, as the reference reports its patch
+    (bench/results/RESULTS.md:54-58, unpatched vs patched):
+      unpatched   upstream's torch recurrence;
+      patched     patch(): only the scan in the HIP kernel (config 2 as defined);
+      scan_conv   patch(conv=True): the mixer's causal conv in its kernel as well
+                  (an extra outside config 2, labelled as such)."""
     import torch
     from transformers import MambaConfig, MambaForCausalLM
 
@@ -442,26 +493,44 @@ def bench_prefill(args, dev):
     model = MambaForCausalLM(cfg).to(dev).float().eval()
     ids = torch.randint(0, 50280, (8, 2048), device=dev,
                         generator=torch.Generator(device=dev).manual_seed(0))
-    arm_scan.patch()
-    calls0 = arm_scan.stats()["fast_calls"]
-    conv0 = arm_scan.stats()["conv_calls"]
-    with torch.no_grad():
-        for _ in range(1):
-            model(ids, use_cache=False, logits_to_keep=1)
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for _ in range(args.prefill_steps):
-            model(ids, use_cache=False, logits_to_keep=1)
-        torch.cuda.synchronize()
-        dt = (time.perf_counter() - t0) / args.prefill_steps
-    st = arm_scan.stats()
-    arm_scan.unpatch()
-    return dict(tokens_per_s=8 * 2048 / dt, ms_per_forward=dt * 1e3,
-                scan_calls_per_forward=(st["fast_calls"] - calls0) / (1 + args.prefill_steps),
-                conv_calls_per_forward=(st["conv_calls"] - conv0) / (1 + args.prefill_steps),
-                fallback_calls=st["fallback_calls"] + st["conv_fallback_calls"], batch=8,
-                seq_len=2048,
-                logits="last position only (logits_to_keep=1)")
+    tokens = ids.numel()
+
+    def timed(steps):
+        with torch.no_grad():
+            logits = model(ids, use_cache=False, logits_to_keep=1).logits
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                model(ids, use_cache=False, logits_to_keep=1)
+            torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / steps, logits
+
+    t_ref, ref = timed(1)
+    scale = max(1.0, ref.abs().max().item())
+    out = dict(batch=8, seq_len=2048, logits="last position only (logits_to_keep=1)",
+               unpatched_tokens_per_s=tokens / t_ref, unpatched_ms_per_forward=t_ref * 1e3)
+    for conv in (False, True):
+        s0 = arm_scan.stats()
+        arm_scan.patch(conv=conv)
+        try:
+            t, got = timed(args.prefill_steps)
+        finally:
+            arm_scan.unpatch()
+        s1 = arm_scan.stats()
+        n = 1 + args.prefill_steps
+        r = dict(tokens_per_s=tokens / t, ms_per_forward=t * 1e3,
+                 scan_calls_per_forward=(s1["fast_calls"] - s0["fast_calls"]) / n,
+                 conv_calls_per_forward=(s1["conv_calls"] - s0["conv_calls"]) / n,
+                 fallback_calls=(s1["fallback_calls"] - s0["fallback_calls"]
+                                 + s1["conv_fallback_calls"] - s0["conv_fallback_calls"]),
+                 logits_max_abs_diff_over_scale=(got - ref).abs().max().item() / scale)
+        if conv:
+            out["scan_conv"] = dict(r, note="extra, outside config 2: patch(conv=True) also "
+                                            "runs the mixer's causal conv in its HIP kernel")
+        else:
+            out.update(r)
+            out["speedup_vs_unpatched"] = t_ref / t
+    return out
 
 
 def bench_decode(dev, new_tokens=64, prompt=128):
@@ -501,7 +570,7 @@ def bench_decode(dev, new_tokens=64, prompt=128):
 
     r = {"batch": 1, "prompt": prompt, "new_tokens": new_tokens}
     r["unpatched_ms_per_token"], ref = ms_per_token()
-    arm_scan.patch()
+    arm_scan.patch(conv=True)
     try:
         step = modeling_mamba.mamba_selective_state_update
         conv_step = modeling_mamba.causal_conv1d_update
@@ -521,34 +590,22 @@ def bench_cpu(seconds):
     """The C++ restatement of the reference's x86 scalar path on host cores,
     over a bounded sample: the same layer scan restricted to a slice of
     channels, repeated until `seconds` of CPU time have passed."""
-    import numpy as np
-
     import oracle
     from armhackathon_amd import workloads
 
-    threads = min(16, os.cpu_count() or 1)
-    oracle.set_threads(threads)
+    host_oracle()
     dim = 1536
-    x = workloads.m1_op(batch=1, dim=dim, length=SHAPE["length"], state=SHAPE["state"], seed=0)
-    rng = np.random.default_rng(100)
-    x["delta"] = (rng.standard_normal(x["u"].shape, dtype=np.float32) * np.float32(0.5)
-                  - np.float32(4.0))
-    bias = rng.uniform(-0.5, 0.5, dim).astype(np.float32)
-    reps, t0 = 0, time.perf_counter()
-    while True:
+    x = workloads.m1_layer(batch=1, dim=dim, length=SHAPE["length"], state=SHAPE["state"],
+                           seed=0)
+
+    def call():
         oracle.selective_scan(x["u"], x["delta"], x["A"], x["B"], x["C"], D=x["D"], z=x["z"],
-                              delta_bias=bias, delta_softplus=True, threading=2)
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= seconds or reps >= 1000:
-            break
+                              delta_bias=x["delta_bias"], delta_softplus=True, threading=2)
+
     nbytes = workloads.m1_bytes(1, dim, SHAPE["length"], SHAPE["state"], z=True, D=True,
                                 bias=True)
-    return dict(value=round(nbytes * reps / el / 1e9, 3), unit="GB/s", cores=threads,
-                kind="port",
-                sample=f"{reps} passes of B1 D{dim} L{SHAPE['length']} N{SHAPE['state']} "
-                       f"(one batch row of the step; softplus+bias, D, z) in {el:.1f} s, "
-                       f"{threads} threads")
+    return cpu_rates(call, nbytes, f"B1 D{dim} L{SHAPE['length']} N{SHAPE['state']} (one "
+                     "batch row of the step; softplus+bias, D, z)", seconds, 1000)
 
 
 def traffic_from_profiles():

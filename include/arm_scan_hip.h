@@ -5,7 +5,7 @@
  * The entry points keep the reference's names, argument order and return codes
  * (kernel/arm-scan-ffi/src/lib.rs). What changes, as the reference's own versioning
  * rule demands (arm-scan-ffi/src/lib.rs:25-37: "bump on any signature or semantic
- * change"), is ABI 7 -> 8:
+ * change"), is ABI 7 -> 9:
  *
  *   - every tensor pointer is a DEVICE pointer (HBM of the current HIP device);
  *   - every entry point takes a trailing `void* stream` (a hipStream_t; NULL is the

@@ -16,7 +16,8 @@ live here:
 * `naive.py`: pure-numpy float64 loops written from the mathematics, sharing
   no code with the C++ file, used to pin it.
 
-Parity status of every function is listed in `oracle/PINNING.md`.
+Every function here is pinned by tests/test_oracle.py: the reference's golden
+vectors (tests/golden/), closed forms and invariants, and `naive.py`.
 """
 
 import ctypes
@@ -64,9 +65,21 @@ class OracleError(RuntimeError):
 _lib = None
 
 
-def build():
-    """Compile libarm_scan_cpu.so with the committed Makefile."""
-    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+def build(out=None):
+    """Compile libarm_scan_cpu.so with the committed Makefile; with `out`, a fresh
+    build (on this host's compiler) into that path instead of the package's copy."""
+    cmd = ["make", "-s", "-C", str(HERE)]
+    if out is not None:
+        cmd += ["-B", f"LIB={out}"]
+    subprocess.run(cmd, check=True)
+
+
+def use(path):
+    """Load the oracle from `path` (a build(out=path) library) from now on."""
+    global LIB_PATH
+    if _lib is not None and Path(path) != LIB_PATH:
+        raise RuntimeError(f"the oracle is already loaded from {LIB_PATH}")
+    LIB_PATH = Path(path)
 
 
 def lib():

@@ -7,11 +7,11 @@ floors). They are copied byte-for-byte, never regenerated, from
 
   1d/            every Mamba-1 case (tests/golden/*.npz, manifest.json)
   2d/            every SS2D case (tests/golden/2d/)
-  mamba3/        SISO cases captured from the official Triton kernel; the
-                 small ones (L = 1, 63, 64, 255, batch 2) — the 2.4 MB L=256
-                 cases 00-03 are left out to keep the repository small
-  mamba3_mimo/   MIMO cases captured from the official TileLang kernel;
-                 05, 06 (L 64/63), 08 (rank 2), 09 (dqk 64, 16 heads)
+  mamba3/        every SISO case captured from the official Triton kernel
+                 (00-03 are L 256 at the published 24 heads x 64, dqk 128)
+  mamba3_mimo/   every MIMO case captured from the official TileLang kernel
+                 (00-04 and 07 at the published head shapes, 08 rank 2,
+                 09 dqk 64 with 16 heads)
 
 Nothing in the GPU tests, smoke() or bench.py reads /root/reference; they read
 these copies.
@@ -27,10 +27,8 @@ DST = Path(__file__).resolve().parent
 SETS = {
     "1d": (SRC, ["*.npz", "manifest.json"]),
     "2d": (SRC / "2d", ["*.npz", "manifest.json"]),
-    "mamba3": (SRC / "mamba3", ["manifest.json"] + [
-        f"mamba3_siso_combined_{i:02d}.npz" for i in (4, 5, 6, 7, 8)]),
-    "mamba3_mimo": (SRC / "mamba3_mimo", ["manifest.json"] + [
-        f"mamba3_mimo_combined_{i:02d}.npz" for i in (5, 6, 8, 9)]),
+    "mamba3": (SRC / "mamba3", ["manifest.json", "mamba3_siso_combined_*.npz"]),
+    "mamba3_mimo": (SRC / "mamba3_mimo", ["manifest.json", "mamba3_mimo_combined_*.npz"]),
 }
 
 

@@ -118,3 +118,47 @@ def test_causal_conv1d_oracle_closed_forms():
     np.testing.assert_allclose(naive.causal_conv1d(2 * x2 - x3, w),
                                2 * naive.causal_conv1d(x2, w) - naive.causal_conv1d(x3, w),
                                rtol=1e-12, atol=1e-12)
+
+
+def _mixer_fixture(golden_dir, name):
+    import json
+
+    z = np.load(golden_dir / "mamba3_block" / f"{name}.npz")
+    meta = json.loads(bytes(z["meta_json"]).decode())
+    params = {k[len("param:"):].replace(".weight", ""): z[k]
+              for k in z.files if k.startswith("param:")}
+    return z["u"], z["y"], params, meta
+
+
+def _oracle_mixer(u, p, meta):
+    return naive.m3_mixer(u, p, meta["nheads"], meta["headdim"], meta["d_state"],
+                          meta["mimo_rank"], meta["ngroups"], meta["num_rope_angles"],
+                          meta["A_floor"], meta["eps"])
+
+
+def _swap_rows(w, a, b, n):
+    """in_proj with its column blocks [a, a+n) and [b, b+n) exchanged."""
+    w = w.copy()
+    w[[*range(a, a + n), *range(b, b + n)]] = w[[*range(b, b + n), *range(a, a + n)]]
+    return w
+
+
+@pytest.mark.parametrize("name", ["mixer_siso", "mixer_mimo"])
+def test_oracle_mixer_matches_reference_block(golden_dir, name):
+    """naive.m3_mixer (the oracle's transcription of block.py:146-199) against the
+    reference's own Mamba3Mixer.forward, captured with the oracle's float64 scans by
+    tests/golden/gen_mixer_fixtures.py. That pins the column split and the
+    Q <- C / K <- B mapping; planted mistakes in either must fail the same gate."""
+    u, y, p, meta = _mixer_fixture(golden_dir, name)
+    got = _oracle_mixer(u, p, meta)
+    err = np.abs(got - y).max() / np.abs(y).max()
+    assert err < 1e-6, err  # the reference casts dd_A and the angles to float32
+    di = meta["nheads"] * meta["headdim"]
+    bc = meta["d_state"] * meta["mimo_rank"] * meta["ngroups"]
+    # Q <- B, K <- C instead: B and C column blocks (and their norms and biases) swapped
+    q = dict(p, in_proj=_swap_rows(p["in_proj"], 2 * di, 2 * di + bc, bc),
+             B_norm=p["C_norm"], C_norm=p["B_norm"], B_bias=p["C_bias"], C_bias=p["B_bias"])
+    assert np.abs(_oracle_mixer(u, q, meta) - y).max() / np.abs(y).max() > 1e-2
+    # x and z split the other way round
+    q = dict(p, in_proj=_swap_rows(p["in_proj"], 0, di, di))
+    assert np.abs(_oracle_mixer(u, q, meta) - y).max() / np.abs(y).max() > 1e-2

@@ -213,3 +213,26 @@ def test_mixer_full_size_against_composition():
             z=z.reshape(b, L, h, p).contiguous())
         want = m.out_proj(y.reshape(b, L, h * p))
     assert rel_err(host(got), host(want)) <= 1e-5
+
+
+@pytest.mark.parametrize("name", ["mixer_siso", "mixer_mimo"])
+def test_mixer_against_reference_block_fixture(golden_dir, name):
+    """Mamba3Mixer with the fixture's weights against the reference's own
+    Mamba3Mixer.forward (apps/mamba3_lm/block.py:146-199), captured in float64 by
+    tests/golden/gen_mixer_fixtures.py: the column split and Q <- C / K <- B mapping."""
+    import json
+
+    import torch
+
+    from armhackathon_amd.mamba3_block import Mamba3Mixer
+
+    z = np.load(golden_dir / "mamba3_block" / f"{name}.npz")
+    meta = json.loads(bytes(z["meta_json"]).decode())
+    case(f"Mamba3Mixer vs reference block fixture {name}")
+    m = Mamba3Mixer(**meta["kwargs"])
+    m.load_state_dict({k[len("param:"):]: torch.from_numpy(z[k].astype(np.float32))
+                       for k in z.files if k.startswith("param:")})
+    m = m.cuda()
+    with torch.no_grad():
+        y = m(torch.from_numpy(z["u"].astype(np.float32)).cuda())
+    assert rel_err(host(y), z["y"]) < TOL

@@ -182,6 +182,19 @@ def test_m1_benchmark_shape(batch):
     assert rel_err(host(last), ref_last) < TOL
 
 
+def test_m1_bench_step_inputs():
+    """The headline bench step exactly as bench.py times it: B8 D1536 L2048 N16 with
+    the raw delta, delta_bias and softplus, D and z (workloads.m1_layer, both input
+    sets), against the float64 oracle, outputs and final states."""
+    for seed in (0, 1):
+        case(f"m1 bench step inputs seed={seed}")
+        x = workloads.m1_layer(seed=seed)
+        out, last = _scan(x, delta_softplus=True)
+        ref, ref_last = _ref(x, delta_softplus=True)
+        assert rel_err(host(out), ref) < TOL
+        assert rel_err(host(last), ref_last) < TOL
+
+
 def _time_major_inputs(x):
     """Device tensors laid out as the Hugging Face mixer hands them over: the gate
     z a (b, D, L) view of (b, L, 2D) storage (modeling_mamba.py: projected_states
@@ -506,3 +519,40 @@ def test_causal_conv1d_time_major_out(width, dim, length):
         t = arm_scan.causal_conv1d(x, w, bias, activation=act, time_major=True)
         assert t.stride() == (length * dim, 1, dim) and a.is_contiguous()
         assert torch.equal(a, t)
+
+
+@pytest.mark.parametrize("reverse", [False, True])
+def test_m1_broadcast_views(reverse):
+    """Broadcast views of the gate (stride 0): through the op they are rerouted to the
+    contiguous path; through the strided C entry point their zero strides are read as
+    given (a broadcast), never as 'contiguous'. Both against the float64 oracle with
+    the gate materialised."""
+    import torch
+
+    import armhackathon_amd as arm_scan
+    from armhackathon_amd import _ffi
+
+    b, d, L, n = 2, 32, 1024, 16
+    x = workloads.m1_op(batch=b, dim=d, length=L, state=n, seed=21)
+    t = dev(x)
+    rng = np.random.default_rng(22)
+    zc = rng.standard_normal((1, d, 1)).astype(np.float32)
+    z_scalar = np.full((1, 1, 1), 0.7, np.float32)
+    for name, small in (("per-channel", zc), ("scalar", z_scalar)):
+        case(f"m1 broadcast gate {name} reverse={reverse}")
+        zt = torch.from_numpy(small).cuda().expand(b, d, L)
+        xm = dict(x, z=np.ascontiguousarray(np.broadcast_to(small, (b, d, L))))
+        ref, ref_last = _ref(xm, reverse=reverse)
+        out, last = arm_scan.selective_scan_time_major(
+            t["u"], t["delta"], t["A"], t["B"], t["C"], D=t["D"], z=zt,
+            return_last_state=True, reverse=reverse)
+        assert rel_err(host(out), ref) < TOL and rel_err(host(last), ref_last) < TOL
+        out2 = torch.empty((b, d, L), device="cuda")
+        last2 = torch.empty((b, d, n), device="cuda")
+        _ffi.scan_strided_raw(_ffi.ArmScanDims(b, d, L, n, 1), t["u"].data_ptr(),
+                              t["delta"].data_ptr(), t["A"].data_ptr(), t["B"].data_ptr(),
+                              t["C"].data_ptr(), t["D"].data_ptr(), zt.data_ptr(), zt.stride(),
+                              0, False, out2.data_ptr(), None, last2.data_ptr(), 0,
+                              reverse=reverse,
+                              stream=torch.cuda.current_stream().cuda_stream)
+        assert rel_err(host(out2), ref) < TOL and rel_err(host(last2), ref_last) < TOL

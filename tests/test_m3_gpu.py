@@ -169,10 +169,10 @@ def test_m3_pair_and_reverse_is_flip():
 
 
 def test_m3_siso_benchmark_shape():
-    """BASELINE config 3 (per-head q/k, L 4096, 24 heads x 64, dqk 128), batch
-    reduced to 2 to bound the oracle's CPU time; outputs, final states, last_bx."""
-    case("siso config 3 (batch 2)")
-    x = workloads.m3_siso(batch=2, seed=3)
+    """BASELINE config 3 at its full size (B4 L4096, per-head q/k, 24 heads x 64,
+    dqk 128); outputs, final states, last_bx."""
+    case("siso config 3 (full B4 L4096)")
+    x = workloads.m3_siso(batch=4, seed=3)
     out, ls, lbx = _siso_gpu(x, return_last_state=True)
     ref, rls, rlbx = _siso_ref(x, want_state=True)
     assert rel_err(host(out), ref.transpose(0, 2, 1, 3)) < TOL
@@ -181,12 +181,12 @@ def test_m3_siso_benchmark_shape():
 
 
 def test_m3_mimo_benchmark_shape():
-    """BASELINE config 4 (rank 4, per-head q/k), batch 1, L 2048 to bound the
-    oracle's CPU time; output and final state."""
+    """BASELINE config 4 at its full size (rank 4, per-head q/k, B4 L4096); output and
+    final state."""
     import armhackathon_amd as arm_scan
 
-    case("mimo config 4 (batch 1, L 2048)")
-    x = workloads.m3_mimo(batch=1, length=2048, seed=4)
+    case("mimo config 4 (full B4 L4096)")
+    x = workloads.m3_mimo(batch=4, length=4096, seed=4)
     t = dev(x)
     out, ls = arm_scan.mamba3_mimo_scan(
         *[t[k] for k in SISO_KEYS], t["psi"], t["zeta"], t["phi"], cos=t["cos"], sin=t["sin"],
@@ -384,3 +384,37 @@ def test_m3_angle_prepass(shape):
     assert np.abs(host(cos) - rc).max() < 2e-5
     assert np.abs(host(sin) - rs).max() < 2e-5
     assert np.all(host(cos)[..., r:] == 1.0) and np.all(host(sin)[..., r:] == 0.0)
+
+
+def test_m3_broadcast_views():
+    """v and the raw angles as broadcast views over batch (stride 0) and the angles
+    over heads: the op takes the contiguous route for the batch broadcast (the head
+    broadcast alone is read in place), and the result matches the float64 oracle on
+    the materialised tensors."""
+    import torch
+
+    import armhackathon_amd as arm_scan
+
+    b, L, h, dv, dqk, r = 2, 64, 4, 16, 32, 8
+    x = workloads.m3_siso(batch=b, length=L, heads=h, dv=dv, dqk=dqk, seed=31)
+    rng = np.random.default_rng(32)
+    ang_small = rng.standard_normal((1, L, 1, r)).astype(np.float32)
+    v_small = rng.standard_normal((1, L, h, dv)).astype(np.float32)
+    t = dev(x)
+    for name, over_batch in (("heads", False), ("batch+heads", True)):
+        case(f"m3 broadcast views over {name}")
+        ang_np = np.broadcast_to(ang_small, (b, L, h, r)) if over_batch else \
+            np.broadcast_to(rng.standard_normal((b, L, 1, r)).astype(np.float32), (b, L, h, r))
+        ta = (torch.from_numpy(ang_small).cuda().expand(b, L, h, r) if over_batch
+              else torch.from_numpy(np.ascontiguousarray(ang_np[:, :, :1])).cuda()
+              .expand(b, L, h, r))
+        tv = torch.from_numpy(v_small).cuda().expand(b, L, h, dv) if over_batch else t["v"]
+        v_np = np.broadcast_to(v_small, (b, L, h, dv)) if over_batch else x["v"]
+        out = arm_scan.mamba3_scan(*[t[k] for k in ("q", "k")], tv,
+                                   *[t[k] for k in ("adt", "dt", "trap", "q_bias", "k_bias")],
+                                   angles=ta)
+        cos, sin = oracle.angles_to_cos_sin(np.ascontiguousarray(ang_np), x["dt"], dqk // 2)
+        ref = oracle.mamba3_scan(x["q"], x["k"], np.ascontiguousarray(v_np), x["adt"], x["dt"],
+                                 x["trap"], x["q_bias"], x["k_bias"], cos, sin,
+                                 dtype=np.float64)
+        assert rel_err(host(out), ref.transpose(0, 2, 1, 3)) < TOL

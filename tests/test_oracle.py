@@ -248,7 +248,7 @@ def _siso_args(kw, dtype=np.float64):
 def test_m3_siso_goldens(golden_dir):
     """Official Triton kernel captures, <= 8 bf16 ULP at tensor scale."""
     files = sorted((golden_dir / "mamba3").glob("*.npz"))
-    assert len(files) == 5
+    assert len(files) == 9  # every capture the reference holds (_09 is missing upstream)
     for f in files:
         kw, gold = _m3_load(f)
         args = _siso_args(kw)
@@ -377,7 +377,7 @@ def _mimo_args(kw):
 def test_m3_mimo_goldens(golden_dir):
     """Official TileLang MIMO captures, <= 12 bf16 ULP (check_mamba3_mimo_op.py:66)."""
     files = sorted((golden_dir / "mamba3_mimo").glob("*.npz"))
-    assert len(files) == 4
+    assert len(files) == 10
     for f in files:
         kw, gold = _m3_load(f)
         out = oracle.mamba3_scan(*_mimo_args(kw), D=kw.get("D"), z=kw.get("Z"),

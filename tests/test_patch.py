@@ -29,9 +29,11 @@ def test_patch_falls_back_on_host_tensors():
             assert targets and "mamba_selective_scan" in targets[0]
             assert any("mamba_selective_state_update" in t for t in targets)
             assert modeling_mamba.mamba_selective_state_update is not orig_step
-            assert any("causal_conv1d_fn" in t for t in targets)
-            assert modeling_mamba.causal_conv1d_fn is not orig_conv
-            assert modeling_mamba.causal_conv1d_update is not orig_conv_step
+            # the default patch is the reference's: the scan (and its decode step),
+            # the mixer's convolution stays upstream's
+            assert not any("causal_conv1d_fn" in t for t in targets)
+            assert modeling_mamba.causal_conv1d_fn is orig_conv
+            assert modeling_mamba.causal_conv1d_update is orig_conv_step
             assert arm_scan.patch() == ["transformers mamba_selective_scan (already patched)"]
             assert modeling_mamba.mamba_selective_scan is not orig
             before = arm_scan.stats()
@@ -46,7 +48,23 @@ def test_patch_falls_back_on_host_tensors():
     assert not arm_scan.unpatch()
     assert after["fallback_calls"] - before["fallback_calls"] == 2
     assert after["fast_calls"] == before["fast_calls"]
-    assert after["conv_fallback_calls"] - before["conv_fallback_calls"] == 2
     assert after["conv_calls"] == before["conv_calls"]
+    # conv=True routes the convolution too (host tensors: it falls back), and
+    # unpatch restores it
+    with torch.no_grad():
+        targets = arm_scan.patch(conv=True)
+        try:
+            assert any("causal_conv1d_fn" in t for t in targets)
+            assert modeling_mamba.causal_conv1d_fn is not orig_conv
+            assert modeling_mamba.causal_conv1d_update is not orig_conv_step
+            before = arm_scan.stats()
+            got2 = model(ids, use_cache=False).logits
+            after = arm_scan.stats()
+        finally:
+            assert arm_scan.unpatch()
+    assert modeling_mamba.causal_conv1d_fn is orig_conv
+    assert modeling_mamba.causal_conv1d_update is orig_conv_step
+    assert after["conv_fallback_calls"] - before["conv_fallback_calls"] == 2
+    assert torch.equal(got2, ref)
     assert torch.equal(ref, got)
     assert transformers is not None

@@ -25,21 +25,23 @@ def _model(layers=3, hidden=64, vocab=512, seed=0):
     return MambaForCausalLM(cfg).cuda().float().eval()
 
 
+@pytest.mark.parametrize("conv", [False, True], ids=["scan", "scan+conv"])
 @pytest.mark.parametrize("length", [300, 301])
-def test_patch_logits_and_engagement(length):
+def test_patch_logits_and_engagement(length, conv):
     """300: the gate read in place and the output written time-major; 301 (not a
-    multiple of 4): the contiguous scan, then the time-major layout."""
+    multiple of 4): the contiguous scan, then the time-major layout. The default
+    patch is the reference's (the scan only); conv=True adds the causal conv."""
     import torch
 
     import armhackathon_amd as arm_scan
 
-    case(f"hf patch logits L={length}")
+    case(f"hf patch logits L={length} conv={conv}")
     model = _model()
     ids = torch.randint(0, 512, (2, length), device="cuda",
                         generator=torch.Generator(device="cuda").manual_seed(1))
     with torch.no_grad():
         ref = model(ids, use_cache=False).logits
-        arm_scan.patch()
+        arm_scan.patch(conv=conv)
         try:
             s0 = arm_scan.stats()
             got = model(ids, use_cache=False).logits
@@ -48,11 +50,43 @@ def test_patch_logits_and_engagement(length):
             arm_scan.unpatch()
     assert s1["fast_calls"] - s0["fast_calls"] == 3
     assert s1["fallback_calls"] == s0["fallback_calls"]
-    assert s1["conv_calls"] - s0["conv_calls"] == 3
+    assert s1["conv_calls"] - s0["conv_calls"] == (3 if conv else 0)
     assert s1["conv_fallback_calls"] == s0["conv_fallback_calls"]
     scale = max(1.0, ref.abs().max().item())
     assert (got - ref).abs().max().item() < 1e-4 * scale
     assert not arm_scan.stats()["patched"]
+
+
+def test_patch_config2_architecture():
+    """BASELINE config 2 itself: the Mamba-130M architecture (24 layers, d_model 768,
+    d_state 16, dt_rank 48, conv 4, vocab 50280), random init, fp32, batch 8 x 2048,
+    scan patched vs upstream's torch recurrence: last-position logits within
+    1e-4 * max(1, scale) (check_hf_patch.py:34,67-69), 24 fast scan calls."""
+    import torch
+    from transformers import MambaConfig, MambaForCausalLM
+
+    import armhackathon_amd as arm_scan
+
+    case("hf patch config 2 architecture B8 L2048")
+    cfg = MambaConfig(vocab_size=50280, hidden_size=768, state_size=16, num_hidden_layers=24,
+                      expand=2, conv_kernel=4, time_step_rank=48)
+    torch.manual_seed(0)
+    model = MambaForCausalLM(cfg).cuda().float().eval()
+    ids = torch.randint(0, 50280, (8, 2048), device="cuda",
+                        generator=torch.Generator(device="cuda").manual_seed(0))
+    with torch.no_grad():
+        ref = model(ids, use_cache=False, logits_to_keep=1).logits
+        arm_scan.patch()
+        try:
+            s0 = arm_scan.stats()
+            got = model(ids, use_cache=False, logits_to_keep=1).logits
+            s1 = arm_scan.stats()
+        finally:
+            arm_scan.unpatch()
+    assert s1["fast_calls"] - s0["fast_calls"] == 24
+    assert s1["fallback_calls"] == s0["fallback_calls"]
+    scale = max(1.0, ref.abs().max().item())
+    assert (got - ref).abs().max().item() < 1e-4 * scale
 
 
 def test_patch_cached_generation():
@@ -66,7 +100,7 @@ def test_patch_cached_generation():
                         generator=torch.Generator(device="cuda").manual_seed(3))
     with torch.no_grad():
         ref = model.generate(ids, max_new_tokens=12, do_sample=False)
-        arm_scan.patch()
+        arm_scan.patch(conv=True)
         try:
             got = model.generate(ids, max_new_tokens=12, do_sample=False)
             st = arm_scan.stats()
