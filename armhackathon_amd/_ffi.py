@@ -86,13 +86,13 @@ def _declare(lib):
     lib.arm_scan_abi_version.argtypes = []
     lib.arm_scan_last_error.restype = ctypes.c_char_p
     lib.arm_scan_last_error.argtypes = []
-    f = lib.arm_scan_selective_scan_f32
-    f.restype = _ci
-    f.argtypes = [ctypes.POINTER(ArmScanDims),
-                  *([_vp] * 8),          # u delta a b c d_skip z delta_bias
-                  _ci, _ci, _ci, _ci,    # delta_softplus reverse backend threading
-                  _vp, _vp, _vp,         # out last_state h0
-                  _vp]                   # stream
+    for f in (lib.arm_scan_selective_scan_f32, lib.arm_scan_selective_scan_noalloc_f32):
+        f.restype = _ci
+        f.argtypes = [ctypes.POINTER(ArmScanDims),
+                      *([_vp] * 8),          # u delta a b c d_skip z delta_bias
+                      _ci, _ci, _ci, _ci,    # delta_softplus reverse backend threading
+                      _vp, _vp, _vp,         # out last_state h0
+                      _vp]                   # stream
     f = lib.arm_scan_selective_scan_strided_f32
     f.restype = _ci
     f.argtypes = [ctypes.POINTER(ArmScanDims),

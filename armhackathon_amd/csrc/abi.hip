@@ -125,6 +125,29 @@ int arm_scan_selective_scan_f32(const ArmScanDims* dims, const float* u, const f
   return run(armscan::m1_scan(p, (hipStream_t)stream), "selective_scan launch");
 }
 
+int arm_scan_selective_scan_noalloc_f32(const ArmScanDims* dims, const float* u,
+                                        const float* delta, const float* a, const float* b,
+                                        const float* c, const float* d_skip, const float* z,
+                                        const float* delta_bias, int delta_softplus,
+                                        int reverse, int backend, int threading, float* out,
+                                        float* last_state, const float* h0, void* stream) {
+  if (!dims || !u || !delta || !a || !b || !c || !out)
+    return fail(ARM_SCAN_ERR_NULL_POINTER, "a required pointer is null");
+  if (int rc = check_enums(backend, threading)) return rc;
+  if (int rc = check_m1_dims(*dims)) return rc;
+  armscan::M1Problem p{};
+  p.batch = dims->batch; p.dim = dims->dim; p.len = dims->len; p.state = dims->state;
+  p.groups = dims->groups;
+  p.u = u; p.delta = delta; p.A = a; p.B = b; p.C = c; p.D = d_skip; p.z = z;
+  p.bias = delta_bias; p.h0 = h0; p.out = out; p.last = last_state;
+  p.softplus = delta_softplus != 0; p.reverse = reverse != 0;
+  // the segment maps go to the library's static scratch on this device: nothing is
+  // allocated, and the plan never needs more than the scratch holds
+  if (hipError_t e = armscan::m1_noalloc_scratch(&p.scratch, &p.scratch_bytes))
+    return hip_fail(e, "scratch lookup");
+  return run(armscan::m1_scan(p, (hipStream_t)stream), "selective_scan (no-alloc) launch");
+}
+
 int arm_scan_selective_scan_strided_f32(const ArmScanDims* dims, const float* u,
                                         const long long* u_strides,
                                         const float* delta, const float* a, const float* b,

@@ -28,6 +28,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdint>
 
 #include "scan_common.h"
@@ -1035,11 +1036,39 @@ long long slab_bytes(const long long (&s)[3], const M1Problem& pr) {
 }
 }  // namespace
 
+// The allocation-free entry point's scratch (arm_scan_selective_scan_noalloc_f32):
+// the segment maps of the few-rows plan live here instead of in stream-ordered
+// allocations. Every device holds its own copy until the process ends; host code
+// reaches it only through the address m1_noalloc_scratch looks up per device.
+constexpr size_t kNoAllocScratchBytes = size_t(4) << 20;
+static __device__ __align__(256) float scratch[kNoAllocScratchBytes / sizeof(float)];
+
+hipError_t m1_noalloc_scratch(float** out, size_t* bytes) {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<float*> addr[kMaxDevices];
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  float* p = addr[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    // with this device current: its copy of the array (racing threads find the same)
+    e = hipGetSymbolAddress((void**)&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    addr[dev].store(p, std::memory_order_release);
+  }
+  *out = p;
+  *bytes = kNoAllocScratchBytes;
+  return hipSuccess;
+}
+
 namespace {
 // Rows cut into segments when there are too few to fill the chip: a 16-row block per
 // CU slot, 768 slots (three per CU) resident at once. Sets k.segs / k.seg_chunks and
-// allocates the segment maps on the stream.
-hipError_t plan_segments(M1Kern& k, hipStream_t st) {
+// allocates the segment maps on the stream, or, with caller scratch, takes them from
+// it, cutting the plan to fewer segments (down to whole rows, which need no maps)
+// until they fit.
+hipError_t plan_segments(M1Kern& k, float* scratch_p, size_t scratch_bytes, hipStream_t st) {
   const long long blocks = k.rows / 16;
   const long long nfull = k.L / (16 * M1_TILE_I);
   k.segs = 1;
@@ -1048,6 +1077,11 @@ hipError_t plan_segments(M1Kern& k, hipStream_t st) {
   if (blocks >= 512 || nfull < 2) return hipSuccess;
   long long segs = (768 + blocks - 1) / blocks;
   if (segs > nfull) segs = nfull;
+  auto map_bytes = [&](long long s) {
+    return (size_t)k.rows * (size_t)(s - 1) * (size_t)k.N * 2 * sizeof(float);
+  };
+  if (scratch_p)
+    while (segs >= 2 && map_bytes(segs) > scratch_bytes) --segs;
   if (segs < 2) return hipSuccess;
   k.seg_chunks = (nfull + segs - 1) / segs;
   k.segs = (int)((nfull + k.seg_chunks - 1) / k.seg_chunks);
@@ -1056,16 +1090,20 @@ hipError_t plan_segments(M1Kern& k, hipStream_t st) {
     k.seg_chunks = nfull;
     return hipSuccess;
   }
-  return stream_alloc((void**)&k.segmap,
-                      (size_t)k.rows * (k.segs - 1) * k.N * 2 * sizeof(float), st);
+  if (scratch_p) {
+    k.segmap = scratch_p;  // every map is written by the fold before the replay reads it
+    return hipSuccess;
+  }
+  return stream_alloc((void**)&k.segmap, map_bytes(k.segs), st);
 }
 
 template <int SIO>
-hipError_t run_tile(M1Kern& k, bool rev, hipStream_t st) {
-  hipError_t e = plan_segments(k, st);
+hipError_t run_tile(M1Kern& k, bool rev, float* scratch_p, size_t scratch_bytes,
+                    hipStream_t st) {
+  hipError_t e = plan_segments(k, scratch_p, scratch_bytes, st);
   if (e != hipSuccess) return e;
   e = rev ? launch_tile<M1_TILE_I, true, SIO>(k, st) : launch_tile<M1_TILE_I, false, SIO>(k, st);
-  if (k.segmap) {
+  if (k.segmap && !scratch_p) {
     const hipError_t fe = hipFreeAsync(k.segmap, st);
     if (e == hipSuccess) e = fe;
   }
@@ -1135,11 +1173,12 @@ hipError_t m1_scan_chunked(const M1Problem& pr, hipStream_t st) {
       k.u_dma = k.z_dma && k.us_d == 1 && k.us_t % 4 == 0 && k.us_b % 4 == 0 &&
                 aligned16(pr.u);
     }
-    return k.z_dma ? run_tile<2>(k, rev, st) : run_tile<1>(k, rev, st);
+    return k.z_dma ? run_tile<2>(k, rev, pr.scratch, pr.scratch_bytes, st)
+                   : run_tile<1>(k, rev, pr.scratch, pr.scratch_bytes, st);
   }
   // the tiled path needs every 16-row block inside one batch/group and 16-byte rows
   const bool tiled = vec && pr.dim % 16 == 0 && (pr.dim / pr.groups) % 16 == 0;
-  if (tiled) return run_tile<0>(k, rev, st);
+  if (tiled) return run_tile<0>(k, rev, pr.scratch, pr.scratch_bytes, st);
   return launch_dir<16, 16>(k, rev, vec, st);
 }
 

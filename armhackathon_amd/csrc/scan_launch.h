@@ -21,9 +21,17 @@ struct M1Problem {
   // null stride array). Every value is taken as given: a stride of 0 is a broadcast.
   int has_strides;
   long long z_stride[3], out_stride[3], u_stride[3];
+  // Caller-provided scratch for the segment maps of the few-rows plan (the
+  // allocation-free entry point passes its static device array): when set, nothing
+  // is allocated, and the plan is cut to what scratch_bytes holds.
+  float* scratch;
+  size_t scratch_bytes;
 };
 
 hipError_t m1_scan(const M1Problem& p, hipStream_t st);
+// The per-device address and size of the allocation-free entry point's static scratch
+// (m1_chunk.hip), looked up once per device with that device current.
+hipError_t m1_noalloc_scratch(float** p, size_t* bytes);
 
 // One decode step of the Mamba-1 scan, the state (batch, dim, N) updated in place
 // (m1_step.hip). Element strides: x, dt, z (batch, dim); B, C (batch, state).

@@ -93,6 +93,23 @@ int arm_scan_selective_scan_f32(const ArmScanDims* dims, const float* u, const f
                                 int delta_softplus, int reverse, int backend, int threading,
                                 float* out, float* last_state, const float* h0, void* stream);
 
+/* No reference counterpart: arm_scan_selective_scan_f32 for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc). Same arguments, checks, codes and kernels; it calls no
+ * hipMalloc/hipFree. The only scratch of this scan, the segment maps of the plan for
+ * few rows (B * D < 8192: rows cut into segments folded first, then replayed), lives
+ * in a static 4 MiB device array instead, one per GPU, held until the process ends.
+ * No size is rejected for it: a plan whose maps would exceed 4 MiB is cut to fewer
+ * segments (whole rows need none). Every map is written before it is read, so no
+ * call depends on what the array held before. Calls that overlap on one GPU (two
+ * streams at once) share the array and race: serialise them. */
+int arm_scan_selective_scan_noalloc_f32(const ArmScanDims* dims, const float* u,
+                                        const float* delta, const float* a, const float* b,
+                                        const float* c, const float* d_skip, const float* z,
+                                        const float* delta_bias, int delta_softplus,
+                                        int reverse, int backend, int threading, float* out,
+                                        float* last_state, const float* h0, void* stream);
+
 /* No reference counterpart: arm_scan_selective_scan_f32 with u, z and out given by
  * element strides (batch, dim, step) instead of as contiguous (batch, dim, len).
  * It serves the Hugging Face seam, which hands the gate z as a (batch, dim, len)

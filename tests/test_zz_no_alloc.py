@@ -1,0 +1,61 @@
+"""arm_scan_selective_scan_noalloc_f32 (the allocation-free variant of
+arm_scan_selective_scan_f32) through the C ABI, against the allocating entry point.
+
+Two calls in a row share the library's static scratch, the second on a smaller
+input: config 1's shape (its plan cuts 1536 rows into 8 segments whose maps live in
+the scratch), then B1 D256 L1024 (4 segments). Same plan, same kernels: the outputs
+and final states must be bit-identical. A third call whose maps would not fit
+(N 64 at L 4096) takes a plan cut to fewer segments, so only the tolerance of the
+float64 oracle applies there, and the allocating call is checked the same way.
+"""
+
+import ctypes
+
+import numpy as np
+import pytest
+
+import oracle
+from armhackathon_amd import _ffi, workloads
+from util import case, dev, host, rel_err
+
+pytestmark = pytest.mark.gpu
+
+
+def _call(fn_name, x, softplus=False, reverse=False):
+    import torch
+
+    b, d, L = x["u"].shape
+    n = x["A"].shape[1]
+    t = dev(x)
+    out = torch.full((b, d, L), float("nan"), device="cuda")
+    last = torch.full((b, d, n), float("nan"), device="cuda")
+    p = lambda k: None if t.get(k) is None else t[k].data_ptr()  # noqa: E731
+    rc = getattr(_ffi.load(), fn_name)(
+        ctypes.byref(_ffi.ArmScanDims(b, d, L, n, 1)), p("u"), p("delta"), p("A"), p("B"),
+        p("C"), p("D"), p("z"), p("delta_bias"), int(softplus), int(reverse), 0, 0,
+        out.data_ptr(), last.data_ptr(), None, torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, _ffi.load().arm_scan_last_error()
+    torch.cuda.synchronize()
+    return host(out), host(last)
+
+
+@pytest.mark.parametrize("reverse", [False, True])
+def test_noalloc_matches_allocating_entry(reverse):
+    for (b, d, L, n, seed) in ((1, 1536, 2048, 16, 40), (1, 256, 1024, 16, 41)):
+        case(f"noalloc vs selective_scan_f32 {b}x{d}x{L} N{n} reverse={reverse}")
+        x = workloads.m1_layer(batch=b, dim=d, length=L, state=n, seed=seed)
+        got, got_last = _call("arm_scan_selective_scan_noalloc_f32", x, True, reverse)
+        ref, ref_last = _call("arm_scan_selective_scan_f32", x, True, reverse)
+        assert np.array_equal(got, ref) and np.array_equal(got_last, ref_last)
+
+
+def test_noalloc_plan_cut_to_the_scratch():
+    case("noalloc B1 D1536 L4096 N64 (maps above the scratch: fewer segments)")
+    x = workloads.m1_op(batch=1, dim=1536, length=4096, state=64, seed=42)
+    got, got_last = _call("arm_scan_selective_scan_noalloc_f32", x)
+    ref, ref_last = _call("arm_scan_selective_scan_f32", x)
+    o64, l64 = oracle.selective_scan(x["u"], x["delta"], x["A"], x["B"], x["C"], D=x["D"],
+                                     z=x["z"], dtype=np.float64)
+    for out, last in ((got, got_last), (ref, ref_last)):
+        assert rel_err(out, o64) < 1e-4 and rel_err(last, l64) < 1e-4
+    assert rel_err(got, ref) < 1e-4
