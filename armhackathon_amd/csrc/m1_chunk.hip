@@ -536,6 +536,22 @@ __device__ __forceinline__ void store_out_stage(const float* zbuf, float* oslab,
   }
 }
 
+
+// Issue priority of this wave from its progress through its tiles: 3 for the first
+// half, 2 to three quarters, 1 to 90%, 0 after. The SIMD arbiter otherwise favours the
+// oldest wave, so the three waves sharing a SIMD (one per resident block, dispatched
+// one after another) finish in dispatch order and leave the SIMD to a single wave for
+// the last fifth of the kernel (measured with per-wave s_memrealtime stamps: waves of
+// the same work ending at 84, 114 and 136 us). A wave that is ahead now yields to the
+// ones behind it; the headline scan runs about 5% faster.
+__device__ __forceinline__ void progress_prio(long long k, long long ntiles) {
+  const long long f = ntiles > 0 ? (100 * k) / ntiles : 0;
+  if (f < 50) __builtin_amdgcn_s_setprio(3);
+  else if (f < 75) __builtin_amdgcn_s_setprio(2);
+  else if (f < 90) __builtin_amdgcn_s_setprio(1);
+  else __builtin_amdgcn_s_setprio(0);
+}
+
 // Workgroup barrier that waits for LDS accesses only (global stores stay in flight).
 __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
@@ -737,6 +753,7 @@ __device__ __forceinline__ void tile_rows(const M1Kern& p, long long blk, int se
     if (segd && c == cb) tile_sync();  // the first tile, the carries and A*log2e above
     const bool last_chunk = c + 1 == nch;
     for (int q = 0; q < ng; ++q, ++k) {
+      progress_prio(k, ntiles);
       if (k + 1 < ntiles) {
         const long long cn = cb + (k + 1) / ng;
         const int qn = (int)((k + 1) % ng);
@@ -861,6 +878,7 @@ __device__ __forceinline__ void fold_rows(const M1Kern& p, long long blk, int se
 #pragma unroll
     for (int m = 1; m < LPR; m <<= 1) srow += __shfl_xor(srow, m, LPR);
     for (int q = 0; q < ng; ++q, ++k) {
+      progress_prio(k, ntiles);
       if (k + 1 < ntiles) {
         const long long cn = cb + (k + 1) / ng;
         const int qn = (int)((k + 1) % ng);
