@@ -362,6 +362,49 @@ __device__ __forceinline__ void dma_stage_part(const M3K& p, const SeqIn& s,
   else if (k0 == 0) dma_clamped<R, REV>(p, s, d, ch, stage, lane);
 }
 
+// The plan of a wave for whole chunks, as running pointers: instruction k of a stage
+// reads ptr[k] + off[k] (the lane's piece) into stage + lds[k], and ptr[k] then moves
+// on by one chunk (step[k] floats). A lane whose piece lies past its section's end
+// (`on` false) reads the instruction's first piece into the section's padding, which
+// nothing reads.
+template <int MD>
+struct DmaRun {
+  const float* ptr[MD];
+  int step[MD];
+  int off[MD];
+  int lds[MD];
+  int count;
+};
+
+template <int MD>
+__device__ __forceinline__ void dma_run(const DmaPlan<MD>& d, DmaRun<MD>& r) {
+  r.count = d.count;
+#pragma unroll
+  for (int k = 0; k < MD; ++k) {
+    r.ptr[k] = d.base[k];
+    r.step[k] = d.delta[k];
+    r.off[k] = d.on[k] ? d.off[k] : 0;
+    r.lds[k] = d.ins[k] * 256;
+  }
+}
+
+// Instructions k0 .. k1-1 of the next whole chunk.
+template <int MD>
+__device__ __forceinline__ void dma_part(DmaRun<MD>& r, float* stage, int k0, int k1) {
+#pragma unroll
+  for (int k = 0; k < MD; ++k) {
+    if (k >= k0 && k < k1 && k < r.count) {
+      dma16(r.ptr[k] + r.off[k], stage + r.lds[k]);
+      r.ptr[k] += r.step[k];
+    }
+  }
+}
+
+template <int MD>
+__device__ __forceinline__ void dma_next(DmaRun<MD>& r, float* stage) {
+  dma_part(r, stage, 0, MD);
+}
+
 // Rotated q/k from the raw columns: SISO rotates interleaved pairs (2u, 2u+1)
 // with angle u (mamba3/scalar.rs:40-48); MIMO rotates split halves (u, u + dqk/2)
 // with angle u (mimo.rs:83-96), the lane holding its 4 columns x and their
@@ -464,7 +507,8 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 2)) m3_chunk_kernel(M3K p) {
   float* stages = sm;
   float* gbuf = stages + NS * p.stage_floats;  // [2][kMaxWaves][64][4]
   float* ybuf = gbuf + 2 * kMaxWaves * 256;     // [2][PT][kMaxWaves][64][4]
-  float* kt = ybuf + 2 * PT * kMaxWaves * 256 + nt * 16 * kKtStride;
+  constexpr bool KQ = !MIMO;  // K transposed in the stage's q piece (SISO)
+  float* kt = ybuf + 2 * PT * kMaxWaves * 256 + nt * 16 * kKtStride;  // MIMO only
   const int off_k = WN * 256, off_cs = 2 * WN * 256;
   const int off_sn = off_cs + p.n_cs * 256, off_ang = off_cs + 2 * p.n_cs * 256;
   const int off_v = off_ang + p.n_ang * 256;
@@ -597,35 +641,89 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 2)) m3_chunk_kernel(M3K p) {
                        : 1.0f;
 
   // The DMA instructions of this wave; the partial waves issue no other vector
-  // memory operation inside the loop.
+  // memory operation inside the loop. Full chunks go through the running pointers of
+  // DmaRun, the last chunk (when partial) through dma_clamped.
   DmaPlan<MD> dp;
   dma_plan<R, REV>(p, in, nt, WN, lane, dp);
-  for (int c = 0; c < NS - 1 && c < p.nchunks; ++c)
-    dma_stage<R, REV, MD>(p, in, dp, c, stages + c * p.stage_floats, lane);
+  DmaRun<MD> dr;
+  dma_run(dp, dr);
+  const int nchunks = p.nchunks;
+  const int nfull = L / T;  // chunks wholly inside the sequence
+  const int sfl = p.stage_floats;
+  for (int c = 0; c < NS - 1 && c < nchunks; ++c) {
+    if (c < nfull) dma_next(dr, stages + c * sfl);
+    else dma_clamped<R, REV>(p, in, dp, c, stages + c * sfl, lane);
+  }
+  const int wait_n = (NS - 2) * dp.count;  // outstanding DMA allowed in the steady state
 
+  // The state update of chunk c runs after the barrier of chunk c+1, from operands kept
+  // in registers (K transposed, w x, e^{c_last}): the MFMA work it brings covers the LDS
+  // latency of chunk c+1's q/k rows.
   f4 S[PT];
 #pragma unroll
   for (int j = 0; j < PT; ++j) S[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+  float kc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  f4 wx[PT];
+#pragma unroll
+  for (int j = 0; j < PT; ++j) wx[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+  float etot = 1.0f;
   f4 kr_last = {0.0f, 0.0f, 0.0f, 0.0f};
   // fused angles: theta before the chunk of the pairs the lane computes
   float carry[2] = {0.0f, 0.0f};       // SISO: 2 per lane
   float carry_m[4 / R] = {};           // MIMO: 4/R per lane
-  for (int ch = 0; ch < p.nchunks; ++ch) {
+  float* gw = gbuf + (nt * 64 + lane) * 4;         // this wave's G partial, chunk parity 0
+  float* yw = ybuf + (nt * 256 + lane * 4);        // its Y partials: + ((par * PT + j) * 8) * 256
+  float* ktw = kt + li * kKtStride + 4 * lj;       // K transpose: written as rows
+  const float* ktr = kt + 4 * lj * kKtStride + li; // read as columns
+  int slot = 0;                                    // ring slot of chunk ch
+  int dslot = NS - 1;                              // ring slot of chunk ch + NS - 1
+  // One chunk. FAST: the chunk this iteration's DMA fetches lies wholly inside the
+  // sequence, so the DMA is issued unconditionally and the compiler may schedule the
+  // MFMA phases across it.
+  auto chunk = [&](const int ch, auto fast) {
+    constexpr bool FAST = decltype(fast)::value;
     // Stage ch has landed once no more of this wave's DMA is outstanding than the
     // stages issued after it.
-    const int later = (ch + NS - 2 < p.nchunks - 1 ? ch + NS - 2 : p.nchunks - 1) - ch;
-    wait_vm_at_most(later * dp.count);
+    if (FAST || ch + NS - 2 < nchunks - 1) wait_vm_at_most(wait_n);
+    else wait_vm_at_most((nchunks - 1 - ch) * dp.count);
     lds_barrier();
-    // this iteration's DMA, one instruction per phase
-    const bool dma_now = ch + NS - 1 < p.nchunks;
-    float* dstage = stages + ((ch + NS - 1) % NS) * p.stage_floats;
-    if (dma_now) dma_stage_part<R, REV, MD>(p, in, dp, ch + NS - 1, dstage, lane, 0, 1);
+    const float* sg = stages + slot * sfl;
+    float* dstage = stages + dslot * sfl;
+    const int dch = ch + NS - 1;  // the chunk this iteration's DMA fetches
+    const bool dma_fast_now = FAST || dch < nfull;
+    if (!FAST && dch >= nfull && dch < nchunks) dma_clamped<R, REV>(p, in, dp, dch, dstage, lane);
 
-    const float* sg = stages + (ch % NS) * p.stage_floats;
-    // ---- rotated q/k rows of this n-tile
+    // ---- q/k rows of this n-tile (LDS reads in flight during the state update)
     const f4 q = ld4(sg + (nt * 64 + lane) * 4);
     const f4 k = ld4(sg + off_k + (nt * 64 + lane) * 4);
     f4 qp = {0.0f, 0.0f, 0.0f, 0.0f}, kp = qp, cs, sn;
+    if (MIMO) {
+      const int pl = ((m0 >> 4) * 64 + ((m0 & 15) >> 2) * 16 + li) * 4;
+      qp = ld4(sg + pl);
+      kp = ld4(sg + off_k + pl);
+    }
+    if (!ANG) {
+      if (MIMO) {
+        const int u4 = (lo ? n0 : n0 - half) >> 2;
+        cs = ld4(sg + off_cs + (u4 * T + step_i) * 4);
+        sn = ld4(sg + off_sn + (u4 * T + step_i) * 4);
+      } else {
+        const int o = ((2 * nt + (lj >> 1)) * T + li) * 4 + 2 * (lj & 1);
+        const f2 c2 = ld2(sg + off_cs + o), s2 = ld2(sg + off_sn + o);
+        cs = f4{c2[0], c2[1], 0.0f, 0.0f};
+        sn = f4{s2[0], s2[1], 0.0f, 0.0f};
+      }
+    }
+    // ---- the deferred state update of chunk ch-1: S = e^{c_last} S + K^T diag(w) X
+#pragma unroll
+    for (int j = 0; j < PT; ++j) {
+      f4 acc = S[j] * etot;
+#pragma unroll
+      for (int m = 0; m < 4; ++m) acc = mfma(kc[m], wx[j][m], acc);
+      S[j] = acc;
+    }
+    if (dma_fast_now) dma_part(dr, dstage, 0, 1);
+    // ---- rotated q/k rows
     if (ANG) {
       // pairs 4u4 .. 4u4+3 of the lane (MIMO) or 2 at 8nt + 2lj (SISO); past nang 0
       const int u4 = MIMO ? (lo ? n0 : n0 - half) >> 2 : 2 * nt + (lj >> 1);
@@ -658,63 +756,68 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 2)) m3_chunk_kernel(M3K p) {
         cs = f4{c[0], c[1], 0.0f, 0.0f};
         sn = f4{sv[0], sv[1], 0.0f, 0.0f};
       }
-      if (MIMO) {
-        const int pl = ((m0 >> 4) * 64 + ((m0 & 15) >> 2) * 16 + li) * 4;
-        qp = ld4(sg + pl);
-        kp = ld4(sg + off_k + pl);
-      }
-    } else if (MIMO) {
-      const int pl = ((m0 >> 4) * 64 + ((m0 & 15) >> 2) * 16 + li) * 4;
-      qp = ld4(sg + pl);
-      kp = ld4(sg + off_k + pl);
-      const int u4 = (lo ? n0 : n0 - half) >> 2;
-      cs = ld4(sg + off_cs + (u4 * T + step_i) * 4);
-      sn = ld4(sg + off_sn + (u4 * T + step_i) * 4);
-    } else {
-      const int o = ((2 * nt + (lj >> 1)) * T + li) * 4 + 2 * (lj & 1);
-      const f2 c2 = ld2(sg + off_cs + o), s2 = ld2(sg + off_sn + o);
-      cs = f4{c2[0], c2[1], 0.0f, 0.0f};
-      sn = f4{s2[0], s2[1], 0.0f, 0.0f};
     }
     const f4 qr = rope<MIMO>(q, qp, bq, bqp, cs, sn, lo);
     const f4 kr = rope<MIMO>(k, kp, bk, bkp, cs, sn, lo);
     kr_last = kr;
-    if (dma_now) dma_stage_part<R, REV, MD>(p, in, dp, ch + NS - 1, dstage, lane, 1, 2);
+    if (dma_fast_now) dma_part(dr, dstage, 1, 2);
     // ---- partial G^T, and partial Q S0^T per slice
+    const int par = ch & 1;
     {
       f4 gp = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int r = 0; r < 4; ++r) gp = mfma(kr[r], qr[r], gp);
-      *reinterpret_cast<f4*>(gbuf + (ch & 1) * kMaxWaves * 256 + (nt * 64 + lane) * 4) = gp;
+      *reinterpret_cast<f4*>(gw + par * kMaxWaves * 256) = gp;
     }
-    if (dma_now) dma_stage_part<R, REV, MD>(p, in, dp, ch + NS - 1, dstage, lane, 2, 3);
+    // K transposed through LDS: the operand of this chunk's (deferred) state update.
+    // SISO: in this wave's own q piece of the stage (read above; no other wave reads
+    // it), rows of 16 floats, with the reduction index s = lj + 4m so that the column
+    // reads meet no bank conflict. MIMO, whose partner pieces other waves read: in a
+    // tile of the wave's own.
+    float* const kq = stages + slot * sfl + nt * 256;
+    *reinterpret_cast<f4*>(KQ ? kq + li * 16 + 4 * lj : ktw) = kr;
+    if (dma_fast_now) dma_part(dr, dstage, 2, 3);
 #pragma unroll
     for (int j = 0; j < PT; ++j) {
       f4 yp = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int r = 0; r < 4; ++r) yp = mfma(qr[r], S[j][r], yp);
-      *reinterpret_cast<f4*>(ybuf + (((ch & 1) * PT + j) * kMaxWaves + nt) * 256 + lane * 4) =
-          yp;
+      *reinterpret_cast<f4*>(yw + ((par * PT + j) * kMaxWaves) * 256) = yp;
     }
-    if (dma_now) dma_stage_part<R, REV, MD>(p, in, dp, ch + NS - 1, dstage, lane, 3, 4);
-    // ---- K transpose, then S = e^{c_last} S + K^T diag(w) X per slice
-    *reinterpret_cast<f4*>(kt + li * kKtStride + 4 * lj) = kr;
-    float kc[4];
 #pragma unroll
-    for (int m = 0; m < 4; ++m) kc[m] = kt[(4 * lj + m) * kKtStride + li];
-    const f4 w = ld4(sg + off_rec + kRecW + 4 * lj);
-    const float etot = sg[off_rec + kRecEtot];
+    for (int m = 0; m < 4; ++m) kc[m] = KQ ? kq[(lj + 4 * m) * 16 + li] : ktr[m * kKtStride];
+    {
+      f4 w;
+      if (KQ) {
 #pragma unroll
-    for (int j = 0; j < PT; ++j) {
-      f4 acc = S[j] * etot;
-#pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        const float x = sg[off_v + ((4 * lj + m) / R) * 16 * PT + j * 16 + li] * psi[j][m];
-        acc = mfma(kc[m], w[m] * x, acc);
+        for (int m = 0; m < 4; ++m) w[m] = sg[off_rec + kRecW + lj + 4 * m];
+      } else {
+        w = ld4(sg + off_rec + kRecW + 4 * lj);
       }
-      S[j] = acc;
+      etot = sg[off_rec + kRecEtot];
+#pragma unroll
+      for (int j = 0; j < PT; ++j)
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          const int srow = KQ ? lj + 4 * m : (4 * lj + m) / R;  // the step of row s
+          wx[j][m] = w[m] * (sg[off_v + srow * 16 * PT + j * 16 + li] * psi[j][m]);
+        }
     }
-    if (dma_now) dma_stage_part<R, REV, MD>(p, in, dp, ch + NS - 1, dstage, lane, 4, MD);
+    if (dma_fast_now) dma_part(dr, dstage, 3, MD);
+    slot = slot + 1 == NS ? 0 : slot + 1;
+    dslot = dslot + 1 == NS ? 0 : dslot + 1;
+  };
+  const int nmain = nfull > NS - 1 ? nfull - (NS - 1) : 0;  // chunks with whole-chunk DMA
+  int ch = 0;
+  for (; ch < nmain; ++ch) chunk(ch, std::true_type{});
+  for (; ch < nchunks; ++ch) chunk(ch, std::false_type{});
+  // the last chunk's state update
+#pragma unroll
+  for (int j = 0; j < PT; ++j) {
+    f4 acc = S[j] * etot;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) acc = mfma(kc[m], wx[j][m], acc);
+    S[j] = acc;
   }
   lds_barrier();
 
@@ -737,8 +840,9 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 2)) m3_chunk_kernel(M3K p) {
 
 size_t chunk_lds_bytes(const M3K& k, int pt, int ns) {
   const int WN = k.dqk / 16;
+  const size_t kt = k.psi ? (size_t)WN * 16 * kKtStride : 0;  // SISO: in the stage
   return sizeof(float) * ((size_t)ns * k.stage_floats + (size_t)2 * kMaxWaves * 256 +
-                          (size_t)2 * pt * kMaxWaves * 256 + (size_t)WN * 16 * kKtStride);
+                          (size_t)2 * pt * kMaxWaves * 256 + kt);
 }
 
 template <int R, bool MIMO, int PT, bool ZOWN, int MD>
