@@ -541,14 +541,20 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 2)) m3_chunk_kernel(M3K p) {
                       (p.out_tm ? (((long long)bi * L + t0) * H + h) * dv
                                 : (((long long)bi * H + h) * L + t0) * dv);
     Stash st = {};
-    auto epilogue = [&](int ch) {
+    const bool has_z = p.z != nullptr;
+    const int nchunks = p.nchunks, sfl = p.stage_floats;
+    const long long chstep = (REV ? -(long long)T : (long long)T) * ostep;  // per chunk
+    float* orow = out_lane;  // the lane's first output of the chunk being finished
+    // FULL: every row of the chunk lies inside the sequence (all chunks but the last)
+    auto epilogue = [&](int ch, auto full) {
+      constexpr bool FULL = decltype(full)::value;
+      auto valid = [&](int r) { return FULL || ch * T + (4 * lj + r) / R < L; };
       // the other traversal's output, under accumulation (loaded first, used last)
       float prev[4] = {0.0f, 0.0f, 0.0f, 0.0f};
       if constexpr (ACC) {
-        const float* prow = out_lane + (REV ? -(long long)ch : (long long)ch) * T * ostep;
 #pragma unroll
         for (int r = 0; r < 4; r += R)
-          if (ch * T + (4 * lj + r) / R < L) prev[r] = prow[(REV ? -(r / R) : r / R) * ostep];
+          if (valid(r)) prev[r] = orow[(REV ? -(r / R) : r / R) * ostep];
       }
       const float* gb = gbuf + (ch & 1) * kMaxWaves * 256;
       const float* yb = ybuf + ((ch & 1) * PT + ej) * kMaxWaves * 256;
@@ -569,38 +575,45 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 2)) m3_chunk_kernel(M3K p) {
       f4 Y = ys[0] * st.ec;  // lane holds Y[row = 4lj + r][p], the inter-chunk part
 #pragma unroll
       for (int m = 0; m < 4; ++m) Y = mfma(G[m], st.x[m], Y);
-      float* orow = out_lane + (REV ? -(long long)ch : (long long)ch) * T * ostep;
 #pragma unroll
       for (int r = 0; r < 4; r += R) {
-        if (ch * T + (4 * lj + r) / R < L) {
+        if (valid(r)) {
           float acc = prev[r];
 #pragma unroll
           for (int rr = 0; rr < R; ++rr) {
             float term = Y[r + rr] + dskip * st.x[r + rr];
-            if (p.z) term *= silu_fast(st.z[r] * zeta[r + rr]);
+            if (has_z) term *= silu_fast(st.z[r] * zeta[r + rr]);
             acc = fmaf(phi[r + rr], term, acc);
           }
           orow[(REV ? -(r / R) : r / R) * ostep] = acc;
         }
       }
+      orow += chstep;
     };
-    for (int ch = 0; ch < p.nchunks; ++ch) {
-      lds_barrier();  // stage ch landed, partials of chunk ch-1 written
-      if (ch > 0) epilogue(ch - 1);
-      const float* sg = stages + (ch % NS) * p.stage_floats;
+    // what the epilogue of a chunk needs from its stage
+    auto stash = [&](const float* sg) {
       st.m = ld4(sg + off_rec + kRecM + li * 16 + 4 * lj);
       st.ec = ld4(sg + off_rec + kRecEc + 4 * lj);
 #pragma unroll
       for (int m = 0; m < 4; ++m)
         st.x[m] = sg[off_v + ((4 * lj + m) / R) * 16 * PT + ej * 16 + li] * psi[m];
-      if (p.z) {
+      if (has_z) {
 #pragma unroll
         for (int r = 0; r < 4; r += R)
           st.z[r] = sg[off_z + ((4 * lj + r) / R) * 16 * PT + ej * 16 + li];
       }
+    };
+    lds_barrier();  // stage 0 landed
+    stash(stages);
+    int slot = 0;
+    for (int ch = 1; ch < nchunks; ++ch) {
+      slot = slot + 1 == NS ? 0 : slot + 1;
+      lds_barrier();  // stage ch landed, partials of chunk ch-1 written
+      epilogue(ch - 1, std::true_type{});
+      stash(stages + slot * sfl);
     }
     lds_barrier();
-    epilogue(p.nchunks - 1);
+    epilogue(nchunks - 1, std::false_type{});
     return;
   }
 
@@ -716,12 +729,11 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 2)) m3_chunk_kernel(M3K p) {
     }
     // ---- the deferred state update of chunk ch-1: S = e^{c_last} S + K^T diag(w) X
 #pragma unroll
-    for (int j = 0; j < PT; ++j) {
-      f4 acc = S[j] * etot;
+    for (int j = 0; j < PT; ++j) S[j] *= etot;
 #pragma unroll
-      for (int m = 0; m < 4; ++m) acc = mfma(kc[m], wx[j][m], acc);
-      S[j] = acc;
-    }
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+      for (int j = 0; j < PT; ++j) S[j] = mfma(kc[m], wx[j][m], S[j]);
     if (dma_fast_now) dma_part(dr, dstage, 0, 1);
     // ---- rotated q/k rows
     if (ANG) {
@@ -761,29 +773,14 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 2)) m3_chunk_kernel(M3K p) {
     const f4 kr = rope<MIMO>(k, kp, bk, bkp, cs, sn, lo);
     kr_last = kr;
     if (dma_fast_now) dma_part(dr, dstage, 1, 2);
-    // ---- partial G^T, and partial Q S0^T per slice
-    const int par = ch & 1;
-    {
-      f4 gp = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-      for (int r = 0; r < 4; ++r) gp = mfma(kr[r], qr[r], gp);
-      *reinterpret_cast<f4*>(gw + par * kMaxWaves * 256) = gp;
-    }
-    // K transposed through LDS: the operand of this chunk's (deferred) state update.
-    // SISO: in this wave's own q piece of the stage (read above; no other wave reads
-    // it), rows of 16 floats, with the reduction index s = lj + 4m so that the column
-    // reads meet no bank conflict. MIMO, whose partner pieces other waves read: in a
-    // tile of the wave's own.
+    // ---- K transposed through LDS: the operand of this chunk's (deferred) state
+    // update. SISO: in this wave's own q piece of the stage (read above; no other wave
+    // reads it), rows of 16 floats, with the reduction index s = lj + 4m so that the
+    // column reads meet no bank conflict. MIMO, whose partner pieces other waves read:
+    // in a tile of the wave's own. The round trip and the reads of w x overlap the
+    // MFMA chains below.
     float* const kq = stages + slot * sfl + nt * 256;
     *reinterpret_cast<f4*>(KQ ? kq + li * 16 + 4 * lj : ktw) = kr;
-    if (dma_fast_now) dma_part(dr, dstage, 2, 3);
-#pragma unroll
-    for (int j = 0; j < PT; ++j) {
-      f4 yp = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-      for (int r = 0; r < 4; ++r) yp = mfma(qr[r], S[j][r], yp);
-      *reinterpret_cast<f4*>(yw + ((par * PT + j) * kMaxWaves) * 256) = yp;
-    }
 #pragma unroll
     for (int m = 0; m < 4; ++m) kc[m] = KQ ? kq[(lj + 4 * m) * 16 + li] : ktr[m * kKtStride];
     {
@@ -803,6 +800,23 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 2)) m3_chunk_kernel(M3K p) {
           wx[j][m] = w[m] * (sg[off_v + srow * 16 * PT + j * 16 + li] * psi[j][m]);
         }
     }
+    // ---- partial G^T, and partial Q S0^T per slice: 1 + PT chains, interleaved
+    const int par = ch & 1;
+    f4 gp = {0.0f, 0.0f, 0.0f, 0.0f};
+    f4 yp[PT];
+#pragma unroll
+    for (int j = 0; j < PT; ++j) yp[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      gp = mfma(kr[r], qr[r], gp);
+#pragma unroll
+      for (int j = 0; j < PT; ++j) yp[j] = mfma(qr[r], S[j][r], yp[j]);
+    }
+    if (dma_fast_now) dma_part(dr, dstage, 2, 3);
+    *reinterpret_cast<f4*>(gw + par * kMaxWaves * 256) = gp;
+#pragma unroll
+    for (int j = 0; j < PT; ++j)
+      *reinterpret_cast<f4*>(yw + ((par * PT + j) * kMaxWaves) * 256) = yp[j];
     if (dma_fast_now) dma_part(dr, dstage, 3, MD);
     slot = slot + 1 == NS ? 0 : slot + 1;
     dslot = dslot + 1 == NS ? 0 : dslot + 1;
@@ -813,12 +827,11 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 2)) m3_chunk_kernel(M3K p) {
   for (; ch < nchunks; ++ch) chunk(ch, std::false_type{});
   // the last chunk's state update
 #pragma unroll
-  for (int j = 0; j < PT; ++j) {
-    f4 acc = S[j] * etot;
+  for (int j = 0; j < PT; ++j) S[j] *= etot;
 #pragma unroll
-    for (int m = 0; m < 4; ++m) acc = mfma(kc[m], wx[j][m], acc);
-    S[j] = acc;
-  }
+  for (int m = 0; m < 4; ++m)
+#pragma unroll
+    for (int j = 0; j < PT; ++j) S[j] = mfma(kc[m], wx[j][m], S[j]);
   lds_barrier();
 
   if (p.last_state) {

@@ -39,6 +39,24 @@ sys.path.insert(0, str(ROOT))
 METRIC = "selective-scan GB/s (% of ~8 TB/s HBM) + Mamba-1 130m prefill tokens/s"
 HBM_PEAK_GBS = 8000.0
 SHAPE = dict(batch=8, dim=1536, length=2048, state=16)
+# The GPU's clocks ramp up from idle over tens of milliseconds: every timed region
+# follows at least this much wall time of the same calls.
+WARM_S = 0.5
+
+
+def warm_up(fn, n):
+    """`n` untimed calls fn(i), continued until the GPU has run them for WARM_S seconds
+    (synchronising every 8 calls, so that the wall time is the GPU's)."""
+    import torch
+
+    t0 = time.perf_counter()
+    i = 0
+    while i < n or time.perf_counter() - t0 < WARM_S:
+        fn(i)
+        i += 1
+        if i % 8 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
 
 
 def parse():
@@ -98,9 +116,7 @@ def bench_scan(args, dev):
                       x["z"].data_ptr(), x["delta_bias"].data_ptr(), True, "auto", "auto",
                       o.data_ptr(), l.data_ptr(), 0, reverse=False, stream=stream.cuda_stream)
 
-    for i in range(args.warmup):
-        step(i)
-    torch.cuda.synchronize()
+    warm_up(step, args.warmup)
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     start.record(stream)
@@ -253,9 +269,7 @@ def bench_config(name, dev, steps, warmup):
             return arm_scan.ss2d_scan(t["u"], t["delta"], t["A"], t["B4"], t["C4"], D=t["D"],
                                       z=t["z"], delta_softplus=False, merge="sum",
                                       per_direction=True, return_last_state=True)
-    for _ in range(warmup):
-        call()
-    torch.cuda.synchronize()
+    warm_up(lambda i: call(), warmup)
     stream = torch.cuda.current_stream(dev)
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record(stream)
@@ -279,8 +293,7 @@ def bench_config(name, dev, steps, warmup):
             return arm_scan.mamba3_mimo_scan(*[t[k] for k in K], t["psi"], t["zeta"],
                                              t["phi"], cos=cos, sin=sin,
                                              return_last_state=True)
-        for _ in range(warmup):
-            unfused()
+        warm_up(lambda i: unfused(), warmup)
         start.record(stream)
         for _ in range(steps):
             unfused()
@@ -321,8 +334,7 @@ def bench_config(name, dev, steps, warmup):
                 return m.out_proj(proj[..., :m.d_inner])
         for key, fn in (("torch_front_end_ms_per_call", torch_route),
                         ("gemms_only_ms_per_call", gemms)):
-            for _ in range(warmup):
-                fn()
+            warm_up(lambda i: fn(), warmup)
             start.record(stream)
             for _ in range(steps):
                 fn()
@@ -344,8 +356,7 @@ def bench_config(name, dev, steps, warmup):
             return arm_scan.mamba3_scan(*[t[k] for k in K], cos=t["cos"], sin=t["sin"])
         for key, fn in (("pair_route_ms_per_call", pair_route),
                         ("causal_ms_per_call", causal)):
-            for _ in range(warmup):
-                fn()
+            warm_up(lambda i: fn(), warmup)
             start.record(stream)
             for _ in range(steps):
                 fn()
