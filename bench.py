@@ -619,6 +619,18 @@ def bench_cpu(seconds):
                      "batch row of the step; softplus+bias, D, z)", seconds, 1000)
 
 
+def issue_floor(ms_per_step):
+    """The step's fp32 issue floor: one v_exp_f32 (two VALU slots, 8 cycles per wave64)
+    and five VALU ops (4 cycles each) per (step, state), spread over MI355X's 1024 SIMDs
+    at 2.4 GHz. The kernel is bound by this issue, not by HBM; `frac` is floor / step."""
+    b, d, L, n = SHAPE["batch"], SHAPE["dim"], SHAPE["length"], SHAPE["state"]
+    cycles = b * d * L * n / 64 * (8 + 5 * 4) / 1024
+    floor_ms = cycles / 2.4e9 * 1e3
+    return {"unit": "ms", "value": round(floor_ms, 4), "frac": round(floor_ms / ms_per_step, 4),
+            "model": "(v_exp_f32 8 + 5 VALU x 4) cycles per (step, state) wave-element, "
+                     "1024 SIMDs, 2.4 GHz"}
+
+
 def traffic_from_profiles():
     """HBM bytes per launch measured by rocprofv3 counters (profiles/), or None."""
     p = ROOT / "profiles" / "m1_scan_ns_traffic.json"
@@ -688,7 +700,8 @@ def main():
                    "bytes_per_step": r["bytes"]},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": traffic_from_profiles()},
+                     "traffic": traffic_from_profiles(),
+                     "issue_floor": issue_floor(r["ms_per_step"])},
         "prefill": prefill,
         **({"decode": decode} if decode is not None else {}),
         "other_configs": configs,
