@@ -13,6 +13,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "../../include/arm_scan_hip.h"
@@ -81,22 +82,41 @@ int run(hipError_t e, const char* where) {
 
 namespace armscan {
 
+// Per-call scratch (gate records, SS2D planes, segment maps, cos/sin) comes from a
+// memory pool the library owns, one per device, created on first use and kept until
+// the process ends. Its release threshold keeps freed blocks for the next call, so a
+// steady stream of calls allocates from memory already mapped; the device's default
+// pool, which the caller or torch may use, keeps its own settings.
 hipError_t stream_alloc(void** p, size_t bytes, hipStream_t st) {
-  static std::atomic<unsigned long long> pools_set{0};  // one bit per device (< 64)
+  constexpr int kMaxDevices = 64;
+  static std::atomic<hipMemPool_t> pools[kMaxDevices] = {};
+  static std::mutex create_mu;
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
-  const unsigned long long bit = 1ull << (dev & 63);
-  if (!(pools_set.load() & bit)) {
-    hipMemPool_t pool;
-    if (hipDeviceGetDefaultMemPool(&pool, dev) == hipSuccess) {
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  hipMemPool_t pool = pools[dev].load(std::memory_order_acquire);
+  if (pool == nullptr) {
+    std::lock_guard<std::mutex> lock(create_mu);
+    pool = pools[dev].load(std::memory_order_acquire);
+    if (pool == nullptr) {
+      hipMemPoolProps props{};
+      props.allocType = hipMemAllocationTypePinned;
+      props.handleTypes = hipMemHandleTypeNone;
+      props.location.type = hipMemLocationTypeDevice;
+      props.location.id = dev;
+      e = hipMemPoolCreate(&pool, &props);
+      if (e != hipSuccess) return e;
       uint64_t keep = UINT64_MAX;
-      // best effort: without it freed scratch returns to the device between calls
-      (void)hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep);
+      e = hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep);
+      if (e != hipSuccess) {
+        (void)hipMemPoolDestroy(pool);
+        return e;
+      }
+      pools[dev].store(pool, std::memory_order_release);
     }
-    pools_set.fetch_or(bit);
   }
-  return hipMallocAsync(p, bytes, st);
+  return hipMallocFromPoolAsync(p, bytes, pool, st);
 }
 
 }  // namespace armscan
