@@ -625,7 +625,9 @@ __device__ __forceinline__ void tile_states(const float* tile, int n0, int N, in
 // The rows of block `blk` (16 per block) through one traversal. SIO 0: z and out
 // (batch, dim, len) contiguous; 1: strided (p.zs_*, p.os_*), z read with buffer
 // loads and out written with buffer stores; 2: strided with unit channel stride,
-// z and out staged through LDS.
+// z and out staged through LDS; 3: as 2, with u staged through the same LDS buffer
+// (its own compile-time case, so that the per-lane u loads of 1 and 2 hold no
+// registers in it).
 template <int I, bool REV, int SIO, bool SEG = false>
 __device__ __forceinline__ void tile_rows(const M1Kern& p, long long blk, int seg = 0) {
   constexpr int LPR = 16, RPW = 4;
@@ -634,7 +636,7 @@ __device__ __forceinline__ void tile_rows(const M1Kern& p, long long blk, int se
   extern __shared__ __attribute__((aligned(16))) float s_lds[];
   float* tiles = s_lds;                                  // [2][G::FLOATS]
   float* zbuf = s_lds + 2 * G::FLOATS;                   // SIO: [256][16] z stage
-  float* small = zbuf + (SIO == 2 ? kZStageFloats : 0);  // carry, A*log2e, zeros
+  float* small = zbuf + (SIO >= 2 ? kZStageFloats : 0);  // carry, A*log2e, zeros
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -703,7 +705,7 @@ __device__ __forceinline__ void tile_rows(const M1Kern& p, long long blk, int se
     }
   };
 
-  // SIO 2: chunk c's z stage is issued once chunk c-1's outputs have left the stage
+  // SIO 2, 3: chunk c's z stage is issued once chunk c-1's outputs have left the stage
   // (a sync), lands by chunk c's first tile sync (ng >= 2) and is read after chunk
   // c's last tile's states.
   const int d0 = (int)(blk * (kWavesPerBlock * RPW) % p.dim);  // the block's first channel
@@ -711,8 +713,8 @@ __device__ __forceinline__ void tile_rows(const M1Kern& p, long long blk, int se
     issue_z_stage<REV>(zbuf, p.z + bib * p.zs_b, p.zs_t, L, c * CH, d0, wave, lane);
   };
   // u through the stage too: per chunk, u's DMA, its read, then z's DMA
-  const bool ustage = SIO == 2 && p.u_dma;
-  if (SIO == 2 && p.z && ce > cb && !ustage) z_stage(cb);
+  constexpr bool ustage = SIO == 3;
+  if (SIO == 2 && p.z && ce > cb) z_stage(cb);
 
   long long k = 0;  // tile counter
   for (long long c = cb; c < ce; ++c) {
@@ -723,7 +725,7 @@ __device__ __forceinline__ void tile_rows(const M1Kern& p, long long blk, int se
       float dd[I], uu[I];
       load_block<I, REV, true>(drow, L, sb, 0.0f, dd, L);
       if (ustage) {
-        if constexpr (SIO == 2) {
+        if constexpr (SIO == 3) {
           // the block's 16 channels of u, 64-byte runs, land with delta's loads; the
           // stage is free (the previous chunk's outputs have left it) and z's DMA
           // follows once every lane has read its u
@@ -760,7 +762,7 @@ __device__ __forceinline__ void tile_rows(const M1Kern& p, long long blk, int se
         issue_tile<I>(tiles + ((k + 1) & 1) * G::FLOATS, Bg, Cg, L, mem0(cn),
                       qn * kTileStates, N, wave, lane);
       }
-      if (SIO != 2 && zrow && q + 1 == ng) {
+      if (SIO < 2 && zrow && q + 1 == ng) {
         if (SIO == 1) {
           const long long tlo = REV ? L - sb - I : sb;  // the block's lowest memory step
           load_block_strided<I, REV>(slab_rsrc(p.z + bib * p.zs_b, p.z_bytes),
@@ -772,10 +774,10 @@ __device__ __forceinline__ void tile_rows(const M1Kern& p, long long blk, int se
       tile_states<I, REV>(tiles + (k & 1) * G::FLOATS, q * kTileStates, N, j, a2s, cbase,
                           carry, (last_chunk && p.last) ? p.last + row * N : nullptr, dt, du,
                           sdt, y);
-      if (SIO == 2 && zrow && q + 1 == ng) {
+      if (SIO >= 2 && zrow && q + 1 == ng) {
         // after the states (no registers held through them), before the sync after
         // which the outputs overwrite it
-        static_assert(SIO != 2 || I == 16, "the stage holds 16 steps per lane block");
+        static_assert(SIO < 2 || I == 16, "the stage holds 16 steps per lane block");
         read_z_stage(zbuf, j, wave, rw, zz);
       }
       tile_sync();
@@ -784,7 +786,7 @@ __device__ __forceinline__ void tile_rows(const M1Kern& p, long long blk, int se
 #pragma unroll
       for (int i = 0; i < I; ++i) y[i] *= silu_fast(zz[i]);
     }
-    if (SIO == 2) {
+    if (SIO >= 2) {
       write_out_stage(zbuf, j, wave, rw, y);
       lds_barrier();
       store_out_stage<REV>(zbuf, p.out + bib * p.os_b, p.os_t, L, c * CH, d0, wave, lane);
@@ -979,7 +981,7 @@ hipError_t launch_tile(const M1Kern& k, hipStream_t st) {
     if (e != hipSuccess) return e;
   }
   const size_t lds =
-      sizeof(float) * (2 * (size_t)Tile<I>::FLOATS + (SIO == 2 ? kZStageFloats : 0) +
+      sizeof(float) * (2 * (size_t)Tile<I>::FLOATS + (SIO >= 2 ? kZStageFloats : 0) +
                        (2 * (size_t)RPB + 1) * k.N);
   if (segs > 1)
     hipLaunchKernelGGL((m1_tile_kernel<I, REV, SIO, true>), dim3((unsigned)(blocks * segs)),
@@ -1191,8 +1193,10 @@ hipError_t m1_scan_chunked(const M1Problem& pr, hipStream_t st) {
       k.u_dma = k.z_dma && k.us_d == 1 && k.us_t % 4 == 0 && k.us_b % 4 == 0 &&
                 aligned16(pr.u);
     }
-    return k.z_dma ? run_tile<2>(k, rev, pr.scratch, pr.scratch_bytes, st)
-                   : run_tile<1>(k, rev, pr.scratch, pr.scratch_bytes, st);
+    if (k.z_dma)
+      return k.u_dma ? run_tile<3>(k, rev, pr.scratch, pr.scratch_bytes, st)
+                     : run_tile<2>(k, rev, pr.scratch, pr.scratch_bytes, st);
+    return run_tile<1>(k, rev, pr.scratch, pr.scratch_bytes, st);
   }
   // the tiled path needs every 16-row block inside one batch/group and 16-byte rows
   const bool tiled = vec && pr.dim % 16 == 0 && (pr.dim / pr.groups) % 16 == 0;
