@@ -14,8 +14,8 @@
 //
 // Two kernels:
 //  * m3_gates_kernel, one lane per (sequence, chunk, row): the chunk's gate record
-//    {M, e^c, w, e^{c_last}} (1168 bytes per chunk), so that the main kernel does
-//    no transcendental work for the decays.
+//    {M, e^c, w, e^{c_last}} (1168 bytes per chunk at rank 1, 112 at rank 4), so that
+//    the main kernel does no transcendental work for the decays.
 //  * m3_chunk_kernel: one block per (sequence, PT 16-column slices of dv), one
 //    wave per 16-column slice of dqk (an "n-tile"). A wave keeps the PT 16x16
 //    pieces S[slice][n-tile] in MFMA registers and per chunk computes
@@ -57,15 +57,22 @@ __device__ __forceinline__ f4 mfma(float a, float b, f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
-// Gate record of one (sequence, chunk), in floats.
-constexpr int kRecM = 0;         // M[i][s], 16 x 16
-constexpr int kRecEc = 256;      // e^{c_i}
-constexpr int kRecW = 272;       // w_s
-constexpr int kRecEtot = 288;    // e^{c_last}
-constexpr int kRecFloats = 292;  // + 3 floats of padding: whole 16-byte pieces
-// With the angle pre-pass fused: pi * dt of each row follows (16 floats).
-constexpr int kRecPdt = 292;
-constexpr int kRecFloatsAng = 308;
+// Gate record of one (sequence, chunk) of T = 16/R steps, in floats. The rows of a
+// step share its gates, so M is kept over step pairs, e^{c} and w per step:
+//   M[step_i][step_s] (T x T), e^{c} (T), w (T), e^{c_last}, padding to whole
+//   16-byte pieces; with the angle pre-pass fused, pi * dt of each of the 16 rows.
+// Rank 1: 292 floats (1168 bytes), rank 2: 84, rank 4: 28 (112 bytes).
+template <int R> struct Rec {
+  static constexpr int T = 16 / R;
+  static constexpr int M = 0, Ec = T * T, W = Ec + T, Etot = W + T;
+  static constexpr int Floats = (Etot + 1 + 3) & ~3;
+  static constexpr int Pdt = Floats, FloatsAng = Floats + 16;
+};
+constexpr int rec_floats(int R, bool ang) {
+  return R == 1 ? (ang ? Rec<1>::FloatsAng : Rec<1>::Floats)
+                : R == 2 ? (ang ? Rec<2>::FloatsAng : Rec<2>::Floats)
+                         : (ang ? Rec<4>::FloatsAng : Rec<4>::Floats);
+}
 
 constexpr int kMaxWaves = 8;   // n-tiles per block: dqk <= 128
 constexpr int kKtStride = 20;  // floats per row of a wave's K transpose tile
@@ -88,7 +95,7 @@ struct M3K {
   // replace cos/sin (n_cs = 0) in n_ang DMA instructions per stage
   const float* ang;
   int nang, n_ang;
-  int rec_floats;  // kRecFloats, or kRecFloatsAng with pi * dt per row
+  int rec_floats;  // Rec<R>::Floats, or Rec<R>::FloatsAng with pi * dt per row
   long long vb, zb, ab, ah;  // element strides: v, z per batch; angles per batch, head
   int vt, zt, at;            // and per step
   // SISO: no same-step term (gamma on M's diagonal, D x) and out += the result
@@ -142,14 +149,24 @@ __global__ void __launch_bounds__(256) m3_gates_kernel(M3K p, int reverse) {
     m[s] = step_s < step ? fexp(c - cs) * ss : (step_s == step && !p.accum ? gamma : 0.0f);
   }
   if (!valid) return;
+  using RC = Rec<R>;
   float* rec = p.rec + cidx * p.rec_floats;
-  if (p.rec_floats > kRecFloats) rec[kRecPdt + row] = pdt;  // 0 past the end: theta holds
-  f4* mrow = reinterpret_cast<f4*>(rec + kRecM + row * 16);
+  if (p.rec_floats > RC::Floats) rec[RC::Pdt + row] = pdt;  // 0 past the end: theta holds
+  if (row % R == 0) {  // the step's first row writes the step's entries
+    if constexpr (R == 1) {
+      f4* mrow = reinterpret_cast<f4*>(rec + RC::M + row * 16);
 #pragma unroll
-  for (int q = 0; q < 4; ++q) mrow[q] = f4{m[4 * q], m[4 * q + 1], m[4 * q + 2], m[4 * q + 3]};
-  rec[kRecEc + row] = fexp(c);
-  rec[kRecW + row] = fexp(clast - c) * scale;
-  if (row < 4) rec[kRecEtot + row] = row == 0 ? fexp(clast) : 0.0f;
+      for (int q = 0; q < 4; ++q)
+        mrow[q] = f4{m[4 * q], m[4 * q + 1], m[4 * q + 2], m[4 * q + 3]};
+    } else {
+#pragma unroll
+      for (int q = 0; q < RC::T; ++q) rec[RC::M + step * RC::T + q] = m[q * R];
+    }
+    rec[RC::Ec + step] = fexp(c);
+    rec[RC::W + step] = fexp(clast - c) * scale;
+  }
+  // e^{c_last}, then zeros to the end of the last 16-byte piece
+  if (row < RC::Floats - RC::Etot) rec[RC::Etot + row] = row == 0 ? fexp(clast) : 0.0f;
 }
 
 // ---------------------------------------------------------------------------
@@ -592,8 +609,17 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 2)) m3_chunk_kernel(M3K p) {
     };
     // what the epilogue of a chunk needs from its stage
     auto stash = [&](const float* sg) {
-      st.m = ld4(sg + off_rec + kRecM + li * 16 + 4 * lj);
-      st.ec = ld4(sg + off_rec + kRecEc + 4 * lj);
+      using RC = Rec<R>;
+      if constexpr (R == 1) {
+        st.m = ld4(sg + off_rec + RC::M + li * 16 + 4 * lj);
+        st.ec = ld4(sg + off_rec + RC::Ec + 4 * lj);
+      } else {  // rows 4lj + r lie in steps (4lj + r) / R
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          st.m[r] = sg[off_rec + RC::M + (li / R) * RC::T + (4 * lj + r) / R];
+          st.ec[r] = sg[off_rec + RC::Ec + (4 * lj + r) / R];
+        }
+      }
 #pragma unroll
       for (int m = 0; m < 4; ++m)
         st.x[m] = sg[off_v + ((4 * lj + m) / R) * 16 * PT + ej * 16 + li] * psi[m];
@@ -752,7 +778,7 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 2)) m3_chunk_kernel(M3K p) {
 #pragma unroll
         for (int j = 0; j < NC; ++j)
           a[j] = have ? sg[off_ang + (u4 * T + step_i) * 4 + (li % R) * NC + j] : 0.0f;
-        fused_angles<R, NC>(a, sg[off_rec + kRecPdt + li], li, lane, carry_m, c, sv);
+        fused_angles<R, NC>(a, sg[off_rec + Rec<R>::Pdt + li], li, lane, carry_m, c, sv);
         const int src = lane - li % R;  // the step's first lane
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -764,7 +790,7 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 2)) m3_chunk_kernel(M3K p) {
         const f2 a2 = have ? ld2(sg + off_ang + (u4 * T + li) * 4 + 2 * (lj & 1)) : f2{0, 0};
         a[0] = a2[0];
         a[1] = a2[1];
-        fused_angles<R, 2>(a, sg[off_rec + kRecPdt + li], li, lane, carry, c, sv);
+        fused_angles<R, 2>(a, sg[off_rec + Rec<R>::Pdt + li], li, lane, carry, c, sv);
         cs = f4{c[0], c[1], 0.0f, 0.0f};
         sn = f4{sv[0], sv[1], 0.0f, 0.0f};
       }
@@ -785,13 +811,16 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 2)) m3_chunk_kernel(M3K p) {
     for (int m = 0; m < 4; ++m) kc[m] = KQ ? kq[(lj + 4 * m) * 16 + li] : ktr[m * kKtStride];
     {
       f4 w;
-      if (KQ) {
+      if (KQ) {  // SISO: rows lj + 4m
 #pragma unroll
-        for (int m = 0; m < 4; ++m) w[m] = sg[off_rec + kRecW + lj + 4 * m];
-      } else {
-        w = ld4(sg + off_rec + kRecW + 4 * lj);
+        for (int m = 0; m < 4; ++m) w[m] = sg[off_rec + Rec<R>::W + lj + 4 * m];
+      } else if (R == 1) {
+        w = ld4(sg + off_rec + Rec<R>::W + 4 * lj);
+      } else {  // rows 4lj + m lie in steps (4lj + m) / R
+#pragma unroll
+        for (int m = 0; m < 4; ++m) w[m] = sg[off_rec + Rec<R>::W + (4 * lj + m) / R];
       }
-      etot = sg[off_rec + kRecEtot];
+      etot = sg[off_rec + Rec<R>::Etot];
 #pragma unroll
       for (int j = 0; j < PT; ++j)
 #pragma unroll
@@ -846,7 +875,7 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 2)) m3_chunk_kernel(M3K p) {
     if (li % R == 0 && last * T + step_i == L - 1) {
       const float* sg = stages + (last % NS) * p.stage_floats;
       *reinterpret_cast<f4*>(p.last_bx + (long long)seq * dqk + n0) =
-          kr_last * sg[off_rec + kRecW + li];
+          kr_last * sg[off_rec + Rec<R>::W + li / R];
     }
   }
 }
@@ -946,7 +975,7 @@ hipError_t m3_scan_chunked(const M3Problem& pr, hipStream_t st) {
   k.zb = pr.z_strides[0]; k.zt = (int)pr.z_strides[1];
   k.zown = pr.z != nullptr && k.zt != k.vt;
   k.ab = pr.ang_strides[0]; k.at = (int)pr.ang_strides[1]; k.ah = pr.ang_strides[2];
-  k.rec_floats = pr.angles ? kRecFloatsAng : kRecFloats;
+  k.rec_floats = rec_floats((int)pr.rank, pr.angles != nullptr);
   auto plan = [&]() {
     const int T = k.steps_per_chunk;
     k.n_cs = pr.angles ? 0 : (T * (k.dqk / 8) + 63) / 64;
