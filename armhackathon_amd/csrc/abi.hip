@@ -86,36 +86,42 @@ namespace armscan {
 // memory pool the library owns, one per device, created on first use and kept until
 // the process ends. Its release threshold keeps freed blocks for the next call, so a
 // steady stream of calls allocates from memory already mapped; the device's default
-// pool, which the caller or torch may use, keeps its own settings.
+// pool, which the caller or torch may use, keeps its own settings. Where a pool cannot
+// be created, the scratch comes from the default pool as it is.
 hipError_t stream_alloc(void** p, size_t bytes, hipStream_t st) {
   constexpr int kMaxDevices = 64;
   static std::atomic<hipMemPool_t> pools[kMaxDevices] = {};
+  static std::atomic<bool> no_pool[kMaxDevices] = {};
   static std::mutex create_mu;
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
   if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
   hipMemPool_t pool = pools[dev].load(std::memory_order_acquire);
-  if (pool == nullptr) {
+  if (pool == nullptr && !no_pool[dev].load(std::memory_order_acquire)) {
     std::lock_guard<std::mutex> lock(create_mu);
     pool = pools[dev].load(std::memory_order_acquire);
-    if (pool == nullptr) {
+    if (pool == nullptr && !no_pool[dev].load(std::memory_order_relaxed)) {
       hipMemPoolProps props{};
       props.allocType = hipMemAllocationTypePinned;
       props.handleTypes = hipMemHandleTypeNone;
       props.location.type = hipMemLocationTypeDevice;
       props.location.id = dev;
-      e = hipMemPoolCreate(&pool, &props);
-      if (e != hipSuccess) return e;
       uint64_t keep = UINT64_MAX;
-      e = hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep);
-      if (e != hipSuccess) {
+      if (hipMemPoolCreate(&pool, &props) != hipSuccess) {
+        pool = nullptr;
+        (void)hipGetLastError();  // the failed creation leaves no error behind
+      } else if (hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep) !=
+                 hipSuccess) {
         (void)hipMemPoolDestroy(pool);
-        return e;
+        pool = nullptr;
+        (void)hipGetLastError();
       }
-      pools[dev].store(pool, std::memory_order_release);
+      if (pool != nullptr) pools[dev].store(pool, std::memory_order_release);
+      else no_pool[dev].store(true, std::memory_order_release);
     }
   }
+  if (pool == nullptr) return hipMallocAsync(p, bytes, st);
   return hipMallocFromPoolAsync(p, bytes, pool, st);
 }
 
