@@ -66,6 +66,9 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--prefill-steps", type=int, default=3)
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--prefill-only", choices=("scan", "scan_conv"), default=None,
+                    help="time only this patched prefill (no unpatched forward, no parity "
+                         "check): the command behind the prefill kernel trace")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--workload", choices=("m1", "m1_b1", "m1_seam", "m3_siso", "m3_mimo",
@@ -516,6 +519,14 @@ def bench_prefill(args, dev):
             torch.cuda.synchronize()
         return (time.perf_counter() - t0) / steps, logits
 
+    if args.prefill_only:
+        arm_scan.patch(conv=args.prefill_only == "scan_conv")
+        try:
+            t, _ = timed(args.prefill_steps)
+        finally:
+            arm_scan.unpatch()
+        return dict(batch=8, seq_len=2048, mode=args.prefill_only, tokens_per_s=tokens / t,
+                    ms_per_forward=t * 1e3)
     t_ref, ref = timed(1)
     scale = max(1.0, ref.abs().max().item())
     out = dict(batch=8, seq_len=2048, logits="last position only (logits_to_keep=1)",
