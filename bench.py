@@ -657,7 +657,8 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the scan shards "
-              "with no communication across rows, see DESIGN.md", file=sys.stderr)
+              "over batch and channel rows with no communication across them, so each GPU "
+              "runs this kernel on its share", file=sys.stderr)
         sys.exit(2)
     import torch
 

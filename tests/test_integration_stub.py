@@ -1,4 +1,5 @@
-"""The reference-side binding printed in INTEGRATION.md, executed (no GPU needed).
+"""The reference-side binding printed in the repository's integration notes, executed
+(no GPU needed).
 
 The python block under "The binding a maintainer would add to the reference" is what a
 maintainer pastes into the reference's python/arm_scan/_ffi.py (:13-22, :41-63,
