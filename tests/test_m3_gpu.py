@@ -122,6 +122,7 @@ MIMO_SHAPES = [
     (1, 20, 2, 16, 32, 4, 1),
     (2, 65, 4, 32, 64, 2, 4),
     (1, 150, 2, 64, 128, 4, 2),
+    (1, 40, 2, 16, 32, 1, 1),  # rank 1 through the MIMO path (psi/zeta/phi)
 ]
 
 
