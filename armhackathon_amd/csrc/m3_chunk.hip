@@ -333,17 +333,6 @@ __device__ __forceinline__ void dma_plan(const M3K& p, const SeqIn& s, int first
   }
 }
 
-// Instructions k0 .. k1-1 of the plan (a wave spreads a stage over its iteration so
-// that the block's DMA does not reach the address unit in one burst).
-template <int MD>
-__device__ __forceinline__ void dma_fast(const DmaPlan<MD>& d, int ch, float* stage, int k0 = 0,
-                                         int k1 = MD) {
-#pragma unroll
-  for (int k = 0; k < MD; ++k)
-    if (k >= k0 && k < k1 && k < d.count && d.on[k])
-      dma16(d.base[k] + ((long long)ch * d.delta[k] + d.off[k]), stage + d.ins[k] * 256);
-}
-
 // Any chunk, with the rows past the end clamped to the last step.
 template <int R, bool REV, int MD>
 __device__ __forceinline__ void dma_clamped(const M3K& p, const SeqIn& s, const DmaPlan<MD>& d,
@@ -361,22 +350,6 @@ __device__ __forceinline__ void dma_clamped(const M3K& p, const SeqIn& s, const 
                                : (long long)t * pc.stride + pc.col;
     dma16(pc.src + o, stage + d.ins[k] * 256);
   }
-}
-
-template <int R, bool REV, int MD>
-__device__ __forceinline__ void dma_stage(const M3K& p, const SeqIn& s, const DmaPlan<MD>& d,
-                                          int ch, float* stage, int lane) {
-  if ((ch + 1) * p.steps_per_chunk <= p.len) dma_fast(d, ch, stage);
-  else dma_clamped<R, REV>(p, s, d, ch, stage, lane);
-}
-
-// Part k0 .. k1-1 of dma_stage; the partial, last chunk goes whole with part 0.
-template <int R, bool REV, int MD>
-__device__ __forceinline__ void dma_stage_part(const M3K& p, const SeqIn& s,
-                                               const DmaPlan<MD>& d, int ch, float* stage,
-                                               int lane, int k0, int k1) {
-  if ((ch + 1) * p.steps_per_chunk <= p.len) dma_fast(d, ch, stage, k0, k1);
-  else if (k0 == 0) dma_clamped<R, REV>(p, s, d, ch, stage, lane);
 }
 
 // The plan of a wave for whole chunks, as running pointers: instruction k of a stage
