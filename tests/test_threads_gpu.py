@@ -2,7 +2,7 @@
 priority): the reference's call is reentrant across threads (arm-scan-ffi/src/lib.rs;
 ctypes releases the GIL). Every thread's results must equal, bit for bit, what one
 thread computes alone: the kernels share no state, and the stream-ordered scratch each
-call takes comes from the device's pool."""
+call takes (segment maps, gate records, SS2D planes) comes from the library's pool."""
 
 import threading
 
@@ -27,13 +27,17 @@ def test_concurrent_calls_on_separate_streams():
     m3 = {k: torch.from_numpy(v).cuda() for k, v in
           workloads.m3_siso(batch=1, length=300, heads=4, dv=32, dqk=64, seed=4).items()}
     keys = ("q", "k", "v", "adt", "dt", "trap", "q_bias", "k_bias")
+    g = {k: torch.from_numpy(v).cuda() for k, v in
+         workloads.ss2d(batch=1, dim=16, height=12, width=20, state=8, seed=5).items()}
 
     def work():
         y1 = arm_scan.selective_scan(m1["u"], F.softplus(m1["delta"]), m1["A"], m1["B"],
                                      m1["C"], D=m1["D"], z=m1["z"])
         y3 = arm_scan.mamba3_scan(*[m3[k] for k in keys], cos=m3["cos"], sin=m3["sin"])
         nc = arm_scan.noncausal_scan(*[m3[k] for k in keys], cos=m3["cos"], sin=m3["sin"])
-        return y1, y3, nc
+        y2 = arm_scan.ss2d_scan(g["u"], g["delta"], g["A"], g["B4"], g["C4"], D=g["D"],
+                                z=g["z"], merge="sum", per_direction=True)
+        return y1, y3, nc, y2
 
     want = work()
     torch.cuda.synchronize()
