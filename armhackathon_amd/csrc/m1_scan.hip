@@ -433,31 +433,58 @@ __global__ void __launch_bounds__(256) transpose_batch_kernel(TransposeBatch b, 
 }
 
 // out = scale * (out + p1 + T(q2) + T(q3)); q2, q3 are (planes, W, H).
+// One 64 x 64 tile of one plane per block and iteration; float4 rows when H and W
+// are multiples of 4.
 __global__ void __launch_bounds__(256) merge4t_kernel(float* __restrict__ out,
                                                       const float* __restrict__ p1,
                                                       const float* __restrict__ q2,
                                                       const float* __restrict__ q3,
                                                       long long planes, int H, int W,
                                                       float scale) {
-  __shared__ float t2[32][33], t3[32][33];
-  const int tiles_w = (W + 31) / 32;
-  const int i0 = (blockIdx.x / tiles_w) * 32, j0 = (blockIdx.x % tiles_w) * 32;
-  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+  __shared__ float t2[64][65], t3[64][65];
+  const int tiles_w = (W + 63) / 64;
+  const int i0 = (blockIdx.x / tiles_w) * 64, j0 = (blockIdx.x % tiles_w) * 64;
+  const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;  // 16 x 16
+  const bool vec = (W % 4 == 0) && (H % 4 == 0);
   for (long long g = blockIdx.y; g < planes; g += gridDim.y) {
     const long long plane = g * H * W;
-    for (int r = ty; r < 32; r += 8) {
-      const int j = j0 + r, i = i0 + tx;  // q is (W, H): rows j, columns i
-      if (i < H && j < W) {
-        t2[r][tx] = q2[plane + (long long)j * H + i];
-        t3[r][tx] = q3[plane + (long long)j * H + i];
+    for (int r = ty; r < 64; r += 16) {
+      const int j = j0 + r, i = i0 + 4 * tx;  // q is (W, H): row j, columns i
+      if (j >= W) continue;
+      const long long o = plane + (long long)j * H + i;
+      if (vec && i + 3 < H) {
+        const float4 a = *reinterpret_cast<const float4*>(q2 + o);
+        const float4 b = *reinterpret_cast<const float4*>(q3 + o);
+        const float va[4] = {a.x, a.y, a.z, a.w}, vb[4] = {b.x, b.y, b.z, b.w};
+        for (int e = 0; e < 4; ++e) {
+          t2[4 * tx + e][r] = va[e];
+          t3[4 * tx + e][r] = vb[e];
+        }
+      } else {
+        for (int e = 0; e < 4; ++e)
+          if (i + e < H) {
+            t2[4 * tx + e][r] = q2[o + e];
+            t3[4 * tx + e][r] = q3[o + e];
+          }
       }
     }
     __syncthreads();
-    for (int r = ty; r < 32; r += 8) {
-      const int i = i0 + r, j = j0 + tx;
-      if (i < H && j < W) {
-        const long long o = plane + (long long)i * W + j;
-        out[o] = scale * (out[o] + p1[o] + t2[tx][r] + t3[tx][r]);
+    for (int r = ty; r < 64; r += 16) {
+      const int i = i0 + r, j = j0 + 4 * tx;  // out is (H, W): row i, columns j
+      if (i >= H) continue;
+      const long long o = plane + (long long)i * W + j;
+      if (vec && j + 3 < W) {
+        float4 a = *reinterpret_cast<const float4*>(out + o);
+        const float4 b = *reinterpret_cast<const float4*>(p1 + o);
+        a.x = scale * (a.x + b.x + t2[r][4 * tx] + t3[r][4 * tx]);
+        a.y = scale * (a.y + b.y + t2[r][4 * tx + 1] + t3[r][4 * tx + 1]);
+        a.z = scale * (a.z + b.z + t2[r][4 * tx + 2] + t3[r][4 * tx + 2]);
+        a.w = scale * (a.w + b.w + t2[r][4 * tx + 3] + t3[r][4 * tx + 3]);
+        *reinterpret_cast<float4*>(out + o) = a;
+      } else {
+        for (int e = 0; e < 4; ++e)
+          if (j + e < W)
+            out[o + e] = scale * (out[o + e] + p1[o + e] + t2[r][4 * tx + e] + t3[r][4 * tx + e]);
       }
     }
     __syncthreads();
@@ -605,7 +632,7 @@ hipError_t transpose_batch(const TransposeSpec* spec, int n, int H, int W, hipSt
 
 hipError_t merge4_transposed(float* out, const float* p1, const float* q2, const float* q3,
                              long long planes, int H, int W, float scale, hipStream_t st) {
-  const long long tiles = (long long)((H + 31) / 32) * ((W + 31) / 32);
+  const long long tiles = (long long)((H + 63) / 64) * ((W + 63) / 64);
   const long long ny = planes < 65535 ? planes : 65535;
   hipLaunchKernelGGL(merge4t_kernel, dim3((unsigned)tiles, (unsigned)ny), dim3(256), 0, st, out,
                      p1, q2, q3, planes, H, W, scale);
