@@ -30,6 +30,7 @@
 
 #include <atomic>
 #include <cstdint>
+#include <type_traits>
 
 #include "scan_common.h"
 #include "scan_launch.h"
@@ -225,6 +226,28 @@ __device__ __forceinline__ void store_block_strided(__amdgpu_buffer_rsrc_t r, un
   for (int k = 0; k < I; ++k)
     __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v[REV ? I - 1 - k : k]),
                                           r, voff, (int)(k * ts * 4), 0);
+}
+
+// A lane block of the row's tail chunk in a strided row (steps `ts` floats apart):
+// one base pointer at traversal step sb and wave-uniform offsets; steps past the
+// row's end read 0 / are not written.
+template <int I, bool REV>
+__device__ __forceinline__ void load_tail(const float* row, long long L, long long sb,
+                                          long long ts, float (&v)[I]) {
+  const float* base = row + (REV ? L - 1 - sb : sb) * ts;
+  const long long st = REV ? -ts : ts;
+#pragma unroll
+  for (int i = 0; i < I; ++i) v[i] = sb + i < L ? base[i * st] : 0.0f;
+}
+
+template <int I, bool REV>
+__device__ __forceinline__ void store_tail(float* row, long long L, long long sb, long long ts,
+                                           const float (&v)[I]) {
+  float* base = row + (REV ? L - 1 - sb : sb) * ts;
+  const long long st = REV ? -ts : ts;
+#pragma unroll
+  for (int i = 0; i < I; ++i)
+    if (sb + i < L) base[i * st] = v[i];
 }
 
 // One state n of one chunk given this lane's B/C blocks (bb, cc): pass 1, the
@@ -443,26 +466,58 @@ __device__ __forceinline__ void lds_block(const float* __restrict__ trow, int j,
 }
 
 // DMA one tile (states n0 .. n0+kTileStates-1 of the chunk whose memory range
-// starts at mem0) into `tile`. Each DMA op fills 256 consecutive tile floats;
-// the block's waves take turns.
-template <int I>
+// starts at mem0) into `tile`. Each DMA op fills 256 consecutive tile floats with
+// 16-byte pieces; the block's waves take turns. DW (rows of B/C not 16-byte aligned:
+// L % 4 != 0 or an unaligned base) moves single floats instead, 64 to an op, into
+// the same layout. `part`: the row's tail chunk, whose range runs past the row; the
+// positions past it are read from kZeroPiece, so that they hold 0 as the general
+// path's bounds-checked loads give.
+__device__ __align__(16) float kZeroPiece[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+
+template <int I, bool DW = false>
 __device__ __forceinline__ void issue_tile(float* tile, const float* Bg, const float* Cg,
                                            long long L, long long mem0, int n0, int N,
-                                           int wave, int lane) {
+                                           int wave, int lane, bool part = false) {
   using G = Tile<I>;
-  constexpr int SPR = G::CH / 4;  // slots per tile row
-  const int t = lane % SPR;
-  const int piece = G::QP * (t & 15) + (t >> 4);
+  if constexpr (!DW) {
+    constexpr int SPR = G::CH / 4;  // slots per tile row
+    const int t = lane % SPR;
+    const int piece = G::QP * (t & 15) + (t >> 4);
 #pragma unroll
-  for (int m0 = 0; m0 < G::DMA; m0 += kWavesPerBlock) {
-    const int m = m0 + wave;  // wave-uniform
-    if (G::DMA % kWavesPerBlock == 0 || m < G::DMA) {
-      const int k = m * (256 / G::CH) + lane / SPR;  // tile row of this lane
+    for (int m0 = 0; m0 < G::DMA; m0 += kWavesPerBlock) {
+      const int m = m0 + wave;  // wave-uniform
+      if (G::DMA % kWavesPerBlock == 0 || m < G::DMA) {
+        const int k = m * (256 / G::CH) + lane / SPR;  // tile row of this lane
+        const int n = n0 + (k % kTileStates);
+        if (n < N && (k < kTileStates || Cg != nullptr)) {  // Cg null: B rows only
+          const long long g = mem0 + 4 * piece;  // L % 4 == 0: a piece lies wholly in or out
+          const float* src = part && (g < 0 || g >= L)
+                                 ? kZeroPiece
+                                 : (k < kTileStates ? Bg : Cg) + (long long)n * L + g;
+          __builtin_amdgcn_global_load_lds(
+              (const void*)src, (__attribute__((address_space(3))) void*)(tile + m * 256), 16,
+              0, 0);
+        }
+      }
+    }
+  } else {
+    constexpr int OPS = G::FLOATS / 64;  // single-float ops per tile
+    static_assert(OPS % kWavesPerBlock == 0, "whole rounds of ops per wave");
+#pragma unroll
+    for (int m0 = 0; m0 < OPS; m0 += kWavesPerBlock) {
+      const int m = m0 + wave;  // wave-uniform
+      const int f = m * 64 + lane;  // tile float of this lane
+      const int k = f / G::CH, fr = f % G::CH;  // tile row, float in the row
+      const int t = fr >> 2;                   // its 16-byte slot
+      const int col = 4 * (G::QP * (t & 15) + (t >> 4)) + (fr & 3);
       const int n = n0 + (k % kTileStates);
-      if (n < N && (k < kTileStates || Cg != nullptr)) {  // Cg null: B rows only
-        const float* src = (k < kTileStates ? Bg : Cg) + (long long)n * L + mem0 + 4 * piece;
+      if (n < N && (k < kTileStates || Cg != nullptr)) {
+        const long long g = mem0 + col;
+        const float* src = part && (g < 0 || g >= L)
+                               ? kZeroPiece
+                               : (k < kTileStates ? Bg : Cg) + (long long)n * L + g;
         __builtin_amdgcn_global_load_lds(
-            (const void*)src, (__attribute__((address_space(3))) void*)(tile + m * 256), 16, 0,
+            (const void*)src, (__attribute__((address_space(3))) void*)(tile + m * 64), 4, 0,
             0);
       }
     }
@@ -629,9 +684,16 @@ __device__ __forceinline__ void tile_states(const float* tile, int n0, int N, in
 // loads and out written with buffer stores; 2: strided with unit channel stride,
 // z and out staged through LDS; 3: as 2, with u staged through the same LDS buffer
 // (its own compile-time case, so that the per-lane u loads of 1 and 2 hold no
-// registers in it).
-template <int I, bool REV, int SIO, bool SEG = false>
+// registers in it). ALN: rows 16-byte aligned (L % 4 == 0, aligned bases), so that
+// rows move in 16-byte pieces; otherwise single floats (SIO 0 only).
+// The row's tail chunk (L % 256 steps) runs in the tile loop as well: its loads and
+// stores check bounds (per lane, by strides, bypassing the LDS stages of SIO 2 and
+// 3), its B/C positions past the row read zeros, and its steps past the row's end
+// are identity maps (dt = 0). TAIL: compiled only for rows with a tail chunk
+// (L % 256 != 0), so that the kernels for whole chunks carry none of its code.
+template <int I, bool REV, int SIO, bool SEG = false, bool ALN = true, bool TAIL = false>
 __device__ __forceinline__ void tile_rows(const M1Kern& p, long long blk, int seg = 0) {
+  static_assert(ALN || SIO == 0, "unaligned rows: contiguous z and out only");
   constexpr int LPR = 16, RPW = 4;
   using G = Tile<I>;
   constexpr long long CH = G::CH;
@@ -689,21 +751,64 @@ __device__ __forceinline__ void tile_rows(const M1Kern& p, long long blk, int se
   for (int i = threadIdx.x; i < N; i += blockDim.x) zeros[i] = 0.0f;
 
   const int ng = (N + kTileStates - 1) / kTileStates;  // tiles per chunk
-  const long long ntiles = (ce - cb) * ng;
+  const long long cl = (TAIL && last_seg && nfull < nch) ? ce + 1 : ce;  // with the tail chunk
+  const long long ntiles = (cl - cb) * ng;
   auto mem0 = [&](long long c) { return REV ? L - (c + 1) * CH : c * CH; };
-  if (ntiles > 0) issue_tile<I>(tiles, Bg, Cg, L, mem0(cb), 0, N, wave, lane);
+  if (ntiles > 0)
+    issue_tile<I, !ALN>(tiles, Bg, Cg, L, mem0(cb), 0, N, wave, lane, TAIL && cb >= nfull);
   // In a segment (one or a few chunks per block) the first tile's sync comes after
   // the first chunk's delta/u loads, in the loop, so that their latencies overlap.
-  if (!segd || ce == cb) tile_sync();
+  if (!segd || cl == cb) tile_sync();
 
-  // the lane block's outputs at traversal base sbo (SIO 0 and 1)
-  auto store_out = [&](long long sbo, const float (&v)[I]) {
-    if (SIO) {
+  // A lane block of a contiguous row. Aligned rows: 16-byte pieces, where in the
+  // tail chunk a piece past the row's end (L % 4 == 0: a piece lies wholly in or
+  // out) reads kZeroPiece; otherwise single floats, bounds-checked in the tail.
+  auto load_c = [&](const float* r, long long sbl, bool full, float (&v)[I]) {
+    if constexpr (ALN) {
+      const long long mb = REV ? L - sbl - I : sbl;  // the block's lowest memory step
+#pragma unroll
+      for (int q = 0; q < I / 4; ++q) {
+        const long long m = mb + 4 * q;
+        const bool in = full || (REV ? m >= 0 : m < L);
+        const float4 x = *reinterpret_cast<const float4*>(in ? r + m : kZeroPiece);
+        const float w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[REV ? I - 1 - (4 * q + e) : 4 * q + e] = w[e];
+      }
+    } else {
+      // one base per block and immediate offsets: traversal step sbl + i is memory
+      // mb + i (forward) or mb + I-1-i (reverse)
+      const float* base = r + (REV ? L - sbl - I : sbl);
+#pragma unroll
+      for (int i = 0; i < I; ++i)
+        v[i] = full || sbl + i < L ? base[REV ? I - 1 - i : i] : 0.0f;
+    }
+  };
+
+  // the lane block's outputs at traversal base sbo (SIO 0 and 1; every SIO's tail)
+  auto store_out = [&](long long sbo, const float (&v)[I], bool full) {
+    if (SIO && !full) {
+      store_tail<I, REV>(orow, L, sbo, p.os_t, v);
+    } else if (SIO) {
       const long long tlo = REV ? L - sbo - I : sbo;  // the block's lowest memory step
       store_block_strided<I, REV>(slab_rsrc(p.out + bib * p.os_b, p.o_bytes),
                                   (unsigned)((d * p.os_d + tlo * p.os_t) * 4), p.os_t, v);
+    } else if constexpr (ALN) {
+      const long long mb = REV ? L - sbo - I : sbo;
+#pragma unroll
+      for (int q = 0; q < I / 4; ++q) {
+        const long long m = mb + 4 * q;
+        float w[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) w[e] = v[REV ? I - 1 - (4 * q + e) : 4 * q + e];
+        if (REV ? m >= 0 : m < L)  // the tail chunk: pieces inside the row only
+          *reinterpret_cast<float4*>(orow + m) = make_float4(w[0], w[1], w[2], w[3]);
+      }
     } else {
-      store_block<I, REV, true>(orow, L, sbo, v, L);
+      float* base = orow + (REV ? L - sbo - I : sbo);
+#pragma unroll
+      for (int i = 0; i < I; ++i)
+        if (sbo + i < L) base[REV ? I - 1 - i : i] = v[i];
     }
   };
 
@@ -719,14 +824,19 @@ __device__ __forceinline__ void tile_rows(const M1Kern& p, long long blk, int se
   if (SIO == 2 && p.z && ce > cb) z_stage(cb);
 
   long long k = 0;  // tile counter
-  for (long long c = cb; c < ce; ++c) {
+  // One chunk; FULL: every step inside the row. The tail chunk is its own compiled
+  // copy, so that its bounds checks hold no registers in the loop over whole chunks.
+  auto run_chunk = [&](long long c, auto full_tag) {
+    constexpr bool full = decltype(full_tag)::value;
     const long long sb = c * CH + (long long)j * I;
     float dt[I], du[I], y[I], zz[I];
     float sdt = 0.0f;
     {
       float dd[I], uu[I];
-      load_block<I, REV, true>(drow, L, sb, 0.0f, dd, L);
-      if (ustage) {
+      load_c(drow, sb, full, dd);
+      if (ustr && !full) {
+        load_tail<I, REV>(urow, L, sb, p.us_t, uu);
+      } else if (ustage) {
         if constexpr (SIO == 3) {
           // the block's 16 channels of u, 64-byte runs, land with delta's loads; the
           // stage is free (the previous chunk's outputs have left it) and z's DMA
@@ -742,12 +852,13 @@ __device__ __forceinline__ void tile_rows(const M1Kern& p, long long blk, int se
         load_block_strided<I, REV>(slab_rsrc(p.u + bib * p.us_b, p.u_bytes),
                                    (unsigned)((d * p.us_d + tlo * p.us_t) * 4), p.us_t, uu);
       } else {
-        load_block<I, REV, true>(urow, L, sb, 0.0f, uu, L);
+        load_c(urow, sb, full, uu);
       }
 #pragma unroll
       for (int i = 0; i < I; ++i) {
         float x = dd[i] + bias;
         if (p.softplus) x = softplus_fast(x);
+        if (!full) x = sb + i < L ? x : 0.0f;  // steps past the row: identity maps
         dt[i] = x;
         du[i] = x * uu[i];
         y[i] = dskip * uu[i];
@@ -760,16 +871,20 @@ __device__ __forceinline__ void tile_rows(const M1Kern& p, long long blk, int se
       progress_prio(k, ntiles);
       if (k + 1 < ntiles) {  // the next tile: state group q + 1 of this chunk, or 0 of the next
         const bool same = q + 1 < ng;
-        issue_tile<I>(tiles + ((k + 1) & 1) * G::FLOATS, Bg, Cg, L, mem0(same ? c : c + 1),
-                      same ? (q + 1) * kTileStates : 0, N, wave, lane);
+        const long long cn = same ? c : c + 1;
+        issue_tile<I, !ALN>(tiles + ((k + 1) & 1) * G::FLOATS, Bg, Cg, L, mem0(cn),
+                            same ? (q + 1) * kTileStates : 0, N, wave, lane,
+                            TAIL && cn >= nfull);
       }
-      if (SIO < 2 && zrow && q + 1 == ng) {
+      if (SIO == 1 && !full && zrow && q + 1 == ng) {
+        load_tail<I, REV>(zrow, L, sb, p.zs_t, zz);
+      } else if (SIO < 2 && zrow && q + 1 == ng) {
         if (SIO == 1) {
           const long long tlo = REV ? L - sb - I : sb;  // the block's lowest memory step
           load_block_strided<I, REV>(slab_rsrc(p.z + bib * p.zs_b, p.z_bytes),
                                      (unsigned)((d * p.zs_d + tlo * p.zs_t) * 4), p.zs_t, zz);
         } else {
-          load_block<I, REV, true>(zrow, L, sb, 0.0f, zz, L);
+          load_c(zrow, sb, full, zz);
         }
       }
       tile_states<I, REV>(tiles + (k & 1) * G::FLOATS, q * kTileStates, N, j, a2s, cbase,
@@ -779,7 +894,8 @@ __device__ __forceinline__ void tile_rows(const M1Kern& p, long long blk, int se
         // after the states (no registers held through them), before the sync after
         // which the outputs overwrite it
         static_assert(SIO < 2 || I == 16, "the stage holds 16 steps per lane block");
-        read_z_stage(zbuf, j, wave, rw, zz);
+        if (full) read_z_stage(zbuf, j, wave, rw, zz);
+        else load_tail<I, REV>(zrow, L, sb, p.zs_t, zz);
       }
       tile_sync();
     }
@@ -787,31 +903,26 @@ __device__ __forceinline__ void tile_rows(const M1Kern& p, long long blk, int se
 #pragma unroll
       for (int i = 0; i < I; ++i) y[i] *= silu_fast(zz[i]);
     }
-    if (SIO >= 2) {
+    if (SIO >= 2 && full) {
       write_out_stage(zbuf, j, wave, rw, y);
       lds_barrier();
       store_out_stage<REV>(zbuf, p.out + bib * p.os_b, p.os_t, L, c * CH, d0, wave, lane);
       lds_barrier();  // every lane has read its outputs before the next z stage lands
       if (p.z && c + 1 < ce && !ustage) z_stage(c + 1);
     } else {
-      store_out(sb, y);
+      store_out(sb, y, full);
     }
-  }
-  if (last_seg && nfull < nch) {
-    // the row's tail chunk goes through the bounds-checked global-load path
-    float dn[I], un[I];
-    chunk<LPR, I, REV, true, false>(p, nfull * CH + (long long)j * I, j, true, true, row, urow,
-                                    drow, zrow, orow, Bg, Cg, a2s, bias, dskip, carry, dn, un,
-                                    false, -1, SIO ? p.zs_t : 1, SIO ? p.os_t : 1,
-                                    ustr ? p.us_t : 1);
-  }
+  };
+  for (long long c = cb; c < ce; ++c) run_chunk(c, std::true_type{});
+  if constexpr (TAIL)
+    if (cl > ce) run_chunk(ce, std::false_type{});
 }
 
 // Pass 1 of a segmented scan: the affine map h -> A h + B of each state over one
 // segment of 16 rows (segments 0 .. segs-2), with the same discretisation and
 // fold as tile_state; the chunk maps compose in order. A of a chunk is
 // 2^(a2 * sum of the row's dt over it), one exponential.
-template <int I, bool REV>
+template <int I, bool REV, bool ALN = true>
 __device__ __forceinline__ void fold_rows(const M1Kern& p, long long blk, int seg) {
   constexpr int LPR = 16, RPW = 4;
   using G = Tile<I>;
@@ -851,7 +962,7 @@ __device__ __forceinline__ void fold_rows(const M1Kern& p, long long blk, int se
   const long long ntiles = (ce - cb) * ng;
   auto mem0 = [&](long long c) { return REV ? L - (c + 1) * CH : c * CH; };
   // the fold reads B only: the tiles' C rows are not fetched
-  if (ntiles > 0) issue_tile<I>(tiles, Bg, nullptr, L, mem0(cb), 0, N, wave, lane);
+  if (ntiles > 0) issue_tile<I, !ALN>(tiles, Bg, nullptr, L, mem0(cb), 0, N, wave, lane);
   long long k = 0;
   for (long long c = cb; c < ce; ++c) {
     const long long sb = c * CH + (long long)j * I;
@@ -859,13 +970,14 @@ __device__ __forceinline__ void fold_rows(const M1Kern& p, long long blk, int se
     float sdt = 0.0f;
     {
       float dd[I], uu[I];
-      load_block<I, REV, true>(drow, L, sb, 0.0f, dd, L);
-      if (p.u_strided) {
+      // the segments folded here hold whole chunks: no bounds to check
+      load_block<I, REV, ALN>(drow, sb + I, sb, 0.0f, dd, L);
+      if (ALN && p.u_strided) {
         const long long tlo = REV ? L - sb - I : sb;  // the block's lowest memory step
         load_block_strided<I, REV>(slab_rsrc(p.u + bib * p.us_b, p.u_bytes),
                                    (unsigned)((d * p.us_d + tlo * p.us_t) * 4), p.us_t, uu);
       } else {
-        load_block<I, REV, true>(urow, L, sb, 0.0f, uu, L);
+        load_block<I, REV, ALN>(urow, sb + I, sb, 0.0f, uu, L);
       }
 #pragma unroll
       for (int i = 0; i < I; ++i) {
@@ -884,8 +996,9 @@ __device__ __forceinline__ void fold_rows(const M1Kern& p, long long blk, int se
       progress_prio(k, ntiles);
       if (k + 1 < ntiles) {  // the next tile: state group q + 1 of this chunk, or 0 of the next
         const bool same = q + 1 < ng;
-        issue_tile<I>(tiles + ((k + 1) & 1) * G::FLOATS, Bg, nullptr, L, mem0(same ? c : c + 1),
-                      same ? (q + 1) * kTileStates : 0, N, wave, lane);
+        issue_tile<I, !ALN>(tiles + ((k + 1) & 1) * G::FLOATS, Bg, nullptr, L,
+                            mem0(same ? c : c + 1), same ? (q + 1) * kTileStates : 0, N, wave,
+                            lane);
       }
       const float* tile = tiles + (k & 1) * G::FLOATS;
 #pragma unroll
@@ -918,11 +1031,11 @@ __device__ __forceinline__ void fold_rows(const M1Kern& p, long long blk, int se
     }
 }
 
-template <int I, bool REV>
+template <int I, bool REV, bool ALN>
 __global__ void __launch_bounds__(64 * kWavesPerBlock, 3)
 m1_seg_fold_kernel(M1Kern p) {
   const long long nblk = p.rows / (kWavesPerBlock * 4);
-  fold_rows<I, REV>(p, blockIdx.x % nblk, (int)(blockIdx.x / nblk));
+  fold_rows<I, REV, ALN>(p, blockIdx.x % nblk, (int)(blockIdx.x / nblk));
 }
 
 // Block id -> row block for time-major z/out: a 128-byte line of those holds 32
@@ -936,7 +1049,7 @@ __device__ __forceinline__ long long paired_block(long long bid, long long nblk)
 }
 
 // Block id -> (row block, segment): with SEG the segments are blockIdx / (row blocks).
-template <int I, bool REV, int SIO, bool SEG>
+template <int I, bool REV, int SIO, bool SEG, bool ALN, bool TAIL>
 __global__ void __launch_bounds__(64 * kWavesPerBlock, 3)
 m1_tile_kernel(M1Kern p) {
   const long long nblk = p.rows / (kWavesPerBlock * 4);
@@ -952,7 +1065,7 @@ m1_tile_kernel(M1Kern p) {
   if (!SEG && nblk % 16 == 0) blk = (bid & 7) * (nblk / 8) + (bid >> 3);
   else if (SIO) blk = paired_block(bid, nblk);
   else if (!SEG && nblk % 8 == 0) blk = (bid & 7) * (nblk / 8) + (bid >> 3);
-  tile_rows<I, REV, SIO, SEG>(p, blk, seg);
+  tile_rows<I, REV, SIO, SEG, ALN, TAIL>(p, blk, seg);
 }
 
 // Several traversals of rows of the same shape in one launch (the directions of
@@ -960,7 +1073,7 @@ m1_tile_kernel(M1Kern p) {
 // takes a contiguous range of row blocks, with the jobs of a row block next to each
 // other, so the row blocks of one batch, which read the same B and C tiles, share
 // its L2 (at D 192 a batch is 12 row blocks; config-5 SS2D 331 -> 327 us).
-template <int I>
+template <int I, bool TAIL>
 __global__ void __launch_bounds__(64 * kWavesPerBlock, 3)
 m1_tile_jobs_kernel(M1Kern p, M1Jobs jobs) {
   const int xcd = blockIdx.x & 7;
@@ -977,18 +1090,18 @@ m1_tile_jobs_kernel(M1Kern p, M1Jobs jobs) {
   p.C = jb.C;
   p.out = jb.out;
   p.last = jb.last;
-  if (jb.rev) tile_rows<I, true, 0>(p, blk);
-  else tile_rows<I, false, 0>(p, blk);
+  if (jb.rev) tile_rows<I, true, 0, false, true, TAIL>(p, blk);
+  else tile_rows<I, false, 0, false, true, TAIL>(p, blk);
 }
 
-template <int I, bool REV, int SIO>
+template <int I, bool REV, int SIO, bool ALN>
 hipError_t launch_tile(const M1Kern& k, hipStream_t st) {
   constexpr int RPB = kWavesPerBlock * 4;
   const long long blocks = (long long)k.rows / RPB;
   const int segs = k.segs > 1 ? k.segs : 1;
   if (segs > 1) {  // pass 1: the maps of segments 0 .. segs-2
     const size_t lds1 = sizeof(float) * (2 * (size_t)Tile<I>::FLOATS + 3 * (size_t)RPB * k.N);
-    hipLaunchKernelGGL((m1_seg_fold_kernel<I, REV>), dim3((unsigned)(blocks * (segs - 1))),
+    hipLaunchKernelGGL((m1_seg_fold_kernel<I, REV, ALN>), dim3((unsigned)(blocks * (segs - 1))),
                        dim3(64 * kWavesPerBlock), lds1, st, k);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
@@ -996,12 +1109,16 @@ hipError_t launch_tile(const M1Kern& k, hipStream_t st) {
   const size_t lds =
       sizeof(float) * (2 * (size_t)Tile<I>::FLOATS + (SIO >= 2 ? kZStageFloats : 0) +
                        (2 * (size_t)RPB + 1) * k.N);
-  if (segs > 1)
-    hipLaunchKernelGGL((m1_tile_kernel<I, REV, SIO, true>), dim3((unsigned)(blocks * segs)),
-                       dim3(64 * kWavesPerBlock), lds, st, k);
+  const dim3 grid((unsigned)(segs > 1 ? blocks * segs : blocks)), wg(64 * kWavesPerBlock);
+  const bool tail = k.L % Tile<I>::CH != 0;
+  if (segs > 1 && tail)
+    hipLaunchKernelGGL((m1_tile_kernel<I, REV, SIO, true, ALN, true>), grid, wg, lds, st, k);
+  else if (segs > 1)
+    hipLaunchKernelGGL((m1_tile_kernel<I, REV, SIO, true, ALN, false>), grid, wg, lds, st, k);
+  else if (tail)
+    hipLaunchKernelGGL((m1_tile_kernel<I, REV, SIO, false, ALN, true>), grid, wg, lds, st, k);
   else
-    hipLaunchKernelGGL((m1_tile_kernel<I, REV, SIO, false>), dim3((unsigned)blocks),
-                       dim3(64 * kWavesPerBlock), lds, st, k);
+    hipLaunchKernelGGL((m1_tile_kernel<I, REV, SIO, false, ALN, false>), grid, wg, lds, st, k);
   return hipGetLastError();
 }
 
@@ -1051,8 +1168,12 @@ hipError_t m1_scan_jobs(const M1Problem& pr, const M1JobSpec* spec, int n, hipSt
   const long long blocks = 8LL * n * ((jobs.blocks_per_job + 7) / 8);
   const size_t lds =
       sizeof(float) * (2 * (size_t)Tile<M1_TILE_I>::FLOATS + (2 * (size_t)16 + 1) * k.N);
-  hipLaunchKernelGGL((m1_tile_jobs_kernel<M1_TILE_I>), dim3((unsigned)blocks),
-                     dim3(64 * kWavesPerBlock), lds, st, k, jobs);
+  if (k.L % Tile<M1_TILE_I>::CH != 0)
+    hipLaunchKernelGGL((m1_tile_jobs_kernel<M1_TILE_I, true>), dim3((unsigned)blocks),
+                       dim3(64 * kWavesPerBlock), lds, st, k, jobs);
+  else
+    hipLaunchKernelGGL((m1_tile_jobs_kernel<M1_TILE_I, false>), dim3((unsigned)blocks),
+                       dim3(64 * kWavesPerBlock), lds, st, k, jobs);
   return hipGetLastError();
 }
 
@@ -1130,12 +1251,13 @@ hipError_t plan_segments(M1Kern& k, float* scratch_p, size_t scratch_bytes, hipS
   return stream_alloc((void**)&k.segmap, map_bytes(k.segs), st);
 }
 
-template <int SIO>
+template <int SIO, bool ALN = true>
 hipError_t run_tile(M1Kern& k, bool rev, float* scratch_p, size_t scratch_bytes,
                     hipStream_t st) {
   hipError_t e = plan_segments(k, scratch_p, scratch_bytes, st);
   if (e != hipSuccess) return e;
-  e = rev ? launch_tile<M1_TILE_I, true, SIO>(k, st) : launch_tile<M1_TILE_I, false, SIO>(k, st);
+  e = rev ? launch_tile<M1_TILE_I, true, SIO, ALN>(k, st)
+          : launch_tile<M1_TILE_I, false, SIO, ALN>(k, st);
   if (k.segmap && !scratch_p) {
     const hipError_t fe = hipFreeAsync(k.segmap, st);
     if (e == hipSuccess) e = fe;
@@ -1211,9 +1333,12 @@ hipError_t m1_scan_chunked(const M1Problem& pr, hipStream_t st) {
                      : run_tile<2>(k, rev, pr.scratch, pr.scratch_bytes, st);
     return run_tile<1>(k, rev, pr.scratch, pr.scratch_bytes, st);
   }
-  // the tiled path needs every 16-row block inside one batch/group and 16-byte rows
-  const bool tiled = vec && pr.dim % 16 == 0 && (pr.dim / pr.groups) % 16 == 0;
-  if (tiled) return run_tile<0>(k, rev, pr.scratch, pr.scratch_bytes, st);
+  // the tiled path needs every 16-row block inside one batch/group; rows that are not
+  // 16-byte aligned move as single floats
+  const bool tiled = pr.dim % 16 == 0 && (pr.dim / pr.groups) % 16 == 0;
+  if (tiled)
+    return vec ? run_tile<0, true>(k, rev, pr.scratch, pr.scratch_bytes, st)
+               : run_tile<0, false>(k, rev, pr.scratch, pr.scratch_bytes, st);
   return launch_dir<16, 16>(k, rev, vec, st);
 }
 

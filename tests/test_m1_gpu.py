@@ -75,6 +75,17 @@ SHAPES = [
     (1, 32, 600, 13, 2),
     (2, 48, 512, 8, 3),
     (1, 16, 4096, 16, 1),
+    # the tiled kernel's tail chunk in its tile loop (L % 256 != 0), and rows that are
+    # not 16-byte multiples (L % 4 != 0: single-float DMA and loads)
+    (1, 16, 260, 16, 1),
+    (2, 32, 1001, 16, 1),
+    (1, 16, 3, 16, 1),
+    (1, 32, 258, 16, 2),
+    (1, 48, 2050, 13, 3),
+    (2, 16, 256, 16, 1),
+    # few rows: the segmented scan (fold + replay) with a tail, aligned and not
+    (1, 1536, 2052, 16, 1),
+    (1, 1536, 2050, 16, 1),
 ]
 
 
