@@ -110,9 +110,12 @@ def test_m1_random_vs_oracle(shape, reverse):
     assert rel_err(host(last), ref_last) < TOL
 
 
-def test_m1_optional_inputs_absent():
-    x = workloads.m1_op(batch=2, dim=24, length=777, state=16, seed=3, z=False, D=False)
-    case("m1 without D/z/bias, softplus off")
+@pytest.mark.parametrize("dim", [24, 32])
+def test_m1_optional_inputs_absent(dim):
+    """dim 24: the global-load kernel; dim 32: the tiled one, with unaligned rows and
+    a tail chunk (L 777)."""
+    x = workloads.m1_op(batch=2, dim=dim, length=777, state=16, seed=3, z=False, D=False)
+    case(f"m1 without D/z/bias, softplus off, dim {dim}")
     out, last = _scan(x)
     ref, ref_last = _ref(x)
     assert rel_err(host(out), ref) < TOL and rel_err(host(last), ref_last) < TOL
