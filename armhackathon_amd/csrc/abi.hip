@@ -563,7 +563,7 @@ int arm_scan_ss2d_f32(const ArmSS2DDims* dims, const float* u, const float* delt
   {
     armscan::M1Problem q = p;
     q.u = u; q.delta = delta; q.z = z;
-    q.B = b4; q.C = c4; q.out = out;  // for the alignment check (the planes keep it: L % 4 == 0)
+    q.B = b4; q.C = c4; q.out = out;
     if (armscan::m1_jobs_supported(q)) {
       // One launch for the four directions. The column directions scan column-major
       // copies of u, delta, z and of their B/C (one batched transpose) and write

@@ -1073,7 +1073,7 @@ m1_tile_kernel(M1Kern p) {
 // takes a contiguous range of row blocks, with the jobs of a row block next to each
 // other, so the row blocks of one batch, which read the same B and C tiles, share
 // its L2 (at D 192 a batch is 12 row blocks; config-5 SS2D 331 -> 327 us).
-template <int I, bool TAIL>
+template <int I, bool TAIL, bool ALN>
 __global__ void __launch_bounds__(64 * kWavesPerBlock, 3)
 m1_tile_jobs_kernel(M1Kern p, M1Jobs jobs) {
   const int xcd = blockIdx.x & 7;
@@ -1090,8 +1090,8 @@ m1_tile_jobs_kernel(M1Kern p, M1Jobs jobs) {
   p.C = jb.C;
   p.out = jb.out;
   p.last = jb.last;
-  if (jb.rev) tile_rows<I, true, 0, false, true, TAIL>(p, blk);
-  else tile_rows<I, false, 0, false, true, TAIL>(p, blk);
+  if (jb.rev) tile_rows<I, true, 0, false, ALN, TAIL>(p, blk);
+  else tile_rows<I, false, 0, false, ALN, TAIL>(p, blk);
 }
 
 template <int I, bool REV, int SIO, bool ALN>
@@ -1142,10 +1142,10 @@ bool aligned16(const void* q) { return q == nullptr || ((uintptr_t)q & 15u) == 0
 
 }  // namespace
 
+// Rows of any length and alignment: unaligned ones (L % 4 != 0 or a base off 16 bytes)
+// take the single-float instantiation.
 bool m1_jobs_supported(const M1Problem& pr) {
-  return pr.len % 4 == 0 && pr.dim % 16 == 0 && pr.groups == 1 && pr.h0 == nullptr &&
-         aligned16(pr.u) && aligned16(pr.delta) && aligned16(pr.z) && aligned16(pr.B) &&
-         aligned16(pr.C) && aligned16(pr.out);
+  return pr.dim % 16 == 0 && pr.groups == 1 && pr.h0 == nullptr;
 }
 
 hipError_t m1_scan_jobs(const M1Problem& pr, const M1JobSpec* spec, int n, hipStream_t st) {
@@ -1158,22 +1158,27 @@ hipError_t m1_scan_jobs(const M1Problem& pr, const M1JobSpec* spec, int n, hipSt
   M1Jobs jobs{};
   jobs.njobs = n;
   jobs.blocks_per_job = k.rows / 16;
+  bool aln = pr.len % 4 == 0;
   for (int i = 0; i < n; ++i) {
     const M1JobSpec& j = spec[i];
-    if (!aligned16(j.u) || !aligned16(j.delta) || !aligned16(j.z) || !aligned16(j.B) ||
-        !aligned16(j.C) || !aligned16(j.out))
-      return hipErrorInvalidValue;
+    aln = aln && aligned16(j.u) && aligned16(j.delta) && aligned16(j.z) && aligned16(j.B) &&
+          aligned16(j.C) && aligned16(j.out);
     jobs.job[i] = M1Job{j.u, j.delta, j.z, j.B, j.C, j.out, j.last, j.rev};
   }
   const long long blocks = 8LL * n * ((jobs.blocks_per_job + 7) / 8);
   const size_t lds =
       sizeof(float) * (2 * (size_t)Tile<M1_TILE_I>::FLOATS + (2 * (size_t)16 + 1) * k.N);
-  if (k.L % Tile<M1_TILE_I>::CH != 0)
-    hipLaunchKernelGGL((m1_tile_jobs_kernel<M1_TILE_I, true>), dim3((unsigned)blocks),
-                       dim3(64 * kWavesPerBlock), lds, st, k, jobs);
+  const bool tail = k.L % Tile<M1_TILE_I>::CH != 0;
+  const dim3 grid((unsigned)blocks), wg(64 * kWavesPerBlock);
+  if (aln && tail)
+    hipLaunchKernelGGL((m1_tile_jobs_kernel<M1_TILE_I, true, true>), grid, wg, lds, st, k, jobs);
+  else if (aln)
+    hipLaunchKernelGGL((m1_tile_jobs_kernel<M1_TILE_I, false, true>), grid, wg, lds, st, k, jobs);
+  else if (tail)
+    hipLaunchKernelGGL((m1_tile_jobs_kernel<M1_TILE_I, true, false>), grid, wg, lds, st, k, jobs);
   else
-    hipLaunchKernelGGL((m1_tile_jobs_kernel<M1_TILE_I, false>), dim3((unsigned)blocks),
-                       dim3(64 * kWavesPerBlock), lds, st, k, jobs);
+    hipLaunchKernelGGL((m1_tile_jobs_kernel<M1_TILE_I, false, false>), grid, wg, lds, st, k,
+                       jobs);
   return hipGetLastError();
 }
 

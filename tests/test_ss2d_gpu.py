@@ -75,6 +75,33 @@ def test_ss2d_per_direction_vs_oracle(shape):
         assert rel_err(host(last), rlast) < 1e-4, merge
 
 
+@pytest.mark.parametrize("shape", [(2, 16, 7, 7, 16), (1, 32, 45, 45, 16)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_ss2d_unaligned_rows(shape):
+    """Grids whose rows are not 16-byte multiples (7x7, 45x45) and inputs placed one
+    float past an aligned base: the one-launch route with single-float moves."""
+    import torch
+    import armhackathon_amd as arm_scan
+
+    b, d, h, w, n = shape
+    case(f"ss2d unaligned rows {shape}")
+    x = workloads.ss2d(batch=b, dim=d, height=h, width=w, state=n, seed=h * w + 1)
+
+    def shifted(a):  # the same values one float past a 256-byte aligned allocation
+        t = torch.empty(a.size + 1, dtype=torch.float32, device="cuda")
+        t[1:] = torch.from_numpy(np.ascontiguousarray(a)).reshape(-1).cuda()
+        return t[1:].view(a.shape)
+
+    t = {k: shifted(v) if k in ("u", "delta", "B4", "C4", "z") else dev(v) for k, v in x.items()}
+    out, last = arm_scan.ss2d_scan(t["u"], t["delta"], t["A"], t["B4"], t["C4"], D=t["D"],
+                                   z=t["z"], delta_softplus=False, merge="sum",
+                                   per_direction=True, return_last_state=True)
+    ref, rlast = oracle.ss2d(x["u"], x["delta"], x["A"], x["B4"], x["C4"], D=x["D"], z=x["z"],
+                             dtype=np.float64, want_state=True)
+    assert rel_err(host(out), ref.sum(0)) < 1e-4
+    assert rel_err(host(last), rlast) < 1e-4
+
+
 def test_ss2d_benchmark_shape():
     """64x64 grid, batch 16, d_inner 192, d_state 16,
     per-direction B/C, D skip and z gate, summed onto the grid."""
