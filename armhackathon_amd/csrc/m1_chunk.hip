@@ -60,6 +60,11 @@ struct M1Kern {
   int segs;
   long long seg_chunks;
   float* segmap;
+  // Row pitch of B and C in floats: L, or L rounded up to 4 when the tiled kernel reads
+  // padded copies of rows that are not 16-byte multiples. bpo: zeros in front of each
+  // padded row (ldb - L for reverse, whose chunks end at L, so that every chunk starts
+  // on a 16-byte piece; 0 otherwise). B and C point at the rows' first data float.
+  long long ldb, bpo;
 };
 
 // One traversal of a multi-traversal launch: its own inputs, B/C, outputs and
@@ -476,8 +481,9 @@ __device__ __align__(16) float kZeroPiece[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 
 template <int I, bool DW = false>
 __device__ __forceinline__ void issue_tile(float* tile, const float* Bg, const float* Cg,
-                                           long long L, long long mem0, int n0, int N,
-                                           int wave, int lane, bool part = false) {
+                                           long long L, long long ldb, long long bpo,
+                                           long long mem0, int n0, int N, int wave, int lane,
+                                           bool part = false) {
   using G = Tile<I>;
   if constexpr (!DW) {
     constexpr int SPR = G::CH / 4;  // slots per tile row
@@ -490,10 +496,11 @@ __device__ __forceinline__ void issue_tile(float* tile, const float* Bg, const f
         const int k = m * (256 / G::CH) + lane / SPR;  // tile row of this lane
         const int n = n0 + (k % kTileStates);
         if (n < N && (k < kTileStates || Cg != nullptr)) {  // Cg null: B rows only
-          const long long g = mem0 + 4 * piece;  // L % 4 == 0: a piece lies wholly in or out
-          const float* src = part && (g < 0 || g >= L)
+          // a piece lies wholly inside the (padded) row [-bpo, ldb - bpo) or outside it
+          const long long g = mem0 + 4 * piece;
+          const float* src = part && (g < -bpo || g >= ldb - bpo)
                                  ? kZeroPiece
-                                 : (k < kTileStates ? Bg : Cg) + (long long)n * L + g;
+                                 : (k < kTileStates ? Bg : Cg) + (long long)n * ldb + g;
           __builtin_amdgcn_global_load_lds(
               (const void*)src, (__attribute__((address_space(3))) void*)(tile + m * 256), 16,
               0, 0);
@@ -515,7 +522,7 @@ __device__ __forceinline__ void issue_tile(float* tile, const float* Bg, const f
         const long long g = mem0 + col;
         const float* src = part && (g < 0 || g >= L)
                                ? kZeroPiece
-                               : (k < kTileStates ? Bg : Cg) + (long long)n * L + g;
+                               : (k < kTileStates ? Bg : Cg) + (long long)n * ldb + g;
         __builtin_amdgcn_global_load_lds(
             (const void*)src, (__attribute__((address_space(3))) void*)(tile + m * 64), 4, 0,
             0);
@@ -691,7 +698,8 @@ __device__ __forceinline__ void tile_states(const float* tile, int n0, int N, in
 // 3), its B/C positions past the row read zeros, and its steps past the row's end
 // are identity maps (dt = 0). TAIL: compiled only for rows with a tail chunk
 // (L % 256 != 0), so that the kernels for whole chunks carry none of its code.
-template <int I, bool REV, int SIO, bool SEG = false, bool ALN = true, bool TAIL = false>
+template <int I, bool REV, int SIO, bool SEG = false, bool ALN = true, bool TAIL = false,
+          bool DWBC = !ALN>
 __device__ __forceinline__ void tile_rows(const M1Kern& p, long long blk, int seg = 0) {
   static_assert(ALN || SIO == 0, "unaligned rows: contiguous z and out only");
   constexpr int LPR = 16, RPW = 4;
@@ -699,8 +707,8 @@ __device__ __forceinline__ void tile_rows(const M1Kern& p, long long blk, int se
   constexpr long long CH = G::CH;
   extern __shared__ __attribute__((aligned(16))) float s_lds[];
   float* tiles = s_lds;                                  // [2][G::FLOATS]
-  float* zbuf = s_lds + 2 * G::FLOATS;                   // SIO: [256][16] z stage
-  float* small = zbuf + (SIO >= 2 ? kZStageFloats : 0);  // carry, A*log2e, zeros
+  float* zbuf = s_lds + 2 * G::FLOATS;  // SIO 2, 3: [256][16] z stage; !ALN: out stage
+  float* small = zbuf + (SIO >= 2 || !ALN ? kZStageFloats : 0);  // carry, A*log2e, zeros
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -720,8 +728,9 @@ __device__ __forceinline__ void tile_rows(const M1Kern& p, long long blk, int se
   // strided z/out: the block's 16 rows share one batch, whose index taken from the
   // block id is wave-uniform (a buffer resource must be)
   const long long bib = blk * (kWavesPerBlock * RPW) / p.dim;
-  const float* Bg = p.B + ((long long)bi * p.groups + g) * N * L;
-  const float* Cg = p.C + ((long long)bi * p.groups + g) * N * L;
+  const long long ldb = p.ldb;
+  const float* Bg = p.B + ((long long)bi * p.groups + g) * N * ldb;
+  const float* Cg = p.C + ((long long)bi * p.groups + g) * N * ldb;
   const float* Arow = p.A + (long long)d * N;
   const float bias = p.bias ? p.bias[d] : 0.0f;
   const float dskip = p.D ? p.D[d] : 0.0f;
@@ -755,7 +764,8 @@ __device__ __forceinline__ void tile_rows(const M1Kern& p, long long blk, int se
   const long long ntiles = (cl - cb) * ng;
   auto mem0 = [&](long long c) { return REV ? L - (c + 1) * CH : c * CH; };
   if (ntiles > 0)
-    issue_tile<I, !ALN>(tiles, Bg, Cg, L, mem0(cb), 0, N, wave, lane, TAIL && cb >= nfull);
+    issue_tile<I, DWBC>(tiles, Bg, Cg, L, ldb, p.bpo, mem0(cb), 0, N, wave, lane,
+                        TAIL && cb >= nfull);
   // In a segment (one or a few chunks per block) the first tile's sync comes after
   // the first chunk's delta/u loads, in the loop, so that their latencies overlap.
   if (!segd || cl == cb) tile_sync();
@@ -805,10 +815,30 @@ __device__ __forceinline__ void tile_rows(const M1Kern& p, long long blk, int se
           *reinterpret_cast<float4*>(orow + m) = make_float4(w[0], w[1], w[2], w[3]);
       }
     } else {
-      float* base = orow + (REV ? L - sbo - I : sbo);
+      // Rows that are not 16-byte multiples: the wave's four rows of the chunk pass
+      // through a wave-private LDS buffer and leave with consecutive lanes storing
+      // consecutive steps (whole lines), where a lane's own 16 single floats would
+      // touch 16 lines 64 bytes apart (measured 186 -> 144 us at B8 D1536 L2050 with
+      // 16-byte moves in place of them). The 16-byte pieces are swizzled by lane
+      // block (q ^ j%4) to spread a row's writes over the banks.
+      static_assert(ALN || I == 16, "the out stage holds 16 steps per lane block");
+      float* wb = zbuf + wave * (RPW * CH);
 #pragma unroll
-      for (int i = 0; i < I; ++i)
-        if (sbo + i < L) base[REV ? I - 1 - i : i] = v[i];
+      for (int q = 0; q < I / 4; ++q)
+        *reinterpret_cast<float4*>(wb + rw * CH + 16 * j + 4 * (q ^ (j & 3))) =
+            make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+      const long long t0 = sbo - (long long)j * I + lane;  // this lane's first step
+      // the wave's first row at step t0; rows L floats apart, steps +-64 per round
+      float* ob = p.out + (blk * kWavesPerBlock + wave) * RPW * L + (REV ? L - 1 - t0 : t0);
+#pragma unroll
+      for (int r = 0; r < RPW; ++r)
+#pragma unroll
+        for (int k4 = 0; k4 < (int)CH / 64; ++k4) {
+          const int ps = 64 * k4 + lane;  // step of the chunk
+          const int jb = ps >> 4, i = ps & 15;
+          const float val = wb[r * CH + 16 * jb + 4 * ((i >> 2) ^ (jb & 3)) + (i & 3)];
+          if (full || t0 + 64 * k4 < L) ob[r * L + (REV ? -64 * k4 : 64 * k4)] = val;
+        }
     }
   };
 
@@ -872,7 +902,7 @@ __device__ __forceinline__ void tile_rows(const M1Kern& p, long long blk, int se
       if (k + 1 < ntiles) {  // the next tile: state group q + 1 of this chunk, or 0 of the next
         const bool same = q + 1 < ng;
         const long long cn = same ? c : c + 1;
-        issue_tile<I, !ALN>(tiles + ((k + 1) & 1) * G::FLOATS, Bg, Cg, L, mem0(cn),
+        issue_tile<I, DWBC>(tiles + ((k + 1) & 1) * G::FLOATS, Bg, Cg, L, ldb, p.bpo, mem0(cn),
                             same ? (q + 1) * kTileStates : 0, N, wave, lane,
                             TAIL && cn >= nfull);
       }
@@ -922,7 +952,7 @@ __device__ __forceinline__ void tile_rows(const M1Kern& p, long long blk, int se
 // segment of 16 rows (segments 0 .. segs-2), with the same discretisation and
 // fold as tile_state; the chunk maps compose in order. A of a chunk is
 // 2^(a2 * sum of the row's dt over it), one exponential.
-template <int I, bool REV, bool ALN = true>
+template <int I, bool REV, bool ALN = true, bool DWBC = !ALN>
 __device__ __forceinline__ void fold_rows(const M1Kern& p, long long blk, int seg) {
   constexpr int LPR = 16, RPW = 4;
   using G = Tile<I>;
@@ -944,7 +974,8 @@ __device__ __forceinline__ void fold_rows(const M1Kern& p, long long blk, int se
   const float* drow = p.delta + row * L;
   // strided u (the seam kernels): the block's 16 rows share one batch, wave-uniform
   const long long bib = blk * (kWavesPerBlock * RPW) / p.dim;
-  const float* Bg = p.B + ((long long)bi * p.groups + g) * N * L;
+  const long long ldb = p.ldb;
+  const float* Bg = p.B + ((long long)bi * p.groups + g) * N * ldb;
   const float bias = p.bias ? p.bias[d] : 0.0f;
   float* sA = small + (wave * RPW + rw) * N;
   float* sB = small + (kWavesPerBlock * RPW + wave * RPW + rw) * N;
@@ -962,7 +993,8 @@ __device__ __forceinline__ void fold_rows(const M1Kern& p, long long blk, int se
   const long long ntiles = (ce - cb) * ng;
   auto mem0 = [&](long long c) { return REV ? L - (c + 1) * CH : c * CH; };
   // the fold reads B only: the tiles' C rows are not fetched
-  if (ntiles > 0) issue_tile<I, !ALN>(tiles, Bg, nullptr, L, mem0(cb), 0, N, wave, lane);
+  if (ntiles > 0)
+    issue_tile<I, DWBC>(tiles, Bg, nullptr, L, ldb, p.bpo, mem0(cb), 0, N, wave, lane);
   long long k = 0;
   for (long long c = cb; c < ce; ++c) {
     const long long sb = c * CH + (long long)j * I;
@@ -996,7 +1028,7 @@ __device__ __forceinline__ void fold_rows(const M1Kern& p, long long blk, int se
       progress_prio(k, ntiles);
       if (k + 1 < ntiles) {  // the next tile: state group q + 1 of this chunk, or 0 of the next
         const bool same = q + 1 < ng;
-        issue_tile<I, !ALN>(tiles + ((k + 1) & 1) * G::FLOATS, Bg, nullptr, L,
+        issue_tile<I, DWBC>(tiles + ((k + 1) & 1) * G::FLOATS, Bg, nullptr, L, ldb, p.bpo,
                             mem0(same ? c : c + 1), same ? (q + 1) * kTileStates : 0, N, wave,
                             lane);
       }
@@ -1031,11 +1063,24 @@ __device__ __forceinline__ void fold_rows(const M1Kern& p, long long blk, int se
     }
 }
 
-template <int I, bool REV, bool ALN>
+template <int I, bool REV, bool ALN, bool DWBC>
 __global__ void __launch_bounds__(64 * kWavesPerBlock, 3)
 m1_seg_fold_kernel(M1Kern p) {
   const long long nblk = p.rows / (kWavesPerBlock * 4);
-  fold_rows<I, REV, ALN>(p, blockIdx.x % nblk, (int)(blockIdx.x / nblk));
+  fold_rows<I, REV, ALN, DWBC>(p, blockIdx.x % nblk, (int)(blockIdx.x / nblk));
+}
+
+// Rows of B or C copied to a row pitch of ldb floats (ldb >= L), each row's data
+// starting `off` floats in and zeros around it, so that the tiled kernel moves them
+// by 16-byte DMA.
+__global__ void __launch_bounds__(256) pad_rows_kernel(const float* __restrict__ src,
+                                                       float* __restrict__ dst, long long rows,
+                                                       long long L, long long ldb,
+                                                       long long off) {
+  const long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= rows * ldb) return;
+  const long long r = e / ldb, t = e - r * ldb - off;
+  dst[e] = t >= 0 && t < L ? src[r * L + t] : 0.0f;
 }
 
 // Block id -> row block for time-major z/out: a 128-byte line of those holds 32
@@ -1049,7 +1094,7 @@ __device__ __forceinline__ long long paired_block(long long bid, long long nblk)
 }
 
 // Block id -> (row block, segment): with SEG the segments are blockIdx / (row blocks).
-template <int I, bool REV, int SIO, bool SEG, bool ALN, bool TAIL>
+template <int I, bool REV, int SIO, bool SEG, bool ALN, bool TAIL, bool DWBC>
 __global__ void __launch_bounds__(64 * kWavesPerBlock, 3)
 m1_tile_kernel(M1Kern p) {
   const long long nblk = p.rows / (kWavesPerBlock * 4);
@@ -1065,7 +1110,7 @@ m1_tile_kernel(M1Kern p) {
   if (!SEG && nblk % 16 == 0) blk = (bid & 7) * (nblk / 8) + (bid >> 3);
   else if (SIO) blk = paired_block(bid, nblk);
   else if (!SEG && nblk % 8 == 0) blk = (bid & 7) * (nblk / 8) + (bid >> 3);
-  tile_rows<I, REV, SIO, SEG, ALN, TAIL>(p, blk, seg);
+  tile_rows<I, REV, SIO, SEG, ALN, TAIL, DWBC>(p, blk, seg);
 }
 
 // Several traversals of rows of the same shape in one launch (the directions of
@@ -1094,31 +1139,36 @@ m1_tile_jobs_kernel(M1Kern p, M1Jobs jobs) {
   else tile_rows<I, false, 0, false, ALN, TAIL>(p, blk);
 }
 
-template <int I, bool REV, int SIO, bool ALN>
+template <int I, bool REV, int SIO, bool ALN, bool DWBC>
 hipError_t launch_tile(const M1Kern& k, hipStream_t st) {
   constexpr int RPB = kWavesPerBlock * 4;
   const long long blocks = (long long)k.rows / RPB;
   const int segs = k.segs > 1 ? k.segs : 1;
   if (segs > 1) {  // pass 1: the maps of segments 0 .. segs-2
     const size_t lds1 = sizeof(float) * (2 * (size_t)Tile<I>::FLOATS + 3 * (size_t)RPB * k.N);
-    hipLaunchKernelGGL((m1_seg_fold_kernel<I, REV, ALN>), dim3((unsigned)(blocks * (segs - 1))),
+    hipLaunchKernelGGL((m1_seg_fold_kernel<I, REV, ALN, DWBC>),
+                       dim3((unsigned)(blocks * (segs - 1))),
                        dim3(64 * kWavesPerBlock), lds1, st, k);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
   const size_t lds =
-      sizeof(float) * (2 * (size_t)Tile<I>::FLOATS + (SIO >= 2 ? kZStageFloats : 0) +
+      sizeof(float) * (2 * (size_t)Tile<I>::FLOATS + (SIO >= 2 || !ALN ? kZStageFloats : 0) +
                        (2 * (size_t)RPB + 1) * k.N);
   const dim3 grid((unsigned)(segs > 1 ? blocks * segs : blocks)), wg(64 * kWavesPerBlock);
   const bool tail = k.L % Tile<I>::CH != 0;
   if (segs > 1 && tail)
-    hipLaunchKernelGGL((m1_tile_kernel<I, REV, SIO, true, ALN, true>), grid, wg, lds, st, k);
+    hipLaunchKernelGGL((m1_tile_kernel<I, REV, SIO, true, ALN, true, DWBC>), grid, wg, lds, st,
+                       k);
   else if (segs > 1)
-    hipLaunchKernelGGL((m1_tile_kernel<I, REV, SIO, true, ALN, false>), grid, wg, lds, st, k);
+    hipLaunchKernelGGL((m1_tile_kernel<I, REV, SIO, true, ALN, false, DWBC>), grid, wg, lds, st,
+                       k);
   else if (tail)
-    hipLaunchKernelGGL((m1_tile_kernel<I, REV, SIO, false, ALN, true>), grid, wg, lds, st, k);
+    hipLaunchKernelGGL((m1_tile_kernel<I, REV, SIO, false, ALN, true, DWBC>), grid, wg, lds, st,
+                       k);
   else
-    hipLaunchKernelGGL((m1_tile_kernel<I, REV, SIO, false, ALN, false>), grid, wg, lds, st, k);
+    hipLaunchKernelGGL((m1_tile_kernel<I, REV, SIO, false, ALN, false, DWBC>), grid, wg, lds,
+                       st, k);
   return hipGetLastError();
 }
 
@@ -1153,6 +1203,7 @@ hipError_t m1_scan_jobs(const M1Problem& pr, const M1JobSpec* spec, int n, hipSt
   M1Kern k{};
   k.A = pr.A; k.D = pr.D; k.bias = pr.bias; k.h0 = nullptr;
   k.L = (long long)pr.len; k.rows = (int)(pr.batch * pr.dim); k.dim = (int)pr.dim;
+  k.ldb = k.L; k.bpo = 0;
   k.N = (int)pr.state; k.groups = 1; k.group_size = (int)pr.dim;
   k.softplus = pr.softplus;
   M1Jobs jobs{};
@@ -1166,8 +1217,8 @@ hipError_t m1_scan_jobs(const M1Problem& pr, const M1JobSpec* spec, int n, hipSt
     jobs.job[i] = M1Job{j.u, j.delta, j.z, j.B, j.C, j.out, j.last, j.rev};
   }
   const long long blocks = 8LL * n * ((jobs.blocks_per_job + 7) / 8);
-  const size_t lds =
-      sizeof(float) * (2 * (size_t)Tile<M1_TILE_I>::FLOATS + (2 * (size_t)16 + 1) * k.N);
+  const size_t lds = sizeof(float) * (2 * (size_t)Tile<M1_TILE_I>::FLOATS +
+                                      (aln ? 0 : kZStageFloats) + (2 * (size_t)16 + 1) * k.N);
   const bool tail = k.L % Tile<M1_TILE_I>::CH != 0;
   const dim3 grid((unsigned)blocks), wg(64 * kWavesPerBlock);
   if (aln && tail)
@@ -1256,13 +1307,13 @@ hipError_t plan_segments(M1Kern& k, float* scratch_p, size_t scratch_bytes, hipS
   return stream_alloc((void**)&k.segmap, map_bytes(k.segs), st);
 }
 
-template <int SIO, bool ALN = true>
+template <int SIO, bool ALN = true, bool DWBC = false>
 hipError_t run_tile(M1Kern& k, bool rev, float* scratch_p, size_t scratch_bytes,
                     hipStream_t st) {
   hipError_t e = plan_segments(k, scratch_p, scratch_bytes, st);
   if (e != hipSuccess) return e;
-  e = rev ? launch_tile<M1_TILE_I, true, SIO, ALN>(k, st)
-          : launch_tile<M1_TILE_I, false, SIO, ALN>(k, st);
+  e = rev ? launch_tile<M1_TILE_I, true, SIO, ALN, DWBC>(k, st)
+          : launch_tile<M1_TILE_I, false, SIO, ALN, DWBC>(k, st);
   if (k.segmap && !scratch_p) {
     const hipError_t fe = hipFreeAsync(k.segmap, st);
     if (e == hipSuccess) e = fe;
@@ -1304,6 +1355,7 @@ hipError_t m1_scan_chunked(const M1Problem& pr, hipStream_t st) {
   k.u = pr.u; k.delta = pr.delta; k.A = pr.A; k.B = pr.B; k.C = pr.C; k.D = pr.D; k.z = pr.z;
   k.bias = pr.bias; k.h0 = pr.h0; k.out = pr.out; k.last = pr.last;
   k.L = (long long)pr.len; k.rows = (int)(pr.batch * pr.dim); k.dim = (int)pr.dim;
+  k.ldb = k.L; k.bpo = 0;
   k.N = (int)pr.state; k.groups = (int)pr.groups; k.group_size = (int)(pr.dim / pr.groups);
   k.softplus = pr.softplus;
   const bool vec = pr.len % 4 == 0 && aligned16(pr.u) && aligned16(pr.delta) &&
@@ -1338,13 +1390,40 @@ hipError_t m1_scan_chunked(const M1Problem& pr, hipStream_t st) {
                      : run_tile<2>(k, rev, pr.scratch, pr.scratch_bytes, st);
     return run_tile<1>(k, rev, pr.scratch, pr.scratch_bytes, st);
   }
-  // the tiled path needs every 16-row block inside one batch/group; rows that are not
-  // 16-byte aligned move as single floats
+  // the tiled path needs every 16-row block inside one batch/group
   const bool tiled = pr.dim % 16 == 0 && (pr.dim / pr.groups) % 16 == 0;
-  if (tiled)
-    return vec ? run_tile<0, true>(k, rev, pr.scratch, pr.scratch_bytes, st)
-               : run_tile<0, false>(k, rev, pr.scratch, pr.scratch_bytes, st);
-  return launch_dir<16, 16>(k, rev, vec, st);
+  if (!tiled) return launch_dir<16, 16>(k, rev, vec, st);
+  if (vec) return run_tile<0, true>(k, rev, pr.scratch, pr.scratch_bytes, st);
+  // Rows that are not 16-byte multiples: u, delta, z and out move as single floats.
+  // B and C (shared by every channel, a few MB) are copied to a row pitch rounded up
+  // to 4 so that the tiles still fill by 16-byte DMA (B8 D1536 L2050: 209 -> 187 us
+  // with 16-byte DMA). The allocation-free entry, which owns no memory for the copy,
+  // moves them as single floats instead.
+  if (k.L % 4 == 0 && aligned16(pr.B) && aligned16(pr.C))
+    return run_tile<0, false, false>(k, rev, pr.scratch, pr.scratch_bytes, st);
+  if (pr.scratch) return run_tile<0, false, true>(k, rev, pr.scratch, pr.scratch_bytes, st);
+  const long long ldb = (k.L + 3) & ~3LL;
+  const long long off = rev ? ldb - k.L : 0;  // reverse chunks end at L: pad in front
+  const long long bcrows = (long long)pr.batch * pr.groups * pr.state;
+  const long long n = bcrows * ldb;
+  float* pad = nullptr;
+  hipError_t e = stream_alloc((void**)&pad, 2 * (size_t)n * sizeof(float), st);
+  if (e != hipSuccess) return e;
+  const unsigned pblocks = (unsigned)((n + 255) / 256);
+  hipLaunchKernelGGL(pad_rows_kernel, dim3(pblocks), dim3(256), 0, st, pr.B, pad, bcrows, k.L,
+                     ldb, off);
+  hipLaunchKernelGGL(pad_rows_kernel, dim3(pblocks), dim3(256), 0, st, pr.C, pad + n, bcrows,
+                     k.L, ldb, off);
+  e = hipGetLastError();
+  if (e == hipSuccess) {
+    k.B = pad + off;  // each row's first data float
+    k.C = pad + n + off;
+    k.ldb = ldb;
+    k.bpo = off;
+    e = run_tile<0, false, false>(k, rev, nullptr, 0, st);
+  }
+  const hipError_t fe = hipFreeAsync(pad, st);
+  return e != hipSuccess ? e : fe;
 }
 
 }  // namespace armscan

@@ -59,3 +59,16 @@ def test_noalloc_plan_cut_to_the_scratch():
     for out, last in ((got, got_last), (ref, ref_last)):
         assert rel_err(out, o64) < 1e-4 and rel_err(last, l64) < 1e-4
     assert rel_err(got, ref) < 1e-4
+
+
+@pytest.mark.parametrize("reverse", [False, True])
+def test_noalloc_unaligned_rows(reverse):
+    """Rows that are not 16-byte multiples (L % 4 != 0): the allocating entry copies B
+    and C to a padded pitch and fills the tiles by 16-byte DMA, the allocation-free one
+    moves them as single floats into the same tiles; the results are bit-identical."""
+    for (b, d, L, n, seed) in ((1, 1536, 2050, 16, 43), (2, 256, 1030, 13, 44)):
+        case(f"noalloc unaligned {b}x{d}x{L} N{n} reverse={reverse}")
+        x = workloads.m1_layer(batch=b, dim=d, length=L, state=n, seed=seed)
+        got, got_last = _call("arm_scan_selective_scan_noalloc_f32", x, True, reverse)
+        ref, ref_last = _call("arm_scan_selective_scan_f32", x, True, reverse)
+        assert np.array_equal(got, ref) and np.array_equal(got_last, ref_last)
