@@ -121,6 +121,35 @@ def test_m1_optional_inputs_absent(dim):
     assert rel_err(host(out), ref) < TOL and rel_err(host(last), ref_last) < TOL
 
 
+@pytest.mark.parametrize("reverse", [False, True])
+@pytest.mark.parametrize("shifted", ["u_delta_z", "all"])
+def test_m1_unaligned_bases(shifted, reverse):
+    """L % 4 == 0 but inputs placed one float past an aligned base: u, delta and z (B/C
+    aligned: read in place by 16-byte DMA) or every tensor (B/C copied to an aligned
+    pitch). The tiled kernel with single-float row moves, against the oracle."""
+    import torch
+    import armhackathon_amd as arm_scan
+
+    case(f"m1 unaligned bases {shifted} reverse={reverse}")
+    x = workloads.m1_layer(batch=2, dim=32, length=1000, state=16, seed=7)
+    names = ("u", "delta", "z") if shifted == "u_delta_z" else ("u", "delta", "z", "B", "C")
+
+    def place(k, a):
+        if k not in names:
+            return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+        t = torch.empty(a.size + 1, dtype=torch.float32, device="cuda")
+        t[1:] = torch.from_numpy(np.ascontiguousarray(a)).reshape(-1).cuda()
+        return t[1:].view(a.shape)
+
+    t = {k: place(k, v) for k, v in x.items()}
+    out, last = arm_scan.selective_scan(t["u"], t["delta"], t["A"], t["B"], t["C"], D=t["D"],
+                                        z=t["z"], delta_bias=t["delta_bias"],
+                                        delta_softplus=True, return_last_state=True,
+                                        reverse=reverse)
+    ref, ref_last = _ref(x, delta_softplus=True, reverse=reverse)
+    assert rel_err(host(out), ref) < TOL and rel_err(host(last), ref_last) < TOL
+
+
 def test_m1_reverse_is_flip_forward_flip():
     """property.rs:138: reverse == flip -> forward -> flip."""
     x = workloads.m1_op(batch=2, dim=32, length=3000, state=16, seed=4)
