@@ -698,6 +698,9 @@ __device__ __forceinline__ void tile_states(const float* tile, int n0, int N, in
 // 3), its B/C positions past the row read zeros, and its steps past the row's end
 // are identity maps (dt = 0). TAIL: compiled only for rows with a tail chunk
 // (L % 256 != 0), so that the kernels for whole chunks carry none of its code.
+// DWBC: B/C rows are not 16-byte multiples in memory, and the tiles fill by single-float
+// DMA (the allocation-free entry, the multi-traversal launch); otherwise their rows are
+// (a padded copy of pitch p.ldb where L % 4 != 0).
 template <int I, bool REV, int SIO, bool SEG = false, bool ALN = true, bool TAIL = false,
           bool DWBC = !ALN>
 __device__ __forceinline__ void tile_rows(const M1Kern& p, long long blk, int seg = 0) {
