@@ -86,7 +86,10 @@ uint32_t arm_scan_abi_version(void);
 /* Replaces arm_scan_selective_scan_f32 (arm-scan-ffi/src/lib.rs:99-216).
  * Nullable: d_skip, z, delta_bias, last_state, h0. `reverse` walks the sequence
  * backward (output t still lands at index t; last_state is then the state after
- * consuming t == 0). h0 seeds the recurrence (orthogonal to reverse). */
+ * consuming t == 0). h0 seeds the recurrence (orthogonal to reverse).
+ * Device scratch, from a memory pool the library owns: the segment maps of the plan
+ * for few rows and, for rows that are not 16-byte multiples (len % 4 != 0 or an
+ * unaligned B/C), a copy of B and C at a padded row pitch. */
 int arm_scan_selective_scan_f32(const ArmScanDims* dims, const float* u, const float* delta,
                                 const float* a, const float* b, const float* c,
                                 const float* d_skip, const float* z, const float* delta_bias,
@@ -95,10 +98,12 @@ int arm_scan_selective_scan_f32(const ArmScanDims* dims, const float* u, const f
 
 /* No reference counterpart: arm_scan_selective_scan_f32 for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops, harnesses
- * that forbid hipMalloc). Same arguments, checks, codes and kernels; it calls no
- * hipMalloc/hipFree. The only scratch of this scan, the segment maps of the plan for
- * few rows (B * D < 8192: rows cut into segments folded first, then replayed), lives
- * in a static 4 MiB device array instead, one per GPU, held until the process ends.
+ * that forbid hipMalloc). Same arguments, checks, codes and results (bit-identical); it
+ * calls no hipMalloc/hipFree. Rows that are not 16-byte multiples read B and C in place
+ * as single floats instead of through a padded copy. The only scratch it keeps, the
+ * segment maps of the plan for few rows (B * D < 8192: rows cut into segments folded
+ * first, then replayed), lives in a static 4 MiB device array, one per GPU, held until
+ * the process ends.
  * No size is rejected for it: a plan whose maps would exceed 4 MiB is cut to fewer
  * segments (whole rows need none). Every map is written before it is read, so no
  * call depends on what the array held before. Calls that overlap on one GPU (two
