@@ -86,6 +86,7 @@ SHAPES = [
     # few rows: the segmented scan (fold + replay) with a tail, aligned and not
     (1, 1536, 2052, 16, 1),
     (1, 1536, 2050, 16, 1),
+    (1, 1536, 777, 13, 1),
 ]
 
 
@@ -191,12 +192,14 @@ def test_m1_deterministic():
 
 def test_m1_bidirectional_fused():
     """Fused pair == forward scan + reverse scan (property.rs:240). Every route of
-    the entry point: the two-traversal launch (dim % 16 == 0, L % 4 == 0: 16x1024,
-    32x4096), the single-pass kernel (L 700, dim 8) and two launches (dim 4, L 6000)."""
+    the entry point: the two-traversal launch (dim % 16 == 0: 16x1024 and 32x4096 whole
+    chunks, 16x700 with a tail chunk, 16x1001 with unaligned rows), the single-pass
+    kernel (dim 8, L 2048) and two launches (dim 4, L 6000)."""
     import armhackathon_amd as arm_scan
     from armhackathon_amd.op import selective_scan_bidirectional_with_state
 
-    for (b, d, L) in ((2, 16, 700), (1, 8, 2048), (1, 4, 6000), (1, 16, 1024), (2, 32, 4096)):
+    for (b, d, L) in ((2, 16, 700), (1, 8, 2048), (1, 4, 6000), (1, 16, 1024), (2, 32, 4096),
+                      (2, 16, 1001)):
         case(f"m1 bidirectional {b}x{d}x{L}")
         x = workloads.m1_op(batch=b, dim=d, length=L, state=16, seed=L)
         x["delta_bias"] = np.full(d, -0.5, np.float32)
