@@ -22,9 +22,10 @@
 //      its partial G^T = K Q^T over its n-tile (4 MFMA),
 //      per slice its partial Q S0^T (4 MFMA),
 //      per slice the update of its S piece (4 MFMA, K transposed through LDS).
-//    The partials meet in LDS; wave j < PT finishes slice j of a chunk while the
-//    partials of the next chunk are computed: masked intra-chunk term (4 MFMA),
-//    D x, gating, rank sum, store.
+//    The partials meet in LDS; two epilogue waves per slice, one for the even
+//    chunks and one for the odd, finish a chunk over the next two chunks' time:
+//    the reduction of the partials, then the masked intra-chunk term (4 MFMA), D x,
+//    gating, rank sum, store.
 //
 // Every input of a chunk (q, k, cos, sin, v and z rows and the gate record)
 // reaches LDS by direct-to-LDS DMA (global_load_lds_dwordx4) NS-1 chunks ahead,
@@ -454,8 +455,8 @@ struct Stash {
 };
 
 // Waves 0 .. WN-1 compute the partials of n-tile `wave` for every slice of the
-// block; waves WN .. WN+PT-1 finish slice wave-WN of the previous chunk. Both kinds
-// pass one barrier per chunk.
+// block; waves WN .. WN+2PT-1 finish slice (wave-WN) % PT of the chunks of parity
+// (wave-WN) / PT. Both kinds pass one barrier per chunk.
 // ACC: an accumulating traversal (p.accum; SISO without angles), a template parameter
 // so that the other kernels carry none of its epilogue work. ZOWN: z's step stride
 // differs from v's; otherwise z's DMA pieces share v's per-chunk step, one scalar
@@ -463,7 +464,7 @@ struct Stash {
 // slower at config 3 with the two strides kept apart).
 template <int R, bool MIMO, bool REV, int PT, bool ANG, bool ACC = false, bool ZOWN = false,
           int MD = kMaxDma>
-__global__ void __launch_bounds__(64 * (kMaxWaves + 2)) m3_chunk_kernel(M3K p) {
+__global__ void __launch_bounds__(64 * (kMaxWaves + 4)) m3_chunk_kernel(M3K p) {
   extern __shared__ __attribute__((aligned(16))) float sm[];
   const int WN = p.dqk / 16;
   const int lane = threadIdx.x & 63;
@@ -476,7 +477,12 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 2)) m3_chunk_kernel(M3K p) {
                        : (MIMO && ANG && WN % 2 == 0)
                              ? ((wave & 1) ? WN / 2 + (wave >> 1) : (wave >> 1))
                              : wave;
-  const int ej = ewave ? wave - WN : 0;             // slice of an epilogue wave
+  // epilogue waves: two per slice, taking the chunks of one parity each; a chunk's
+  // epilogue spans two barrier intervals (reduce, then MFMA and store), so in every
+  // interval the reductions of one parity and the finishing of the other run on
+  // different SIMDs
+  const int ej = ewave ? (wave - WN) % PT : 0;      // slice of an epilogue wave
+  const int epar = ewave ? (wave - WN) / PT : 0;    // chunk parity of an epilogue wave
   const int li = lane & 15, lj = lane >> 4;
   // blocks of one sequence share an XCD (block id mod 8), and so its L2
   const int bx = blockIdx.x & 7, by = blockIdx.x >> 3;
@@ -534,18 +540,11 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 2)) m3_chunk_kernel(M3K p) {
     const bool has_z = p.z != nullptr;
     const int nchunks = p.nchunks, sfl = p.stage_floats;
     const long long chstep = (REV ? -(long long)T : (long long)T) * ostep;  // per chunk
-    float* orow = out_lane;  // the lane's first output of the chunk being finished
-    // FULL: every row of the chunk lies inside the sequence (all chunks but the last)
-    auto epilogue = [&](int ch, auto full) {
-      constexpr bool FULL = decltype(full)::value;
-      auto valid = [&](int r) { return FULL || ch * T + (4 * lj + r) / R < L; };
-      // the other traversal's output, under accumulation (loaded first, used last)
-      float prev[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-      if constexpr (ACC) {
-#pragma unroll
-        for (int r = 0; r < 4; r += R)
-          if (valid(r)) prev[r] = orow[(REV ? -(r / R) : r / R) * ostep];
-      }
+    // part A of chunk ch: the partials reduced and masked (lane: G[li][4lj + r] and the
+    // inter-chunk Y[4lj + r][p]); it reads the partial buffers right after the
+    // barrier that publishes them
+    f4 G = {0.0f, 0.0f, 0.0f, 0.0f}, Y = {0.0f, 0.0f, 0.0f, 0.0f};
+    auto part_a = [&](int ch) {
       const float* gb = gbuf + (ch & 1) * kMaxWaves * 256;
       const float* yb = ybuf + ((ch & 1) * PT + ej) * kMaxWaves * 256;
       f4 gs[kMaxWaves], ys[kMaxWaves];  // all reads in flight at once
@@ -561,24 +560,37 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 2)) m3_chunk_kernel(M3K p) {
           gs[w2] += gs[w2 + d];
           ys[w2] += ys[w2 + d];
         }
-      f4 G = gs[0] * st.m;   // lane holds G[i = li][s = 4lj + r], masked
-      f4 Y = ys[0] * st.ec;  // lane holds Y[row = 4lj + r][p], the inter-chunk part
+      G = gs[0] * st.m;
+      Y = ys[0] * st.ec;
+    };
+    // part B of chunk ch: the intra-chunk term, D x, gating, rank sum, store.
+    // FULL: every row of the chunk lies inside the sequence (all chunks but the last)
+    auto part_b = [&](int ch, auto full) {
+      constexpr bool FULL = decltype(full)::value;
+      auto valid = [&](int r) { return FULL || ch * T + (4 * lj + r) / R < L; };
+      float* orow = out_lane + (long long)ch * chstep;
+      float prev[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      if constexpr (ACC) {
 #pragma unroll
-      for (int m = 0; m < 4; ++m) Y = mfma(G[m], st.x[m], Y);
+        for (int r = 0; r < 4; r += R)
+          if (valid(r)) prev[r] = orow[(REV ? -(r / R) : r / R) * ostep];
+      }
+      f4 Yc = Y;
+#pragma unroll
+      for (int m = 0; m < 4; ++m) Yc = mfma(G[m], st.x[m], Yc);
 #pragma unroll
       for (int r = 0; r < 4; r += R) {
         if (valid(r)) {
           float acc = prev[r];
 #pragma unroll
           for (int rr = 0; rr < R; ++rr) {
-            float term = Y[r + rr] + dskip * st.x[r + rr];
+            float term = Yc[r + rr] + dskip * st.x[r + rr];
             if (has_z) term *= silu_fast(st.z[r] * zeta[r + rr]);
             acc = fmaf(phi[r + rr], term, acc);
           }
           orow[(REV ? -(r / R) : r / R) * ostep] = acc;
         }
       }
-      orow += chstep;
     };
     // what the epilogue of a chunk needs from its stage
     auto stash = [&](const float* sg) {
@@ -603,16 +615,24 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 2)) m3_chunk_kernel(M3K p) {
       }
     };
     lds_barrier();  // stage 0 landed
-    stash(stages);
+    if (epar == 0) stash(stages);
     int slot = 0;
     for (int ch = 1; ch < nchunks; ++ch) {
       slot = slot + 1 == NS ? 0 : slot + 1;
       lds_barrier();  // stage ch landed, partials of chunk ch-1 written
-      epilogue(ch - 1, std::true_type{});
-      stash(stages + slot * sfl);
+      const int c = ch - 1;
+      if ((c & 1) == epar) part_a(c);
+      else if (c >= 1) part_b(c - 1, std::true_type{});  // this wave's previous chunk
+      if ((ch & 1) == epar) stash(stages + slot * sfl);
     }
-    lds_barrier();
-    epilogue(nchunks - 1, std::false_type{});
+    lds_barrier();  // partials of the last chunk written
+    const int cl = nchunks - 1;
+    if ((cl & 1) == epar) {
+      part_a(cl);
+      part_b(cl, std::false_type{});
+    } else if (cl >= 1) {
+      part_b(cl - 1, std::true_type{});
+    }
     return;
   }
 
@@ -868,24 +888,24 @@ hipError_t launch_chunk(const M3K& k, bool rev, hipStream_t st) {
   if (k.ang) {  // forward only: theta is a forward cumsum
     if (rev) return hipErrorInvalidValue;
     hipLaunchKernelGGL((m3_chunk_kernel<R, MIMO, false, PT, true, false, ZOWN, MD>),
-                       dim3((unsigned)blocks), dim3(64 * (WN + PT)), lds, st, k);
+                       dim3((unsigned)blocks), dim3(64 * (WN + 2 * PT)), lds, st, k);
   } else if (k.accum) {
     if constexpr (R == 1 && !MIMO) {
       if (rev)
         hipLaunchKernelGGL((m3_chunk_kernel<1, false, true, PT, false, true, ZOWN, MD>),
-                           dim3((unsigned)blocks), dim3(64 * (WN + PT)), lds, st, k);
+                           dim3((unsigned)blocks), dim3(64 * (WN + 2 * PT)), lds, st, k);
       else
         hipLaunchKernelGGL((m3_chunk_kernel<1, false, false, PT, false, true, ZOWN, MD>),
-                           dim3((unsigned)blocks), dim3(64 * (WN + PT)), lds, st, k);
+                           dim3((unsigned)blocks), dim3(64 * (WN + 2 * PT)), lds, st, k);
     } else {
       return hipErrorInvalidValue;  // accumulation is SISO only (m3_scan checks it)
     }
   } else if (rev) {
     hipLaunchKernelGGL((m3_chunk_kernel<R, MIMO, true, PT, false, false, ZOWN, MD>),
-                       dim3((unsigned)blocks), dim3(64 * (WN + PT)), lds, st, k);
+                       dim3((unsigned)blocks), dim3(64 * (WN + 2 * PT)), lds, st, k);
   } else {
     hipLaunchKernelGGL((m3_chunk_kernel<R, MIMO, false, PT, false, false, ZOWN, MD>),
-                       dim3((unsigned)blocks), dim3(64 * (WN + PT)), lds, st, k);
+                       dim3((unsigned)blocks), dim3(64 * (WN + 2 * PT)), lds, st, k);
   }
   return hipGetLastError();
 }
