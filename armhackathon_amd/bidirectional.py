@@ -1,10 +1,14 @@
 """Bidirectional selective scan (python/arm_scan/bidirectional.py:98-175).
 
 The same projected tensors traversed in both time directions and merged.
-The tied-weights case goes through the fused kernel
-(`selective_scan_bidirectional`), which reads u/delta/B/C/z once and evaluates
-exp(delta*A) once for both directions. Untied weights (`reverse_params`) run
-two scans, the backward one in the kernel's reverse index mode (no flips).
+The tied-weights case goes through one call of the bidirectional entry point
+(`selective_scan_bidirectional`): where its 16-row blocks fill the chip, both
+directions run as two traversals of one launch, each evaluating its own
+exp(delta*A) (measured faster than sharing it, whose whole-row scans and barriers
+cost more than the exp); rows that fit one on-chip pass on fewer rows take the
+kernel that shares exp(delta*A) between the directions; the rest, two launches.
+Untied weights (`reverse_params`) run two scans, the backward one in the kernel's
+reverse index mode (no flips).
 
 Merge semantics are the reference's: "sum" | "mean" | "concat" | "none"; D and
 z apply inside each direction, so a "sum" carries 2*D*u.

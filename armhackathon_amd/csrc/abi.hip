@@ -255,9 +255,15 @@ int arm_scan_selective_scan_bidirectional_f32(
   // evaluates exp(dt A) once per direction, yet at B16 D192 it takes 49 / 91 / 173 us
   // for L 1024 / 2048 / 4096 against 59 / 92 us for the single-pass kernel that shares
   // the exp (whose whole-row scans and barriers cost more than the exp they save) and
-  // 222 us for two launches at L 4096.
+  // 222 us for two launches at L 4096. That launch scans whole rows, one 16-row block
+  // each, so it is taken where its blocks fill the chip (the single-direction scan
+  // would not cut rows into segments either: 256 row blocks or more, or rows of fewer
+  // than two chunks). Fewer rows take the exp-sharing kernel where a row fits it, else
+  // two launches, each cutting its rows into segments.
   p.out = out_fwd;
-  if (armscan::m1_jobs_supported(p)) {
+  const bool jobs_fill = 2 * (dims->batch * dims->dim / 16) >= armscan::kM1WholeRowBlocks ||
+                         dims->len < 2 * armscan::kM1ChunkSteps;
+  if (jobs_fill && armscan::m1_jobs_supported(p)) {
     const armscan::M1JobSpec jobs[2] = {{u, delta, z, b, c, out_fwd, last_fwd, 0},
                                         {u, delta, z, b, c, out_bwd, last_bwd, 1}};
     return run(armscan::m1_scan_jobs(p, jobs, 2, st), "bidirectional launch");

@@ -31,6 +31,7 @@
 #include <atomic>
 #include <cstdint>
 #include <type_traits>
+#include <utility>
 
 #include "scan_common.h"
 #include "scan_launch.h"
@@ -1282,12 +1283,13 @@ namespace {
 // it, cutting the plan to fewer segments (down to whole rows, which need no maps)
 // until they fit.
 hipError_t plan_segments(M1Kern& k, float* scratch_p, size_t scratch_bytes, hipStream_t st) {
+  static_assert(16 * M1_TILE_I == kM1ChunkSteps, "chunk size shared with the ABI's routing");
   const long long blocks = k.rows / 16;
   const long long nfull = k.L / (16 * M1_TILE_I);
   k.segs = 1;
   k.seg_chunks = nfull;
   k.segmap = nullptr;
-  if (blocks >= 512 || nfull < 2) return hipSuccess;
+  if (blocks >= kM1WholeRowBlocks || nfull < 2) return hipSuccess;
   long long segs = (768 + blocks - 1) / blocks;
   if (segs > nfull) segs = nfull;
   auto map_bytes = [&](long long s) {
@@ -1330,6 +1332,26 @@ bool m1_strided_io(const M1Problem& pr) {
          !contiguous_strides(pr.out_stride, pr) || !contiguous_strides(pr.u_stride, pr);
 }
 
+// Whether a strided (batch, dim, len) layout gives every element its own address:
+// with the dimensions of more than one element sorted by stride, each stride must
+// step past the whole extent of the smaller ones. (This also rejects some exotic
+// interleavings that do not overlap; no tensor view produces those.)
+bool distinct_elements(const long long (&s)[3], const M1Problem& pr) {
+  const long long n[3] = {(long long)pr.batch, (long long)pr.dim, (long long)pr.len};
+  int ord[3], k = 0;
+  for (int i = 0; i < 3; ++i)
+    if (n[i] > 1) ord[k++] = i;
+  for (int a = 1; a < k; ++a)  // insertion sort by stride
+    for (int b = a; b > 0 && s[ord[b]] < s[ord[b - 1]]; --b) std::swap(ord[b], ord[b - 1]);
+  long long extent = 0;  // largest offset reached by the smaller dimensions
+  for (int a = 0; a < k; ++a) {
+    const int i = ord[a];
+    if (s[i] <= extent) return false;
+    extent += s[i] * (n[i] - 1);
+  }
+  return true;
+}
+
 bool m1_strided_supported(const M1Problem& pr, const char** why) {
   auto no = [&](const char* w) {
     if (why) *why = w;
@@ -1346,7 +1368,8 @@ bool m1_strided_supported(const M1Problem& pr, const char** why) {
     if (t == 0 && !pr.z) continue;
     if (contiguous_strides(s, pr)) continue;
     if (s[0] < 0 || s[1] < 0 || s[2] < 0) return no("negative z/out/u strides");
-    if (t == 1 && (s[1] == 0 || s[2] == 0)) return no("out strides must not be zero");
+    if (t == 1 && !distinct_elements(s, pr))
+      return no("out strides make elements overlap (a zero or too small stride)");
     if (slab_bytes(s, pr) >= (1LL << 32) || 4LL * (M1_TILE_I - 1) * s[2] >= (1LL << 31))
       return no("a batch of strided z/out/u must span less than 4 GiB");
   }

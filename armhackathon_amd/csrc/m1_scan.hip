@@ -433,19 +433,19 @@ __global__ void __launch_bounds__(256) transpose_batch_kernel(TransposeBatch b, 
 }
 
 // out = scale * (out + p1 + T(q2) + T(q3)); q2, q3 are (planes, W, H).
-// One 64 x 64 tile of one plane per block and iteration; float4 rows when H and W
-// are multiples of 4.
+// One 64 x 64 tile of one plane per block and iteration; float4 rows when `vec`: H and
+// W multiples of 4 and all four tensors 16-byte aligned (the host checks; out is the
+// caller's and may sit at any float offset).
 __global__ void __launch_bounds__(256) merge4t_kernel(float* __restrict__ out,
                                                       const float* __restrict__ p1,
                                                       const float* __restrict__ q2,
                                                       const float* __restrict__ q3,
                                                       long long planes, int H, int W,
-                                                      float scale) {
+                                                      float scale, int vec) {
   __shared__ float t2[64][65], t3[64][65];
   const int tiles_w = (W + 63) / 64;
   const int i0 = (blockIdx.x / tiles_w) * 64, j0 = (blockIdx.x % tiles_w) * 64;
   const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;  // 16 x 16
-  const bool vec = (W % 4 == 0) && (H % 4 == 0);
   for (long long g = blockIdx.y; g < planes; g += gridDim.y) {
     const long long plane = g * H * W;
     for (int r = ty; r < 64; r += 16) {
@@ -634,8 +634,10 @@ hipError_t merge4_transposed(float* out, const float* p1, const float* q2, const
                              long long planes, int H, int W, float scale, hipStream_t st) {
   const long long tiles = (long long)((H + 63) / 64) * ((W + 63) / 64);
   const long long ny = planes < 65535 ? planes : 65535;
+  auto a16 = [](const void* q) { return ((uintptr_t)q & 15u) == 0; };
+  const int vec = W % 4 == 0 && H % 4 == 0 && a16(out) && a16(p1) && a16(q2) && a16(q3);
   hipLaunchKernelGGL(merge4t_kernel, dim3((unsigned)tiles, (unsigned)ny), dim3(256), 0, st, out,
-                     p1, q2, q3, planes, H, W, scale);
+                     p1, q2, q3, planes, H, W, scale, vec);
   return hipGetLastError();
 }
 

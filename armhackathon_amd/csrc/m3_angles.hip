@@ -18,6 +18,12 @@
 // cut into segments: a first kernel sums each segment's increments, and the block
 // of segment s starts from the sum of the segments before it. Pieces whose pairs
 // are all past r only write the identity rotation.
+//
+// Angles are summed in turns (theta / 2pi; an increment is tanh(angle) * dt / 2) and
+// every carried sum is reduced to [-1/2, 1/2] turns, the period of cos/sin: a sum
+// never grows, so each add rounds at ulp(1/2) turns, where a running theta in
+// radians rounds at ulp(theta) (1.5e-5 rad near 225 rad, which one-signed angles
+// reach over 4096 steps).
 
 #include <hip/hip_runtime.h>
 
@@ -46,6 +52,9 @@ constexpr int kPieces = 8;                         // pieces of 4 pairs per line
 constexpr int kStepLanes = kAngThreads / kPieces;  // 32
 constexpr int kAngSteps = 4;                       // consecutive steps per thread and tile
 constexpr int kTile = kStepLanes * kAngSteps;      // 128 steps
+
+// x turns reduced to [-1/2, 1/2] (exact: x - rint(x) is representable)
+__device__ __forceinline__ float turns_mod1(float x) { return x - __builtin_rintf(x); }
 
 // tanh(a) = 1 - 2 / (1 + e^{2a}); saturates to +-1 through e^{2a} = inf or 0.
 __device__ __forceinline__ float tanh_pp(float a) {
@@ -76,8 +85,8 @@ struct AngLine {
     dtp = p.dt + bh * p.L;
   }
 
-  // the thread's increments tanh(angle) * pi * dt of its steps of the tile at t0,
-  // as inclusive sums in pre and their total in tot (0 past r and past L)
+  // the thread's increments tanh(angle) * dt / 2 (turns) of its steps of the tile at
+  // t0, as inclusive sums in pre and their total in tot (0 past r and past L)
   __device__ __forceinline__ void tile_sums(const AngK& p, long long t0,
                                             float (&pre)[kAngSteps][4],
                                             float (&tot)[4]) const {
@@ -87,9 +96,9 @@ struct AngLine {
     for (int j = 0; j < kAngSteps; ++j) {
       const long long t = t0 + (long long)sl * kAngSteps + j;
       float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-      float pdt = 0.0f;
+      float hdt = 0.0f;
       if (t < p.L && na > 0) {
-        pdt = 3.14159265358979f * dtp[t];
+        hdt = 0.5f * dtp[t];  // pi * dt radians in turns (exact)
         if (p.vec) {
           const float4 v = *reinterpret_cast<const float4*>(angp + t * astride);
           a[0] = v.x; a[1] = v.y; a[2] = v.z; a[3] = v.w;
@@ -99,7 +108,7 @@ struct AngLine {
       }
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        tot[e] += tanh_pp(a[e]) * pdt;  // pairs past r: a = 0, so 0
+        tot[e] += tanh_pp(a[e]) * hdt;  // pairs past r: a = 0, so 0
         pre[j][e] = tot[e];
       }
     }
@@ -122,12 +131,12 @@ __global__ void __launch_bounds__(kAngThreads) m3_angle_totals_kernel(AngK p) {
     float pre[kAngSteps][4], tot[4];
     ln.tile_sums(p, t0, pre, tot);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) acc[e] += tot[e];
+    for (int e = 0; e < 4; ++e) acc[e] = turns_mod1(acc[e] + tot[e]);
   }
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
 #pragma unroll
-    for (int d = kPieces; d < 64; d <<= 1) acc[e] += __shfl_xor(acc[e], d);
+    for (int d = kPieces; d < 64; d <<= 1) acc[e] = turns_mod1(acc[e] + __shfl_xor(acc[e], d));
     if (lane < kPieces) wsum[wave][ln.m][e] = acc[e];
   }
   __syncthreads();
@@ -136,8 +145,8 @@ __global__ void __launch_bounds__(kAngThreads) m3_angle_totals_kernel(AngK p) {
     for (int e = 0; e < 4; ++e) {
       float s = 0.0f;
 #pragma unroll
-      for (int w = 0; w < kAngThreads / 64; ++w) s += wsum[w][tid][e];
-      p.seg_tot[(line * p.segs + seg) * 32 + 4 * tid + e] = s;
+      for (int w = 0; w < kAngThreads / 64; ++w) s = turns_mod1(s + wsum[w][tid][e]);
+      p.seg_tot[(line * p.segs + seg) * 32 + 4 * tid + e] = turns_mod1(s);
     }
   }
 }
@@ -169,7 +178,8 @@ __global__ void __launch_bounds__(kAngThreads) m3_angles_kernel(AngK p) {
   if (ln.na > 0) {
     for (int s = 0; s < seg; ++s) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) carry[e] += p.seg_tot[(line * p.segs + s) * 32 + 4 * ln.m + e];
+      for (int e = 0; e < 4; ++e)
+        carry[e] = turns_mod1(carry[e] + p.seg_tot[(line * p.segs + s) * 32 + 4 * ln.m + e]);
     }
   }
   const long long t_end = (long long)(seg + 1) * p.seg_len;
@@ -202,7 +212,7 @@ __global__ void __launch_bounds__(kAngThreads) m3_angles_kernel(AngK p) {
         all += v;
       }
       base[e] += carry[e] + before;
-      carry[e] += all;
+      carry[e] = turns_mod1(carry[e] + all);
     }
     __syncthreads();  // wsum is rewritten by the next tile
     if (ln.nu == 0) continue;
@@ -213,9 +223,8 @@ __global__ void __launch_bounds__(kAngThreads) m3_angles_kernel(AngK p) {
       float c[4], s[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        // cos/sin of revolutions, theta / 2pi reduced to [-1/2, 1/2]
-        const float rev = (base[e] + pre[j][e]) * 0.15915494309189535f;
-        const float f = rev - __builtin_rintf(rev);
+        // cos/sin of turns reduced to [-1/2, 1/2]
+        const float f = turns_mod1(base[e] + pre[j][e]);
         c[e] = __builtin_amdgcn_cosf(f);
         s[e] = __builtin_amdgcn_sinf(f);
       }

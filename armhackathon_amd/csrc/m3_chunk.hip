@@ -61,13 +61,14 @@ __device__ __forceinline__ f4 mfma(float a, float b, f4 c) {
 // Gate record of one (sequence, chunk) of T = 16/R steps, in floats. The rows of a
 // step share its gates, so M is kept over step pairs, e^{c} and w per step:
 //   M[step_i][step_s] (T x T), e^{c} (T), w (T), e^{c_last}, padding to whole
-//   16-byte pieces; with the angle pre-pass fused, pi * dt of each of the 16 rows.
+//   16-byte pieces; with the angle pre-pass fused, dt / 2 of each of the 16 rows
+//   (the rotation per unit of tanh(angle), pi * dt radians, in turns).
 // Rank 1: 292 floats (1168 bytes), rank 2: 84, rank 4: 28 (112 bytes).
 template <int R> struct Rec {
   static constexpr int T = 16 / R;
   static constexpr int M = 0, Ec = T * T, W = Ec + T, Etot = W + T;
   static constexpr int Floats = (Etot + 1 + 3) & ~3;
-  static constexpr int Pdt = Floats, FloatsAng = Floats + 16;
+  static constexpr int Hdt = Floats, FloatsAng = Floats + 16;
 };
 constexpr int rec_floats(int R, bool ang) {
   return R == 1 ? (ang ? Rec<1>::FloatsAng : Rec<1>::Floats)
@@ -120,12 +121,12 @@ __global__ void __launch_bounds__(256) m3_gates_kernel(M3K p, int reverse) {
   }
   const int step = row / R;
   const long long g = (long long)ch * T + step;
-  float a = 0.0f, gamma = 0.0f, scale = 0.0f, pdt = 0.0f;
+  float a = 0.0f, gamma = 0.0f, scale = 0.0f, hdt = 0.0f;
   if (valid && g < L) {
     const long long base = (long long)seq * L;  // gates are (b, h, l): seq = b*heads + h
     const long long t = reverse ? L - 1 - g : g;
     a = p.adt[base + t];
-    pdt = 3.14159265358979f * p.dt[base + t];
+    hdt = 0.5f * p.dt[base + t];  // pi * dt radians in turns (exact)
     gamma = p.dt[base + t] * sigmoid(p.trap[base + t]);
     scale = gamma;
     if (g + 1 < L) {
@@ -152,7 +153,7 @@ __global__ void __launch_bounds__(256) m3_gates_kernel(M3K p, int reverse) {
   if (!valid) return;
   using RC = Rec<R>;
   float* rec = p.rec + cidx * p.rec_floats;
-  if (p.rec_floats > RC::Floats) rec[RC::Pdt + row] = pdt;  // 0 past the end: theta holds
+  if (p.rec_floats > RC::Floats) rec[RC::Hdt + row] = hdt;  // 0 past the end: theta holds
   if (row % R == 0) {  // the step's first row writes the step's entries
     if constexpr (R == 1) {
       f4* mrow = reinterpret_cast<f4*>(rec + RC::M + row * 16);
@@ -420,26 +421,29 @@ __device__ __forceinline__ float tanh_fast(float a) {
 
 // The angle pre-pass fused (python/arm_scan/mamba3.py:41-89: theta =
 // cumsum_l(tanh(angle) * pi * dt), then cos/sin), for NA rotation pairs of the
-// lane at row li of the chunk: the increments of rows li - R, li - 2R, .. (the
-// earlier steps, same rank) are summed by a DPP row scan, the chunk's start
-// angle `carry` is added, and the carry moves to the angle at the chunk's last
-// step. cos/sin by the hardware functions of revolutions after reducing theta/2pi
-// to [-1/2, 1/2]. All 64 lanes take part (the row scan and the carry's shuffle).
+// lane at row li of the chunk, in turns (theta / 2pi): hdt = dt / 2 is pi * dt
+// radians in turns. The increments of rows li - R, li - 2R, .. (the earlier
+// steps, same rank) are summed by a DPP row scan and added to the chunk's start
+// angle `carry`; the sum is reduced to [-1/2, 1/2] turns, where cos/sin by the
+// hardware functions of turns are exact to a few ulp, and the reduced angle at
+// the chunk's last step carries on. The carry never grows: every add rounds at
+// ulp(1/2) (3e-8 turns), where a running theta in radians rounds at ulp(theta)
+// (1.5e-5 rad near 225 rad, the end of a sequence of one-signed angles at L 4096).
+// All 64 lanes take part (the row scan and the carry's shuffle).
 template <int R, int NA>
-__device__ __forceinline__ void fused_angles(const float (&a)[NA], float pdt, int li,
+__device__ __forceinline__ void fused_angles(const float (&a)[NA], float hdt, int li,
                                              int lane, float (&carry)[NA], float (&cs)[NA],
                                              float (&sn)[NA]) {
 #pragma unroll
   for (int e = 0; e < NA; ++e) {
-    float t = tanh_fast(a[e]) * pdt;
+    float t = tanh_fast(a[e]) * hdt;
     if (R <= 1) t += dpp<kRowShr1, 0xF>(0.0f, t);
     if (R <= 2) t += dpp<kRowShr2, 0xF>(0.0f, t);
     if (R <= 4) t += dpp<kRowShr4, 0xF>(0.0f, t);
     t += dpp<kRowShr8, 0xF>(0.0f, t);
-    const float theta = carry[e] + t;
-    carry[e] = __shfl(theta, (lane & ~15) | (16 - R + li % R));
-    const float x = theta * 0.15915494309189535f;  // revolutions
+    const float x = carry[e] + t;  // turns
     const float f = x - __builtin_rintf(x);
+    carry[e] = __shfl(f, (lane & ~15) | (16 - R + li % R));
     cs[e] = __builtin_amdgcn_cosf(f);
     sn[e] = __builtin_amdgcn_sinf(f);
   }
@@ -771,7 +775,7 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 4)) m3_chunk_kernel(M3K p) {
 #pragma unroll
         for (int j = 0; j < NC; ++j)
           a[j] = have ? sg[off_ang + (u4 * T + step_i) * 4 + (li % R) * NC + j] : 0.0f;
-        fused_angles<R, NC>(a, sg[off_rec + Rec<R>::Pdt + li], li, lane, carry_m, c, sv);
+        fused_angles<R, NC>(a, sg[off_rec + Rec<R>::Hdt + li], li, lane, carry_m, c, sv);
         const int src = lane - li % R;  // the step's first lane
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -783,7 +787,7 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 4)) m3_chunk_kernel(M3K p) {
         const f2 a2 = have ? ld2(sg + off_ang + (u4 * T + li) * 4 + 2 * (lj & 1)) : f2{0, 0};
         a[0] = a2[0];
         a[1] = a2[1];
-        fused_angles<R, 2>(a, sg[off_rec + Rec<R>::Pdt + li], li, lane, carry, c, sv);
+        fused_angles<R, 2>(a, sg[off_rec + Rec<R>::Hdt + li], li, lane, carry, c, sv);
         cs = f4{c[0], c[1], 0.0f, 0.0f};
         sn = f4{sv[0], sv[1], 0.0f, 0.0f};
       }

@@ -59,6 +59,10 @@ struct M1JobSpec {
   float *out, *last;
   int rev;
 };
+// Steps per chunk of the tiled Mamba-1 kernel (16 lanes of 16 steps a row), and the
+// row blocks (16 rows each) at which a launch stops cutting rows into segments.
+constexpr long long kM1ChunkSteps = 256;
+constexpr long long kM1WholeRowBlocks = 512;
 bool m1_jobs_supported(const M1Problem& p);
 hipError_t m1_scan_jobs(const M1Problem& p, const M1JobSpec* spec, int n, hipStream_t st);
 // Batched (planes, H, W) -> (planes, W, H) transposes of up to 8 tensors.

@@ -329,8 +329,8 @@ def _(u, delta, a, b, c, d_skip, z, delta_bias, delta_softplus):
 def selective_scan_bidirectional(u, delta, A, B, C, D=None, z=None,
                                  delta_bias=None, delta_softplus=False):
     """Forward and reverse scans of the same inputs in one call
-    (python/arm_scan/op.py:138-160) -> (out_fwd, out_bwd). exp(delta*A) is
-    evaluated once and shared by both directions."""
+    (python/arm_scan/op.py:138-160) -> (out_fwd, out_bwd), through
+    arm_scan_selective_scan_bidirectional_f32 (its routes: include/arm_scan_hip.h)."""
     batch, dim, length = u.shape
     state = A.shape[1]
     B = _bc4(B, batch, state, length)

@@ -72,7 +72,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--workload", choices=("m1", "m1_b1", "m1_seam", "m3_siso", "m3_mimo",
-                                           "ss2d",
+                                           "ss2d", "m1_longctx", "m1_bidir_few",
                                            "m3_siso_angles", "m3_mimo_angles",
                                            "m3_noncausal", "m3_block"),
                     default="m1",
@@ -147,6 +147,18 @@ def config_inputs(name, dev):
             x = workloads.m1_op(batch=1, dim=1536, length=2048, state=16, seed=100 + sd)
             sets.append({k: torch.from_numpy(v).to(dev) for k, v in x.items() if v is not None})
         return sets, workloads.m1_bytes(1, 1536, 2048, 16, z=True, D=True, last_state=True)
+    if name == "m1_longctx":
+        # the reference's long-context shape (bench/bench_longctx.py:30-33): 768 rows,
+        # the few-rows plan cuts each into 16 segments; one set is 1.2 GB of inputs
+        x = workloads.m1_layer(batch=1, dim=768, length=131072, state=16, seed=9)
+        return ({k: torch.from_numpy(v).to(dev) for k, v in x.items()},
+                workloads.m1_bytes(1, 768, 131072, 16, z=True, D=True, bias=True,
+                                   last_state=True))
+    if name == "ss2d":
+        # two sets (236 MB each) alternate: one alone would fit in the 256 MB MALL
+        xs = [workloads.ss2d(seed=sd) for sd in (5, 6)]
+        nbytes = workloads.ss2d_bytes(xs[0], merge="sum")
+        return [{k: torch.from_numpy(v).to(dev) for k, v in x.items()} for x in xs], nbytes
     if name == "m1_seam":
         t = scan_inputs(0, dev)
         b, d, L, n = SHAPE["batch"], SHAPE["dim"], SHAPE["length"], SHAPE["state"]
@@ -208,7 +220,10 @@ CONFIG_NAMES = {
                     "other): forward traversal, then the backward one accumulated without "
                     "the same-step term",
     "m3_mimo": "config 4: Mamba-3 MIMO rank 4, B4 L4096 24 heads x 64, dqk 128 (final state)",
-    "ss2d": "config 5: SS2D 4 directions, B16 D192 64x64 N16, D, z, merge sum (final states)",
+    "ss2d": "config 5: SS2D 4 directions, B16 D192 64x64 N16, D, z, merge sum (final states; "
+            "2 input sets rotated: one set fits in the 256 MB MALL)",
+    "m1_longctx": "long context: Mamba-1 selective_scan B1 D768 L131072 N16, bias+softplus, "
+                  "D, z, final state (the reference's bench_longctx shape)",
 }
 
 
@@ -236,6 +251,11 @@ def bench_config(name, dev, steps, warmup):
                           x["z"].data_ptr(), 0, False, "auto", "auto", outs[i].data_ptr(),
                           lasts[i].data_ptr(), 0, reverse=False,
                           stream=torch.cuda.current_stream(dev).cuda_stream)
+    elif name == "m1_longctx":
+        def call():
+            return arm_scan.selective_scan(t["u"], t["delta"], t["A"], t["B"], t["C"], D=t["D"],
+                                           z=t["z"], delta_bias=t["delta_bias"],
+                                           delta_softplus=True, return_last_state=True)
     elif name == "m1_seam":
         def call():
             return arm_scan.selective_scan_time_major(
@@ -268,9 +288,13 @@ def bench_config(name, dev, steps, warmup):
             return arm_scan.mamba3_mimo_scan(*[t[k] for k in K], t["psi"], t["zeta"], t["phi"],
                                              cos=t["cos"], sin=t["sin"], return_last_state=True)
     else:
+        it = {"i": 0}
+
         def call():
-            return arm_scan.ss2d_scan(t["u"], t["delta"], t["A"], t["B4"], t["C4"], D=t["D"],
-                                      z=t["z"], delta_softplus=False, merge="sum",
+            x = t[it["i"] & 1]
+            it["i"] += 1
+            return arm_scan.ss2d_scan(x["u"], x["delta"], x["A"], x["B4"], x["C4"], D=x["D"],
+                                      z=x["z"], delta_softplus=False, merge="sum",
                                       per_direction=True, return_last_state=True)
     warm_up(lambda i: call(), warmup)
     stream = torch.cuda.current_stream(dev)
@@ -373,6 +397,46 @@ def bench_config(name, dev, steps, warmup):
                 **extra)
 
 
+def bench_bidir_few(dev, steps):
+    """Bidirectional Mamba-1 on few rows: the entry point's route (the exp-sharing
+    kernel where a row fits it, else two launches that cut rows into segments) against
+    two single-direction calls and, for reference, the two-job whole-row launch that
+    wide shapes take. ms per call, HIP events, after the warm-up."""
+    import torch
+
+    import armhackathon_amd as arm_scan
+    from armhackathon_amd import workloads
+
+    out = {}
+    for (b, d, L) in ((1, 16, 65536), (1, 768, 32768), (1, 1536, 2048), (16, 192, 4096)):
+        x = workloads.m1_op(batch=b, dim=d, length=L, state=16, seed=11)
+        t = {k: torch.from_numpy(v).to(dev) for k, v in x.items() if v is not None}
+        a = (t["u"], t["delta"], t["A"], t["B"], t["C"])
+        kw = dict(D=t["D"], z=t["z"])
+
+        def pair():
+            return arm_scan.selective_scan_bidirectional(*a, **kw)
+
+        def singles():
+            return (arm_scan.selective_scan(*a, **kw),
+                    arm_scan.selective_scan(*a, reverse=True, **kw))
+        r = {}
+        stream = torch.cuda.current_stream(dev)
+        for key, fn in (("bidirectional_ms", pair), ("two_calls_ms", singles)):
+            warm_up(lambda i: fn(), 5)
+            st, sp = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            st.record(stream)
+            for _ in range(steps):
+                fn()
+            sp.record(stream)
+            torch.cuda.synchronize()
+            r[key] = round(st.elapsed_time(sp) / steps, 4)
+        out[f"B{b} D{d} L{L}"] = r
+        del t, a, kw
+        torch.cuda.empty_cache()
+    return out
+
+
 def bench_config_cpu(name, seconds):
     """The C++ restatement of the reference's x86 path on host cores for one of
     configs 1 and 3-5, over a bounded sample of the config (config 1 whole, batch 1 of
@@ -409,6 +473,14 @@ def bench_config_cpu(name, seconds):
             bwd = oracle.mamba3_scan(*args, reverse=True)
             return fwd + bwd - naive.m3_same_step(x["q"], x["k"], x["v"], x["dt"], x["trap"],
                                                   x["q_bias"], x["k_bias"]).transpose(0, 2, 1, 3)
+    elif name == "m1_longctx":
+        x = workloads.m1_layer(batch=1, dim=48, length=131072, state=16, seed=9)
+        nbytes = workloads.m1_bytes(1, 48, 131072, 16, z=True, D=True, bias=True)
+        sample = "48 of the 768 channels of the long-context shape"
+
+        def call():
+            oracle.selective_scan(x["u"], x["delta"], x["A"], x["B"], x["C"], D=x["D"],
+                                  z=x["z"], delta_bias=x["delta_bias"], delta_softplus=True)
     elif name == "m3_mimo":
         x = workloads.m3_mimo(batch=1, seed=4)
         nbytes, sample = workloads.m3_bytes(x), "batch 1 of config 4"
@@ -675,6 +747,11 @@ def main():
         print(json.dumps({"copy_calibration_bytes": src.numel() * 4}), flush=True)
         return
     _ffi.load()
+    if args.workload == "m1_bidir_few":
+        print(json.dumps({"metric": "ms per call", "unit": "ms", "n_gpus": 1, "dtype": "f32",
+                          "data": "synthetic", "detail": bench_bidir_few(dev, args.steps)}),
+              flush=True)
+        return
     if args.workload != "m1":
         r = bench_config(args.workload, dev, args.steps, args.warmup)
         print(json.dumps({"metric": "algorithmic GB/s of one call", "value": r["gbs"],
@@ -687,7 +764,7 @@ def main():
     configs = None if args.no_configs else {
         name: bench_config(name, dev, steps, 10)
         for name, steps in (("m1_b1", 400), ("m3_siso", 100), ("m3_mimo", 40), ("ss2d", 100),
-                            ("m3_noncausal", 50))}
+                            ("m3_noncausal", 50), ("m1_longctx", 40))}
     cpu = None if args.no_cpu else bench_cpu(args.cpu_seconds)
     if configs is not None and not args.no_cpu:
         for name in configs:

@@ -151,7 +151,10 @@ int arm_scan_selective_state_update_f32(
     int dt_softplus, float* out, void* stream);
 
 /* Replaces arm_scan_selective_scan_bidirectional_f32 (arm-scan-ffi/src/lib.rs:235-354):
- * the forward and the reverse scan of the same inputs in one pass sharing exp(delta*A).
+ * the forward and the reverse scan of the same inputs, both seeded from zero. Where its
+ * 16-row blocks fill the chip the two directions are two traversals of one launch (each
+ * evaluating exp(delta*A)); fewer rows that fit one on-chip pass share exp(delta*A) in
+ * one kernel; other shapes run two launches.
  * last_fwd / last_bwd: both or neither (else ARM_SCAN_ERR_INVALID_DIMS). */
 int arm_scan_selective_scan_bidirectional_f32(
     const ArmScanDims* dims, const float* u, const float* delta, const float* a,

@@ -168,3 +168,22 @@ def test_last_error_is_per_thread():
     assert seen["zero"][0] == 2 and seen["groups"][0] == 2
     assert seen["zero"][1] != seen["groups"][1]
     assert "zero" in seen["zero"][1] and "groups" in seen["groups"][1]
+
+
+def test_m1_strided_out_overlap_rejected():
+    """A strided out whose (batch, dim, step) elements would share addresses is rejected
+    before any launch (blocks writing one element would race): a zero stride on any
+    dimension of more than one element, or a batch stride inside one batch's extent."""
+    L = _ffi.load()
+    b, d, n_len = 2, 16, 8
+
+    def call(os):
+        arr = (ctypes.c_longlong * 3)(*os)
+        return L.arm_scan_selective_scan_strided_f32(
+            ctypes.byref(_ffi.ArmScanDims(b, d, n_len, 4, 1)), FAKE, None, FAKE, FAKE, FAKE,
+            FAKE, None, None, None, None, 0, 0, FAKE, arr, None, None, None)
+
+    for os in ((0, n_len, 1), (d * n_len, 0, 1), (d * n_len, n_len, 0), (64, n_len, 1),
+               (d * n_len, 4, 1), (d, 1, 8)):
+        assert call(os) == 2, os
+        assert "overlap" in L.arm_scan_last_error().decode()

@@ -11,9 +11,11 @@
 
 Gate: tensor-scale relative error <= 1e-4 (fp32 against float64; the in/out
 projections are fp32 GEMMs). The reference's block-level goldens (block_io_00/01 in
-its tests/golden/mamba3/manifest.json) are not in its tree, so the split order and the
-Q <- C / K <- B mapping are pinned by the transcription of block.py:146-199 in the
-oracle, not by a capture.
+its tests/golden/mamba3/manifest.json) are not in its tree; the split order and the
+Q <- C / K <- B mapping are pinned by fixtures written from the reference's own
+Mamba3Mixer.forward (tests/golden/mamba3_block/, checked against the oracle's mixer in
+tests/test_block.py with the B/C and x/z swaps planted and failing), which the mixer
+here is also run against.
 """
 
 import numpy as np

@@ -11,7 +11,13 @@ libarm_scan_hip.so, so the document cannot drift from the library:
 * the struct mirrors have the header's fields, in order;
 * host-rejected calls through scan_raw, scan_bidir_raw and mamba3_raw come back as
   the reference's codes (arm-scan-ffi/src/lib.rs:53-58). They are rejected before any
-  launch, so the fake pointers they carry are never dereferenced.
+  launch. Where a GPU is present their pointers are real (small) device buffers, so a
+  loosened check shows as a failed assertion, not as a kernel reading an unmapped
+  address; without a GPU nothing can launch and a placeholder address stands in;
+* on the GPU, successful calls through the same three functions on device tensors,
+  against the float64 oracle, and the reference's 1d goldens replayed through
+  scan_raw under its own gates, as the reference replays them through its ABI
+  (tests/check_ffi.py:157-233).
 """
 
 import ctypes
@@ -19,12 +25,37 @@ import re
 import types
 from pathlib import Path
 
+import numpy as np
 import pytest
 
-from armhackathon_amd import _ffi
+import oracle
+from armhackathon_amd import _ffi, workloads
+from util import case, dev, host, rel_err
 
 ROOT = Path(__file__).resolve().parents[1]
-FAKE = 0x1000
+
+
+def _gpu():
+    try:
+        import torch
+        return torch.cuda.is_available()
+    except Exception:
+        return False
+
+
+_bufs = []
+
+
+def _buf():
+    """A pointer for a call the host must reject: a real 4 KiB device buffer when a GPU
+    is present (nothing out of bounds happens even if a check were loosened), else a
+    placeholder address (no GPU: nothing can launch)."""
+    if not _gpu():
+        return 0x1000
+    import torch
+    t = torch.zeros(1024, device="cuda")
+    _bufs.append(t)
+    return t.data_ptr()
 
 
 def _stub_source():
@@ -96,6 +127,7 @@ def _codes(fn):
 
 
 def test_stub_scan_raw_rejections(stub):
+    FAKE = _buf()
     zero = stub.ArmScanDims(0, 16, 8, 4, 1)
     ok = stub.ArmScanDims(1, 16, 8, 4, 1)
     call = lambda dims, backend="auto": stub.scan_raw(
@@ -107,6 +139,7 @@ def test_stub_scan_raw_rejections(stub):
 
 
 def test_stub_bidir_raw_rejections(stub):
+    FAKE = _buf()
     ok = stub.ArmScanDims(1, 16, 8, 4, 1)
     code, msg = _codes(lambda: stub.scan_bidir_raw(
         ok, FAKE, FAKE, FAKE, FAKE, FAKE, 0, 0, 0, False, "auto", "auto", FAKE, FAKE,
@@ -117,6 +150,7 @@ def test_stub_bidir_raw_rejections(stub):
 
 
 def test_stub_mamba3_raw_rejections(stub):
+    FAKE = _buf()
     odd = stub.ArmMamba3Dims(1, 2, 16, 15, 8, 1, 1)
     ptrs = [FAKE] * 10 + [None] * 5
     assert _codes(lambda: stub.mamba3_raw(odd, ptrs, 0, 0, 0, FAKE, None, None))[0] == 2
@@ -126,3 +160,116 @@ def test_stub_mamba3_raw_rejections(stub):
     assert _codes(lambda: stub.mamba3_raw(ok, ptrs, 0, 0, 5, FAKE, None, None))[0] == 4
     with pytest.raises(ValueError):
         stub.mamba3_raw(ok, ptrs[:14], 0, 0, 0, FAKE, None, None)
+
+
+# ---- successful calls on device tensors (GPU) ------------------------------------
+
+def _p(t, k):
+    return 0 if t.get(k) is None else t[k].data_ptr()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("reverse", [False, True])
+def test_stub_scan_raw_on_device(stub, reverse):
+    """scan_raw as the reference's op.py calls it (device pointers in place of host
+    ones), with D, z, delta_bias, softplus and h0, against the float64 oracle."""
+    import torch
+
+    case(f"stub scan_raw 2x48x777 reverse={reverse}")
+    x = workloads.m1_layer(batch=2, dim=48, length=777, state=16, seed=70)
+    x["h0"] = np.random.default_rng(71).standard_normal((2, 48, 16)).astype(np.float32)
+    t = dev(x)
+    out = torch.full((2, 48, 777), float("nan"), device="cuda")
+    last = torch.full((2, 48, 16), float("nan"), device="cuda")
+    stub.scan_raw(stub.ArmScanDims(2, 48, 777, 16, 1), _p(t, "u"), _p(t, "delta"),
+                  _p(t, "A"), _p(t, "B"), _p(t, "C"), _p(t, "D"), _p(t, "z"),
+                  _p(t, "delta_bias"), True, "auto", "auto", out.data_ptr(),
+                  last.data_ptr(), _p(t, "h0"), reverse=reverse)
+    torch.cuda.synchronize()
+    ref, ref_last = oracle.selective_scan(
+        x["u"], x["delta"], x["A"], x["B"], x["C"], D=x["D"], z=x["z"],
+        delta_bias=x["delta_bias"], delta_softplus=True, reverse=reverse, h0=x["h0"],
+        dtype=np.float64)
+    assert rel_err(host(out), ref) < 1e-4
+    assert rel_err(host(last), ref_last) < 1e-4
+
+
+@pytest.mark.gpu
+def test_stub_scan_bidir_raw_on_device(stub):
+    import torch
+
+    case("stub scan_bidir_raw 1x32x1000")
+    x = workloads.m1_op(batch=1, dim=32, length=1000, state=16, seed=72)
+    t = dev(x)
+    o = [torch.full((1, 32, 1000), float("nan"), device="cuda") for _ in range(2)]
+    la = [torch.full((1, 32, 16), float("nan"), device="cuda") for _ in range(2)]
+    stub.scan_bidir_raw(stub.ArmScanDims(1, 32, 1000, 16, 1), _p(t, "u"), _p(t, "delta"),
+                        _p(t, "A"), _p(t, "B"), _p(t, "C"), _p(t, "D"), _p(t, "z"), 0,
+                        False, "auto", "auto", o[0].data_ptr(), o[1].data_ptr(),
+                        la[0].data_ptr(), la[1].data_ptr())
+    torch.cuda.synchronize()
+    ref = oracle.selective_scan_bidirectional(x["u"], x["delta"], x["A"], x["B"], x["C"],
+                                              D=x["D"], z=x["z"], dtype=np.float64)
+    for got, want in zip((*o, *la), ref):
+        assert rel_err(host(got), want) < 1e-4
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("reverse", [False, True])
+def test_stub_mamba3_raw_on_device(stub, reverse):
+    """mamba3_raw with the fifteen input pointers of the reference's order (q k v adt dt
+    trap q_bias k_bias cos sin D z psi zeta phi), out head-major, last_state and
+    last_bx, against the float64 oracle."""
+    import torch
+
+    case(f"stub mamba3_raw 2x100x3 dv16 dqk32 reverse={reverse}")
+    x = workloads.m3_siso(batch=2, length=100, heads=3, dv=16, dqk=32, seed=73)
+    rng = np.random.default_rng(74)
+    x["D"] = rng.standard_normal(3).astype(np.float32)
+    x["z"] = rng.standard_normal(x["v"].shape).astype(np.float32)
+    t = dev(x)
+    keys = ("q", "k", "v", "adt", "dt", "trap", "q_bias", "k_bias", "cos", "sin", "D", "z")
+    ptrs = [_p(t, k) for k in keys] + [None, None, None]
+    out = torch.full((2, 3, 100, 16), float("nan"), device="cuda")
+    ls = torch.full((2, 3, 16, 32), float("nan"), device="cuda")
+    lbx = torch.full((2, 3, 32), float("nan"), device="cuda")
+    stub.mamba3_raw(stub.ArmMamba3Dims(2, 3, 16, 32, 100, 1, 3), ptrs, int(reverse), 0, 0,
+                    out.data_ptr(), ls.data_ptr(), lbx.data_ptr())
+    torch.cuda.synchronize()
+    ref, rls, rlbx = oracle.mamba3_scan(*[x[k] for k in keys[:10]], D=x["D"], z=x["z"],
+                                        reverse=reverse, dtype=np.float64, want_state=True)
+    assert rel_err(host(out), ref) < 1e-4
+    assert rel_err(host(ls), rls) < 1e-4
+    assert rel_err(host(lbx), rlbx) < 1e-4
+
+
+@pytest.mark.gpu
+def test_stub_replays_reference_goldens(stub, golden_dir):
+    """Every 1d golden through scan_raw under the reference's gates (check_ffi.py:
+    153-154, 205-206): max |out - out_f64| < 1e-4, last_state relative < 1e-4."""
+    import json
+
+    import torch
+
+    man = json.loads((golden_dir / "1d" / "manifest.json").read_text())
+    for m in man:
+        case(f"stub golden {m['name']}")
+        z = np.load(golden_dir / "1d" / f"{m['name']}.npz")
+        meta = json.loads(bytes(z["meta_json"]).decode())
+        x = {k: z[k].astype(np.float32) for k in ("u", "delta", "A", "B", "C")}
+        for k, name in (("D", "D_skip"), ("z", "z"), ("delta_bias", "delta_bias")):
+            if name in z.files:
+                x[k] = z[name].astype(np.float32)
+        b, d, L = x["u"].shape
+        n = x["A"].shape[1]
+        g = x["B"].shape[1] if x["B"].ndim == 4 else 1
+        t = dev(x)
+        out = torch.full((b, d, L), float("nan"), device="cuda")
+        last = torch.full((b, d, n), float("nan"), device="cuda")
+        stub.scan_raw(stub.ArmScanDims(b, d, L, n, g), _p(t, "u"), _p(t, "delta"),
+                      _p(t, "A"), _p(t, "B"), _p(t, "C"), _p(t, "D"), _p(t, "z"),
+                      _p(t, "delta_bias"), meta["delta_softplus"], "auto", "auto",
+                      out.data_ptr(), last.data_ptr())
+        torch.cuda.synchronize()
+        assert np.abs(host(out) - z["out_f64"]).max() < 1e-4, m["name"]
+        assert rel_err(host(last), z["last_state_f64"]) < 1e-4, m["name"]

@@ -169,32 +169,37 @@ def test_m3_pair_and_reverse_is_flip():
     assert rel_err(host(fwd), _siso_ref(x).transpose(0, 2, 1, 3)) < TOL
 
 
-def test_m3_siso_benchmark_shape():
+@pytest.mark.parametrize("reverse", [False, True])
+def test_m3_siso_benchmark_shape(reverse):
     """BASELINE config 3 at its full size (B4 L4096, per-head q/k, 24 heads x 64,
-    dqk 128); outputs, final states, last_bx."""
-    case("siso config 3 (full B4 L4096)")
+    dqk 128), both traversals against the float64 oracle: outputs, final states and
+    last_bx. Reverse pins the trapezoid's neighbour on a backward walk (step t-1,
+    mamba3/scalar.rs:95-115) at the length where a wrong neighbour or a missing
+    last-step term would have 4096 steps to accumulate."""
+    case(f"siso config 3 (full B4 L4096) reverse={reverse}")
     x = workloads.m3_siso(batch=4, seed=3)
-    out, ls, lbx = _siso_gpu(x, return_last_state=True)
-    ref, rls, rlbx = _siso_ref(x, want_state=True)
+    out, ls, lbx = _siso_gpu(x, return_last_state=True, reverse=reverse)
+    ref, rls, rlbx = _siso_ref(x, want_state=True, reverse=reverse)
     assert rel_err(host(out), ref.transpose(0, 2, 1, 3)) < TOL
     assert rel_err(host(ls), rls) < TOL
     assert rel_err(host(lbx), rlbx) < TOL
 
 
-def test_m3_mimo_benchmark_shape():
-    """BASELINE config 4 at its full size (rank 4, per-head q/k, B4 L4096); output and
-    final state."""
+@pytest.mark.parametrize("reverse", [False, True])
+def test_m3_mimo_benchmark_shape(reverse):
+    """BASELINE config 4 at its full size (rank 4, per-head q/k, B4 L4096), both
+    traversals against the float64 oracle: output and final state."""
     import armhackathon_amd as arm_scan
 
-    case("mimo config 4 (full B4 L4096)")
+    case(f"mimo config 4 (full B4 L4096) reverse={reverse}")
     x = workloads.m3_mimo(batch=4, length=4096, seed=4)
     t = dev(x)
     out, ls = arm_scan.mamba3_mimo_scan(
         *[t[k] for k in SISO_KEYS], t["psi"], t["zeta"], t["phi"], cos=t["cos"], sin=t["sin"],
-        return_last_state=True)
+        return_last_state=True, reverse=reverse)
     ref, rls, _ = oracle.mamba3_scan(*[x[k] for k in SISO_KEYS], x["cos"], x["sin"],
                                      psi=x["psi"], zeta=x["zeta"], phi=x["phi"],
-                                     dtype=np.float64, want_state=True)
+                                     reverse=reverse, dtype=np.float64, want_state=True)
     assert rel_err(host(out), ref.transpose(0, 2, 1, 3)) < TOL
     assert rel_err(host(ls), rls) < TOL
 
@@ -385,6 +390,62 @@ def test_m3_angle_prepass(shape):
     assert np.abs(host(cos) - rc).max() < 2e-5
     assert np.abs(host(sin) - rs).max() < 2e-5
     assert np.all(host(cos)[..., r:] == 1.0) and np.all(host(sin)[..., r:] == 0.0)
+
+
+@pytest.mark.parametrize("mimo", [False, True], ids=["siso", "mimo"])
+def test_m3_one_signed_angles_long(mimo):
+    """Config 3 / 4 shapes (batch 1, L 4096) with one-signed angles N(2, 1): tanh(angle)
+    stays near 1, so theta climbs steadily to a few hundred radians by the last step,
+    where a running float32 theta would round at ulp(theta) ~ 1.5e-5 rad per add.
+    Three routes against the float64 pre-pass and the oracle (1e-4): the pre-pass fused
+    into the scan, the pre-pass kernels then the scan on their cos/sin (forward, and
+    reverse, which always takes the pre-pass), and the pre-pass kernels alone, within
+    2e-5 of the float64 cos/sin. r = dqk/4 (the published rotation fraction) and r =
+    dqk/2 (every pair rotates)."""
+    import armhackathon_amd as arm_scan
+    from armhackathon_amd.mamba3 import _run_angles, angles_to_cos_sin
+
+    for r in (32, 64):
+        x = (workloads.m3_mimo if mimo else workloads.m3_siso)(batch=1, length=4096, seed=60)
+        rng = np.random.default_rng(61 + r)
+        b, L, h = x["v"].shape[:3]
+        angles = (rng.standard_normal((b, L, h, r)) + 2.0).astype(np.float32)
+        x["cos"], x["sin"] = oracle.angles_to_cos_sin(angles, x["dt"], x["q"].shape[-1] // 2)
+        theta_end = np.pi * (np.tanh(angles.astype(np.float64)) *
+                             x["dt"].transpose(0, 2, 1)[..., None]).sum(axis=1)
+        assert theta_end.min() > 100.0, theta_end.min()
+        t = dev(x)
+        ta = dev(angles)
+        mk = (t["psi"], t["zeta"], t["phi"]) if mimo else (None, None, None)
+        kw = dict(psi=x["psi"], zeta=x["zeta"], phi=x["phi"]) if mimo else {}
+
+        case(f"one-signed angles {'mimo' if mimo else 'siso'} r={r}: pre-pass kernels")
+        cos, sin = angles_to_cos_sin(ta, t["dt"], x["q"].shape[-1] // 2)
+        assert np.abs(host(cos) - x["cos"]).max() < 2e-5
+        assert np.abs(host(sin) - x["sin"]).max() < 2e-5
+        for reverse in (False, True):
+            case(f"one-signed angles {'mimo' if mimo else 'siso'} r={r} reverse={reverse}")
+            ref, rls, _ = oracle.mamba3_scan(*[x[k] for k in SISO_KEYS], x["cos"], x["sin"],
+                                             reverse=reverse, dtype=np.float64,
+                                             want_state=True, **kw)
+            ref = ref.transpose(0, 2, 1, 3)
+            if not reverse:
+                out, ls, _ = _run_angles(*[t[k] for k in SISO_KEYS], ta, None, None, *mk,
+                                         True)
+                assert rel_err(host(out), ref) < TOL
+                assert rel_err(host(ls), rls) < TOL
+            if mimo:
+                out2 = arm_scan.mamba3_mimo_scan(*[t[k] for k in SISO_KEYS], *mk, cos=cos,
+                                                 sin=sin, reverse=reverse)
+                out3 = arm_scan.mamba3_mimo_scan(*[t[k] for k in SISO_KEYS], *mk,
+                                                 angles=ta, reverse=reverse)
+            else:
+                out2 = arm_scan.mamba3_scan(*[t[k] for k in SISO_KEYS], cos=cos, sin=sin,
+                                            reverse=reverse)
+                out3 = arm_scan.mamba3_scan(*[t[k] for k in SISO_KEYS], angles=ta,
+                                            reverse=reverse)
+            assert rel_err(host(out2), ref) < TOL
+            assert rel_err(host(out3), ref) < TOL
 
 
 def test_m3_broadcast_views():

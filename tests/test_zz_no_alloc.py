@@ -72,3 +72,80 @@ def test_noalloc_unaligned_rows(reverse):
         got, got_last = _call("arm_scan_selective_scan_noalloc_f32", x, True, reverse)
         ref, ref_last = _call("arm_scan_selective_scan_f32", x, True, reverse)
         assert np.array_equal(got, ref) and np.array_equal(got_last, ref_last)
+
+
+def _hip():
+    """The HIP runtime already in the process (torch's and the library's, one soname)."""
+    import torch  # noqa: F401  (loads the runtime)
+
+    hip = ctypes.CDLL("libamdhip64.so.7")
+    vp = ctypes.c_void_p
+    hip.hipStreamBeginCapture.argtypes = [vp, ctypes.c_int]
+    hip.hipStreamEndCapture.argtypes = [vp, ctypes.POINTER(vp)]
+    hip.hipGraphGetNodes.argtypes = [vp, ctypes.POINTER(vp), ctypes.POINTER(ctypes.c_size_t)]
+    hip.hipGraphNodeGetType.argtypes = [vp, ctypes.POINTER(ctypes.c_int)]
+    hip.hipGraphDestroy.argtypes = [vp]
+    return hip
+
+
+KERNEL, MEMSET, MEM_ALLOC, MEM_FREE = 0, 2, 10, 11  # hipGraphNodeType
+
+
+def _captured_node_types(fn_name, x, reverse):
+    """Record one call into a HIP graph on a capturing stream (nothing runs: the graph is
+    inspected and destroyed, never launched) and return the types of its nodes."""
+    import torch
+
+    hip = _hip()
+    b, d, L = x["u"].shape
+    n = x["A"].shape[1]
+    t = dev(x)
+    out = torch.empty((b, d, L), device="cuda")
+    last = torch.empty((b, d, n), device="cuda")
+    p = lambda k: None if t.get(k) is None else t[k].data_ptr()  # noqa: E731
+    s = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    graph = ctypes.c_void_p()
+    assert hip.hipStreamBeginCapture(s.cuda_stream, 2) == 0  # hipStreamCaptureModeRelaxed
+    rc = getattr(_ffi.load(), fn_name)(
+        ctypes.byref(_ffi.ArmScanDims(b, d, L, n, 1)), p("u"), p("delta"), p("A"), p("B"),
+        p("C"), p("D"), p("z"), p("delta_bias"), 1, int(reverse), 0, 0, out.data_ptr(),
+        last.data_ptr(), None, s.cuda_stream)
+    end = hip.hipStreamEndCapture(s.cuda_stream, ctypes.byref(graph))
+    if rc != 0 or end != 0:
+        return None  # the capture refused a call (the control below allows that)
+    count = ctypes.c_size_t(0)
+    assert hip.hipGraphGetNodes(graph, None, ctypes.byref(count)) == 0
+    nodes = (ctypes.c_void_p * max(count.value, 1))()
+    assert hip.hipGraphGetNodes(graph, nodes, ctypes.byref(count)) == 0
+    types = []
+    for i in range(count.value):
+        ty = ctypes.c_int(-1)
+        assert hip.hipGraphNodeGetType(nodes[i], ctypes.byref(ty)) == 0
+        types.append(ty.value)
+    assert hip.hipGraphDestroy(graph) == 0
+    return types
+
+
+@pytest.mark.parametrize("shape", [(1, 1536, 2048, 16), (1, 1536, 2050, 16), (8, 64, 300, 16)],
+                         ids=["segmented", "unaligned", "whole_rows"])
+def test_noalloc_records_no_allocation(shape):
+    """The defining property: a call of the allocation-free entry, recorded into a HIP
+    graph by stream capture, holds kernel nodes only (no allocation, free or memset
+    node), on the few-rows plan (segment maps in the static scratch), on rows that are
+    not 16-byte multiples (B/C read in place, where the allocating entry makes a padded
+    copy) and on whole rows. The allocating entry on the segmented shape records an
+    allocation and a free (or the capture refuses it), so the check tells them apart."""
+    b, d, L, n = shape
+    x = workloads.m1_layer(batch=b, dim=d, length=L, state=n, seed=45)
+    _call("arm_scan_selective_scan_noalloc_f32", x, True)  # set-up (scratch lookup) first
+    for reverse in (False, True):
+        case(f"noalloc capture {shape} reverse={reverse}")
+        types = _captured_node_types("arm_scan_selective_scan_noalloc_f32", x, reverse)
+        assert types and all(t == KERNEL for t in types), types
+    if shape[2] == 2048 and shape[0] == 1:
+        # the allocating entry either records its stream-ordered allocation and free, or
+        # the capture refuses the pool allocation: either way it is not allocation-free
+        case("allocating entry capture (control)")
+        types = _captured_node_types("arm_scan_selective_scan_f32", x, False)
+        assert types is None or (MEM_ALLOC in types and MEM_FREE in types), types
