@@ -256,12 +256,13 @@ int arm_scan_selective_scan_bidirectional_f32(
   // for L 1024 / 2048 / 4096 against 59 / 92 us for the single-pass kernel that shares
   // the exp (whose whole-row scans and barriers cost more than the exp they save) and
   // 222 us for two launches at L 4096. That launch scans whole rows, one 16-row block
-  // each, so it is taken where its blocks fill the chip (the single-direction scan
-  // would not cut rows into segments either: 256 row blocks or more, or rows of fewer
-  // than two chunks). Fewer rows take the exp-sharing kernel where a row fits it, else
-  // two launches, each cutting its rows into segments.
+  // per direction, so it is taken where those blocks give every CU one (B16 D192: 384
+  // blocks), or where rows are too short to cut into segments anyway. Fewer rows take
+  // the exp-sharing kernel where a row fits it (B1 D1536 L2048: 84 us against 114 us
+  // for two segmented calls), else two launches, each cutting its rows into segments
+  // (B1 D16 L65536: 174 us; B1 D768 L32768: 401 us).
   p.out = out_fwd;
-  const bool jobs_fill = 2 * (dims->batch * dims->dim / 16) >= armscan::kM1WholeRowBlocks ||
+  const bool jobs_fill = 2 * (dims->batch * dims->dim / 16) >= armscan::kM1JobsMinBlocks ||
                          dims->len < 2 * armscan::kM1ChunkSteps;
   if (jobs_fill && armscan::m1_jobs_supported(p)) {
     const armscan::M1JobSpec jobs[2] = {{u, delta, z, b, c, out_fwd, last_fwd, 0},

@@ -41,6 +41,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdint>
 #include <type_traits>
 
@@ -80,6 +81,24 @@ constexpr int kMaxWaves = 8;   // n-tiles per block: dqk <= 128
 constexpr int kKtStride = 20;  // floats per row of a wave's K transpose tile
 constexpr int kStages = 4;   // deepest DMA ring
 constexpr size_t kLdsBudget = 160 * 1024;
+// sequences of fewer chunks stay whole (the fold pass would cost more than it saves)
+constexpr int kMinSplitChunks = 64;
+constexpr int kMinSplitChunksRank1 = 256;
+constexpr int kFoldStages = 8;       // deepest DMA ring of the fold pass
+
+// CUs of the current device (0 if unknown), looked up once per device.
+int device_cus() {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<int> cache[kMaxDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n > 0) return n;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    return 0;
+  cache[dev].store(n, std::memory_order_relaxed);
+  return n;
+}
 
 struct M3K {
   const float *q, *k, *v, *qb, *kb, *cos, *sin, *D, *z, *psi, *zeta, *phi;
@@ -102,6 +121,18 @@ struct M3K {
   int vt, zt, at;            // and per step
   // SISO: no same-step term (gamma on M's diagonal, D x) and out += the result
   int accum;
+  // Sequences cut at chunk `split` (0: whole sequences): blocks [0, seg_blocks) run
+  // chunks [split, nchunks) from the state m3_fold_kernel left in `fold` (seq, dv, dqk),
+  // blocks [seg_blocks, 2 seg_blocks) run chunks [0, split) from zero.
+  int split, seg_blocks;
+  float* fold;
+  int skip_q;  // the stage holds no q section (m3_fold_kernel's): k's comes first
+  // The fold runs in nsub pieces of sub_len chunks, one block each (per sequence and dv
+  // slices): piece s leaves its state from zero in fold + s * nseq * dv * dqk and its
+  // decay (the product of its chunks' e^{c_last}) in fold_decay[s * nseq + seq]; the
+  // resuming blocks combine them in order.
+  int nsub, sub_len;
+  float* fold_decay;
 };
 
 // ---------------------------------------------------------------------------
@@ -195,6 +226,36 @@ __device__ __forceinline__ void wait_vm_at_most(int n) {
   else waitcnt_vm<0>();
 }
 
+// The same with every count up to 24 (the fold pass's deep ring: up to 6 stages of
+// 2 or 3 instructions in flight per wave), coarser above.
+__device__ __forceinline__ void wait_vm_fine(int n) {
+  if (n >= 32) waitcnt_vm<32>();
+  else if (n >= 24) waitcnt_vm<24>();
+  else if (n >= 16) {
+    if (n >= 21) {
+      if (n >= 22) waitcnt_vm<22>();
+      else waitcnt_vm<21>();
+    } else if (n >= 18) {
+      if (n >= 20) waitcnt_vm<20>();
+      else waitcnt_vm<18>();
+    } else if (n >= 17) waitcnt_vm<17>();
+    else waitcnt_vm<16>();
+  } else if (n >= 8) {
+    if (n >= 12) {
+      if (n >= 15) waitcnt_vm<15>();
+      else if (n >= 14) waitcnt_vm<14>();
+      else if (n >= 13) waitcnt_vm<13>();
+      else waitcnt_vm<12>();
+    } else if (n >= 10) {
+      if (n >= 11) waitcnt_vm<11>();
+      else waitcnt_vm<10>();
+    } else if (n >= 9) waitcnt_vm<9>();
+    else waitcnt_vm<8>();
+  } else {
+    wait_vm_at_most(n);
+  }
+}
+
 // Workgroup barrier that orders LDS only: outstanding global loads and stores
 // stay in flight.
 __device__ __forceinline__ void lds_barrier() {
@@ -236,14 +297,16 @@ __device__ __forceinline__ DmaPiece dma_decode(const M3K& p, const SeqIn& s, int
   d.on = true;
   d.rec = false;
   int rel = ins;
-  if (rel < 2 * WN) {
-    const int nt = rel < WN ? rel : rel - WN;
+  const int nq = p.skip_q ? 0 : WN;  // q's instructions
+  if (rel < nq + WN) {
+    const bool isq = rel < nq;
+    const int nt = isq ? rel : rel - nq;
     const int li = lane & 15, lj = lane >> 4;
-    d.src = rel < WN ? s.q : s.k;
+    d.src = isq ? s.q : s.k;
     d.step = li / R;
     d.col = (li % R) * p.groups * p.dqk + nt * 16 + 4 * lj;
     d.stride = s.qstride;
-  } else if ((rel -= 2 * WN) < 2 * p.n_cs) {
+  } else if ((rel -= nq + WN) < 2 * p.n_cs) {
     const bool sn = rel >= p.n_cs;
     const int j = (sn ? rel - p.n_cs : rel) * 64 + lane;
     d.on = j < T * (p.dqk / 8);
@@ -369,11 +432,11 @@ struct DmaRun {
 };
 
 template <int MD>
-__device__ __forceinline__ void dma_run(const DmaPlan<MD>& d, DmaRun<MD>& r) {
+__device__ __forceinline__ void dma_run(const DmaPlan<MD>& d, DmaRun<MD>& r, int first_chunk) {
   r.count = d.count;
 #pragma unroll
   for (int k = 0; k < MD; ++k) {
-    r.ptr[k] = d.base[k];
+    r.ptr[k] = d.base[k] + (long long)first_chunk * d.delta[k];
     r.step[k] = d.delta[k];
     r.off[k] = d.on[k] ? d.off[k] : 0;
     r.lds[k] = d.ins[k] * 256;
@@ -488,8 +551,20 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 4)) m3_chunk_kernel(M3K p) {
   const int ej = ewave ? (wave - WN) % PT : 0;      // slice of an epilogue wave
   const int epar = ewave ? (wave - WN) / PT : 0;    // chunk parity of an epilogue wave
   const int li = lane & 15, lj = lane >> 4;
+  // this block's chunks [cb, ce): the tail segment (from the folded state) comes first
+  // in block order, so that its longer blocks start first; the head segment's blocks
+  // fill the CUs left over, several in turn
+  int bid = blockIdx.x, cb = 0, ce = p.nchunks;
+  if (p.split) {
+    if (bid >= p.seg_blocks) {
+      bid -= p.seg_blocks;
+      ce = p.split;
+    } else {
+      cb = p.split;
+    }
+  }
   // blocks of one sequence share an XCD (block id mod 8), and so its L2
-  const int bx = blockIdx.x & 7, by = blockIdx.x >> 3;
+  const int bx = bid & 7, by = bid >> 3;
   const int nb = p.nparts / PT;  // blocks per sequence
   const int seq = (by / nb) * 8 + bx;
   const int p0 = (by % nb) * PT * 16;  // first dv column of the block
@@ -542,7 +617,7 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 4)) m3_chunk_kernel(M3K p) {
                                 : (((long long)bi * H + h) * L + t0) * dv);
     Stash st = {};
     const bool has_z = p.z != nullptr;
-    const int nchunks = p.nchunks, sfl = p.stage_floats;
+    const int sfl = p.stage_floats;
     const long long chstep = (REV ? -(long long)T : (long long)T) * ostep;  // per chunk
     // part A of chunk ch: the partials reduced and masked (lane: G[li][4lj + r] and the
     // inter-chunk Y[4lj + r][p]); it reads the partial buffers right after the
@@ -618,23 +693,25 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 4)) m3_chunk_kernel(M3K p) {
           st.z[r] = sg[off_z + ((4 * lj + r) / R) * 16 * PT + ej * 16 + li];
       }
     };
-    lds_barrier();  // stage 0 landed
-    if (epar == 0) stash(stages);
+    // chunks cb .. ce-1 (parities by the absolute chunk index, as the partial waves
+    // write them); the ring slot of chunk ch is (ch - cb) mod NS
+    lds_barrier();  // stage of chunk cb landed
+    if ((cb & 1) == epar) stash(stages);
     int slot = 0;
-    for (int ch = 1; ch < nchunks; ++ch) {
+    for (int ch = cb + 1; ch < ce; ++ch) {
       slot = slot + 1 == NS ? 0 : slot + 1;
       lds_barrier();  // stage ch landed, partials of chunk ch-1 written
       const int c = ch - 1;
       if ((c & 1) == epar) part_a(c);
-      else if (c >= 1) part_b(c - 1, std::true_type{});  // this wave's previous chunk
+      else if (c > cb) part_b(c - 1, std::true_type{});  // this wave's previous chunk
       if ((ch & 1) == epar) stash(stages + slot * sfl);
     }
-    lds_barrier();  // partials of the last chunk written
-    const int cl = nchunks - 1;
+    lds_barrier();  // partials of the block's last chunk written
+    const int cl = ce - 1;
     if ((cl & 1) == epar) {
       part_a(cl);
       part_b(cl, std::false_type{});
-    } else if (cl >= 1) {
+    } else if (cl > cb) {
       part_b(cl - 1, std::true_type{});
     }
     return;
@@ -682,13 +759,13 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 4)) m3_chunk_kernel(M3K p) {
   DmaPlan<MD> dp;
   dma_plan<R, REV>(p, in, nt, WN, lane, dp);
   DmaRun<MD> dr;
-  dma_run(dp, dr);
-  const int nchunks = p.nchunks;
+  dma_run(dp, dr, cb);
   const int nfull = L / T;  // chunks wholly inside the sequence
   const int sfl = p.stage_floats;
-  for (int c = 0; c < NS - 1 && c < nchunks; ++c) {
-    if (c < nfull) dma_next(dr, stages + c * sfl);
-    else dma_clamped<R, REV>(p, in, dp, c, stages + c * sfl, lane);
+  // ring slot r holds chunk cb + r first
+  for (int r = 0; r < NS - 1 && cb + r < ce; ++r) {
+    if (cb + r < nfull) dma_next(dr, stages + r * sfl);
+    else dma_clamped<R, REV>(p, in, dp, cb + r, stages + r * sfl, lane);
   }
   const int wait_n = (NS - 2) * dp.count;  // outstanding DMA allowed in the steady state
 
@@ -698,6 +775,14 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 4)) m3_chunk_kernel(M3K p) {
   f4 S[PT];
 #pragma unroll
   for (int j = 0; j < PT; ++j) S[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+  // resuming at chunk cb = split: the head segment's state, its pieces in order
+  for (int sb = 0; cb > 0 && sb < p.nsub; ++sb) {
+    const float dcy = p.fold_decay[sb * p.nseq + seq];
+    const float* fold = p.fold + (long long)sb * p.nseq * dv * dqk;
+#pragma unroll
+    for (int j = 0; j < PT; ++j)
+      S[j] = S[j] * dcy + ld4(fold + ((long long)seq * dv + p0 + j * 16 + li) * dqk + n0);
+  }
   float kc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   f4 wx[PT];
 #pragma unroll
@@ -720,14 +805,14 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 4)) m3_chunk_kernel(M3K p) {
     constexpr bool FAST = decltype(fast)::value;
     // Stage ch has landed once no more of this wave's DMA is outstanding than the
     // stages issued after it.
-    if (FAST || ch + NS - 2 < nchunks - 1) wait_vm_at_most(wait_n);
-    else wait_vm_at_most((nchunks - 1 - ch) * dp.count);
+    if (FAST || ch + NS - 2 < ce - 1) wait_vm_at_most(wait_n);
+    else wait_vm_at_most((ce - 1 - ch) * dp.count);
     lds_barrier();
     const float* sg = stages + slot * sfl;
     float* dstage = stages + dslot * sfl;
     const int dch = ch + NS - 1;  // the chunk this iteration's DMA fetches
-    const bool dma_fast_now = FAST || dch < nfull;
-    if (!FAST && dch >= nfull && dch < nchunks) dma_clamped<R, REV>(p, in, dp, dch, dstage, lane);
+    const bool dma_fast_now = FAST || (dch < nfull && dch < ce);
+    if (!FAST && dch >= nfull && dch < ce) dma_clamped<R, REV>(p, in, dp, dch, dstage, lane);
 
     // ---- q/k rows of this n-tile (LDS reads in flight during the state update)
     const f4 q = ld4(sg + (nt * 64 + lane) * 4);
@@ -847,10 +932,12 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 4)) m3_chunk_kernel(M3K p) {
     slot = slot + 1 == NS ? 0 : slot + 1;
     dslot = dslot + 1 == NS ? 0 : dslot + 1;
   };
-  const int nmain = nfull > NS - 1 ? nfull - (NS - 1) : 0;  // chunks with whole-chunk DMA
-  int ch = 0;
+  // chunks whose DMA target (NS-1 ahead) is a whole chunk of this block's range
+  const int dend = nfull < ce ? nfull : ce;
+  const int nmain = dend - (NS - 1);
+  int ch = cb;
   for (; ch < nmain; ++ch) chunk(ch, std::true_type{});
-  for (; ch < nchunks; ++ch) chunk(ch, std::false_type{});
+  for (; ch < ce; ++ch) chunk(ch, std::false_type{});
   // the last chunk's state update
 #pragma unroll
   for (int j = 0; j < PT; ++j) S[j] *= etot;
@@ -860,21 +947,176 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 4)) m3_chunk_kernel(M3K p) {
     for (int j = 0; j < PT; ++j) S[j] = mfma(kc[m], wx[j][m], S[j]);
   lds_barrier();
 
-  if (p.last_state) {
+  if (p.last_state && ce == p.nchunks) {
 #pragma unroll
     for (int j = 0; j < PT; ++j)
       *reinterpret_cast<f4*>(p.last_state + ((long long)seq * dv + p0 + j * 16 + li) * dqk + n0) =
           S[j];
   }
-  if (p.last_bx && p0 == 0) {
+  if (p.last_bx && p0 == 0 && ce == p.nchunks) {
     // scale k at the final step = k times the w of its row (the chunk's last valid row)
     const int last = p.nchunks - 1;
     if (li % R == 0 && last * T + step_i == L - 1) {
-      const float* sg = stages + (last % NS) * p.stage_floats;
+      const float* sg = stages + ((last - cb) % NS) * p.stage_floats;
       *reinterpret_cast<f4*>(p.last_bx + (long long)seq * dqk + n0) =
           kr_last * sg[off_rec + Rec<R>::W + li / R];
     }
   }
+}
+
+// The state a sequence reaches after its chunks [0, p.split), from zero, written to
+// p.fold (seq, dv, dqk): the partial waves' state update alone (no q, no outputs, no
+// epilogue waves), S = e^{c_last} S + K^T diag(w) X per chunk, for the blocks of
+// m3_chunk_kernel that resume at chunk p.split. Its stage is the scan's without q and z
+// (the host builds this kernel's M3K so: skip_q), about 20 KB at config 3, so that a
+// ring of up to kFoldStages stages keeps 7 chunks of DMA in flight: the pass does little
+// work per chunk, and with the scan's 3 chunks ahead it waited on memory. K is
+// transposed through a per-wave tile, for SISO as for MIMO.
+template <int R, bool MIMO, bool REV, int PT, int MD>
+__global__ void __launch_bounds__(64 * kMaxWaves) m3_fold_kernel(M3K p) {
+  extern __shared__ __attribute__((aligned(16))) float sm[];
+  const int WN = p.dqk / 16;
+  const int lane = threadIdx.x & 63;
+  const int nt = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int li = lane & 15, lj = lane >> 4;
+  const int sub = blockIdx.x / p.seg_blocks;  // this block's piece of the head segment
+  const int bid = blockIdx.x - sub * p.seg_blocks;
+  const int bx = bid & 7, by = bid >> 3;
+  const int nb = p.nparts / PT;
+  const int seq = (by / nb) * 8 + bx;
+  const int p0 = (by % nb) * PT * 16;
+  if (seq >= p.nseq) return;  // whole block: no barrier is reached
+  const int H = p.heads;
+  const int bi = seq / H, h = seq - bi * H;
+  const int grp = h / (H / p.groups);
+  const int L = p.len, dqk = p.dqk, dv = p.dv, T = p.steps_per_chunk, NS = p.nstages;
+  const int half = dqk / 2;
+  const int n0 = nt * 16 + 4 * lj;
+  const bool lo = !MIMO || n0 < half;
+  const int step_i = li / R;
+  // chunks [cb, ce) of the head segment [0, split), all whole (split < L / T)
+  const int cb = sub * p.sub_len;
+  const int ce = cb + p.sub_len < p.split ? cb + p.sub_len : p.split;
+  float* stages = sm;
+  float* kt = stages + NS * p.stage_floats + nt * 16 * kKtStride;
+  const int off_k = 0, off_cs = WN * 256;
+  const int off_sn = off_cs + p.n_cs * 256;
+  const int off_v = off_cs + 2 * p.n_cs * 256;
+  const int off_rec = off_v + p.n_v * 256;
+
+  SeqIn in;
+  in.q = p.q + ((long long)bi * L * R * p.groups + grp) * dqk;
+  in.k = p.k + ((long long)bi * L * R * p.groups + grp) * dqk;
+  in.cos = p.cos + ((long long)bi * L * H + h) * half;
+  in.sin = p.sin + ((long long)bi * L * H + h) * half;
+  in.v = p.v + (long long)bi * p.vb + (long long)h * dv + p0;
+  in.z = nullptr;
+  in.ang = nullptr;
+  in.rec = p.rec + (long long)seq * p.nchunks * p.rec_floats;
+  in.qstride = R * p.groups * dqk;
+  in.csstride = H * half;
+  in.angstride = 0;
+  in.vstride = p.vt;
+  in.zstride = p.vt;
+
+  f4 bk, bkp = {0.0f, 0.0f, 0.0f, 0.0f};
+  const int m0 = n0 < half ? n0 + half : n0 - half;  // MIMO partner columns
+  {
+    const long long bo = ((long long)h * R + (li % R)) * dqk;
+    bk = ld4(p.kb + bo + n0);
+    if (MIMO) bkp = ld4(p.kb + bo + m0);
+  }
+  float psi[PT][4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m)
+#pragma unroll
+    for (int j = 0; j < PT; ++j)
+      psi[j][m] = MIMO ? p.psi[((long long)h * R + (4 * lj + m) % R) * dv + p0 + j * 16 + li]
+                       : 1.0f;
+
+  DmaPlan<MD> dp;
+  dma_plan<R, REV>(p, in, nt, WN, lane, dp);
+  DmaRun<MD> dr;
+  dma_run(dp, dr, cb);
+  const int sfl = p.stage_floats;
+  for (int r = 0; r < NS - 1 && cb + r < ce; ++r) dma_next(dr, stages + r * sfl);
+  const int wait_n = (NS - 2) * dp.count;
+
+  f4 S[PT];
+#pragma unroll
+  for (int j = 0; j < PT; ++j) S[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+  float kc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  f4 wx[PT];
+#pragma unroll
+  for (int j = 0; j < PT; ++j) wx[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+  float etot = 1.0f, decay = 1.0f;
+  float* ktw = kt + li * kKtStride + 4 * lj;
+  const float* ktr = kt + 4 * lj * kKtStride + li;
+  int slot = 0, dslot = NS - 1;
+  for (int ch = cb; ch < ce; ++ch) {
+    if (ch + NS - 2 < ce - 1) wait_vm_fine(wait_n);
+    else wait_vm_fine((ce - 1 - ch) * dp.count);
+    lds_barrier();
+    const float* sg = stages + slot * sfl;
+    float* dstage = stages + dslot * sfl;
+    const bool dma_now = ch + NS - 1 < ce;
+    const f4 k = ld4(sg + off_k + (nt * 64 + lane) * 4);
+    f4 kp = {0.0f, 0.0f, 0.0f, 0.0f}, cs, sn;
+    if (MIMO) {
+      const int pl = ((m0 >> 4) * 64 + ((m0 & 15) >> 2) * 16 + li) * 4;
+      kp = ld4(sg + off_k + pl);
+      const int u4 = (lo ? n0 : n0 - half) >> 2;
+      cs = ld4(sg + off_cs + (u4 * T + step_i) * 4);
+      sn = ld4(sg + off_sn + (u4 * T + step_i) * 4);
+    } else {
+      const int o = ((2 * nt + (lj >> 1)) * T + li) * 4 + 2 * (lj & 1);
+      const f2 c2 = ld2(sg + off_cs + o), s2 = ld2(sg + off_sn + o);
+      cs = f4{c2[0], c2[1], 0.0f, 0.0f};
+      sn = f4{s2[0], s2[1], 0.0f, 0.0f};
+    }
+    // the deferred update of chunk ch-1
+#pragma unroll
+    for (int j = 0; j < PT; ++j) S[j] *= etot;
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+      for (int j = 0; j < PT; ++j) S[j] = mfma(kc[m], wx[j][m], S[j]);
+    if (dma_now) dma_part(dr, dstage, 0, 2);
+    const f4 kr = rope<MIMO>(k, kp, bk, bkp, cs, sn, lo);
+    // K transposed: reduction index s = 4lj + m (rows 4lj + m of the chunk)
+    *reinterpret_cast<f4*>(ktw) = kr;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) kc[m] = ktr[m * kKtStride];
+    f4 w;
+    if (R == 1) {
+      w = ld4(sg + off_rec + Rec<R>::W + 4 * lj);
+    } else {
+#pragma unroll
+      for (int m = 0; m < 4; ++m) w[m] = sg[off_rec + Rec<R>::W + (4 * lj + m) / R];
+    }
+    etot = sg[off_rec + Rec<R>::Etot];
+    decay *= etot;
+#pragma unroll
+    for (int j = 0; j < PT; ++j)
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        wx[j][m] = w[m] * (sg[off_v + ((4 * lj + m) / R) * 16 * PT + j * 16 + li] * psi[j][m]);
+      }
+    if (dma_now) dma_part(dr, dstage, 2, MD);
+    slot = slot + 1 == NS ? 0 : slot + 1;
+    dslot = dslot + 1 == NS ? 0 : dslot + 1;
+  }
+#pragma unroll
+  for (int j = 0; j < PT; ++j) S[j] *= etot;
+#pragma unroll
+  for (int m = 0; m < 4; ++m)
+#pragma unroll
+    for (int j = 0; j < PT; ++j) S[j] = mfma(kc[m], wx[j][m], S[j]);
+  float* fold = p.fold + (long long)sub * p.nseq * dv * dqk;
+#pragma unroll
+  for (int j = 0; j < PT; ++j)
+    *reinterpret_cast<f4*>(fold + ((long long)seq * dv + p0 + j * 16 + li) * dqk + n0) = S[j];
+  if (p0 == 0 && nt == 0 && lane == 0) p.fold_decay[sub * p.nseq + seq] = decay;
 }
 
 size_t chunk_lds_bytes(const M3K& k, int pt, int ns) {
@@ -884,10 +1126,25 @@ size_t chunk_lds_bytes(const M3K& k, int pt, int ns) {
                           (size_t)2 * pt * kMaxWaves * 256 + kt);
 }
 
+size_t fold_lds_bytes(const M3K& k, int ns) {
+  const int WN = k.dqk / 16;
+  return sizeof(float) * ((size_t)ns * k.stage_floats + (size_t)WN * 16 * kKtStride);
+}
+
+template <int R, bool MIMO, int PT, int MD>
+hipError_t launch_fold(const M3K& kf, bool rev, hipStream_t st) {
+  const long long blocks = (long long)kf.seg_blocks * kf.nsub;
+  const size_t lds = fold_lds_bytes(kf, kf.nstages);
+  const dim3 grid((unsigned)blocks), wg(64 * (kf.dqk / 16));
+  if (rev) hipLaunchKernelGGL((m3_fold_kernel<R, MIMO, true, PT, MD>), grid, wg, lds, st, kf);
+  else hipLaunchKernelGGL((m3_fold_kernel<R, MIMO, false, PT, MD>), grid, wg, lds, st, kf);
+  return hipGetLastError();
+}
+
 template <int R, bool MIMO, int PT, bool ZOWN, int MD>
 hipError_t launch_chunk(const M3K& k, bool rev, hipStream_t st) {
   const int WN = k.dqk / 16;
-  const long long blocks = 8LL * (k.nparts / PT) * ((k.nseq + 7) / 8);
+  const long long blocks = 8LL * (k.nparts / PT) * ((k.nseq + 7) / 8) * (k.split ? 2 : 1);
   const size_t lds = chunk_lds_bytes(k, PT, k.nstages);
   if (k.ang) {  // forward only: theta is a forward cumsum
     if (rev) return hipErrorInvalidValue;
@@ -914,12 +1171,20 @@ hipError_t launch_chunk(const M3K& k, bool rev, hipStream_t st) {
   return hipGetLastError();
 }
 
+// The scan, preceded when its sequences are split (k.split) by the fold of their head
+// segments (kf: the same problem, its stage without z), on the same DMA plan width.
 template <int R, bool MIMO>
-hipError_t launch_chunk_pt(const M3K& k, bool rev, hipStream_t st) {
+hipError_t launch_chunk_pt(const M3K& k, const M3K& kf, bool rev, hipStream_t st) {
   const bool narrow = k.n_ins <= kNarrowDma * (k.dqk / 16);
   auto go = [&](auto zown, auto md) {
     constexpr bool Z = decltype(zown)::value;
     constexpr int M = decltype(md)::value;
+    if (k.split) {
+      const hipError_t e = kf.ptiles == 4   ? launch_fold<R, MIMO, 4, M>(kf, rev, st)
+                           : kf.ptiles == 2 ? launch_fold<R, MIMO, 2, M>(kf, rev, st)
+                                            : launch_fold<R, MIMO, 1, M>(kf, rev, st);
+      if (e != hipSuccess) return e;
+    }
     return k.ptiles == 2 ? launch_chunk<R, MIMO, 2, Z, M>(k, rev, st)
                          : launch_chunk<R, MIMO, 1, Z, M>(k, rev, st);
   };
@@ -992,9 +1257,77 @@ hipError_t m3_scan_chunked(const M3Problem& pr, hipStream_t st) {
   if (chunk_lds_bytes(k, k.ptiles, k.nstages) > kLdsBudget) return hipErrorInvalidValue;
   if (k.n_ins > kMaxDma * WN) return hipErrorInvalidValue;  // DMA by the WN partial waves
 
+  // Too few sequences for the chip. A block takes a whole CU (its LDS), so with P
+  // blocks on C > P CUs, C - P CUs idle through the scan. Each sequence is then cut at
+  // chunk `split`: a fold pass first computes the state every sequence reaches there
+  // (the state update alone), then the scan runs 2P blocks, the P that resume at
+  // `split` first and the P head segments [0, split) after them, several in turn on
+  // the CUs the first P leave free. With deep = ceil(P / (C - P)) head segments per
+  // free CU, each paying its ring's fill and drain (about 2 NS chunks), split =
+  // (nchunks - 2 NS (deep - 1)) / (deep + 1) ends both groups together (configs 3 and
+  // 4: 192 blocks on 256 CUs, deep 3, split near a quarter). The fold costs about 0.7
+  // of a scan chunk per chunk at rank 1 and 0.4 at rank 4 (rank-4 chunks hold 4 steps
+  // whose state update is a quarter of their work), so rank 1 splits from 256 chunks
+  // (measured at B4 H24 against whole sequences: L 2048 +5%, 4096 -2%, 8192 -7%) and
+  // other ranks from 64 (rank 4: L 1024 -5%, 2048 -11%, 4096 -14%, 8192 -16%). The fused
+  // angle pre-pass carries theta along the whole sequence, so it keeps whole sequences.
+  M3K kf = k;
+  const long long blocks = (long long)k.nseq * (k.nparts / k.ptiles);
+  const int cus = device_cus();
+  const int min_chunks = R == 1 ? kMinSplitChunksRank1 : kMinSplitChunks;
+  if (!pr.angles && cus > 0 && blocks < cus && k.nchunks >= min_chunks &&
+      2 * chunk_lds_bytes(k, k.ptiles, k.nstages) > kLdsBudget) {
+    const long long deep = (blocks + (cus - blocks) - 1) / (cus - blocks);
+    const int split =
+        (int)((k.nchunks - 2LL * k.nstages * (deep - 1)) / (deep + 1));
+    if (split >= kMinSplitChunks / 4 && split < k.len / k.steps_per_chunk) {
+      k.split = split;
+      k.seg_blocks = 8 * (k.nparts / k.ptiles) * ((k.nseq + 7) / 8);
+      kf.split = split;
+      kf.z = nullptr;  // the fold's stage: the scan's without q and z
+      kf.zown = 0;
+      kf.n_z = 0;
+      kf.skip_q = 1;
+      // a fold block takes up to four dv slices (the scan two), so that the k, cos and
+      // sin rows it shares across slices are fetched once for four (configs 3 and 4)
+      const int T = k.steps_per_chunk;
+      auto fold_plan = [&](int pt) {
+        kf.ptiles = pt;
+        kf.n_v = (T * 4 * pt + 63) / 64;
+        kf.n_ins = WN + 2 * k.n_cs + kf.n_v + (k.rec_floats / 4 + 63) / 64;
+        kf.stage_floats = kf.n_ins * 256;
+      };
+      const int wide = k.n_ins <= kNarrowDma * WN ? kNarrowDma : kMaxDma;  // the scan's plan
+      fold_plan(k.nparts % 4 == 0 ? 4 : k.ptiles);
+      if (kf.n_ins > wide * WN) fold_plan(k.ptiles);
+      const long long fblocks = (long long)k.nseq * (k.nparts / kf.ptiles);
+      // three fold blocks per CU (a shallow ring each: latency is covered by the other
+      // blocks' waves), in as many pieces of the head segment as fill the CUs so
+      kf.nstages = kFoldStages;
+      while (kf.nstages > 2 && 3 * fold_lds_bytes(kf, kf.nstages) > kLdsBudget) --kf.nstages;
+      int nsub = (int)((3LL * cus + fblocks - 1) / fblocks);
+      nsub = nsub < 1 ? 1 : nsub > split ? split : nsub;
+      k.sub_len = kf.sub_len = (split + nsub - 1) / nsub;
+      k.nsub = kf.nsub = (split + k.sub_len - 1) / k.sub_len;
+      kf.seg_blocks = 8 * (k.nparts / kf.ptiles) * ((k.nseq + 7) / 8);
+    }
+  }
+
   const size_t nrec = (size_t)k.nseq * k.nchunks;
   hipError_t e = stream_alloc((void**)&k.rec, nrec * k.rec_floats * sizeof(float), st);
   if (e != hipSuccess) return e;
+  kf.rec = k.rec;
+  if (k.split) {
+    const size_t fs = (size_t)k.nsub * k.nseq * k.dv * k.dqk;
+    e = stream_alloc((void**)&k.fold, (fs + (size_t)k.nsub * k.nseq) * sizeof(float), st);
+    if (e != hipSuccess) {
+      (void)hipFreeAsync(k.rec, st);
+      return e;
+    }
+    k.fold_decay = k.fold + fs;
+    kf.fold = k.fold;
+    kf.fold_decay = k.fold_decay;
+  }
   const unsigned gblocks = (unsigned)((nrec + 15) / 16);
   const int rev = pr.reverse ? 1 : 0;
   if (R == 1) hipLaunchKernelGGL(m3_gates_kernel<1>, dim3(gblocks), dim3(256), 0, st, k, rev);
@@ -1003,12 +1336,16 @@ hipError_t m3_scan_chunked(const M3Problem& pr, hipStream_t st) {
   e = hipGetLastError();
   if (e == hipSuccess) {
     const bool mimo = pr.psi != nullptr;
-    if (!mimo) e = launch_chunk_pt<1, false>(k, rev, st);
-    else if (R == 1) e = launch_chunk_pt<1, true>(k, rev, st);
-    else if (R == 2) e = launch_chunk_pt<2, true>(k, rev, st);
-    else e = launch_chunk_pt<4, true>(k, rev, st);
+    if (!mimo) e = launch_chunk_pt<1, false>(k, kf, rev, st);
+    else if (R == 1) e = launch_chunk_pt<1, true>(k, kf, rev, st);
+    else if (R == 2) e = launch_chunk_pt<2, true>(k, kf, rev, st);
+    else e = launch_chunk_pt<4, true>(k, kf, rev, st);
   }
-  const hipError_t fe = hipFreeAsync(k.rec, st);
+  hipError_t fe = hipFreeAsync(k.rec, st);
+  if (k.fold) {
+    const hipError_t fe2 = hipFreeAsync(k.fold, st);
+    if (fe == hipSuccess) fe = fe2;
+  }
   return e != hipSuccess ? e : fe;
 }
 

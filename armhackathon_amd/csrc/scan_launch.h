@@ -63,6 +63,8 @@ struct M1JobSpec {
 // row blocks (16 rows each) at which a launch stops cutting rows into segments.
 constexpr long long kM1ChunkSteps = 256;
 constexpr long long kM1WholeRowBlocks = 512;
+// blocks from which a multi-traversal launch of whole rows is preferred (one per CU)
+constexpr long long kM1JobsMinBlocks = 256;
 bool m1_jobs_supported(const M1Problem& p);
 hipError_t m1_scan_jobs(const M1Problem& p, const M1JobSpec* spec, int n, hipStream_t st);
 // Batched (planes, H, W) -> (planes, W, H) transposes of up to 8 tensors.

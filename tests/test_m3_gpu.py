@@ -204,6 +204,54 @@ def test_m3_mimo_benchmark_shape(reverse):
     assert rel_err(host(ls), rls) < TOL
 
 
+SPLIT_CASES = [
+    # (mimo, rank, batch, length, heads, dv, dqk, groups): few sequences for the chip, so
+    # each is cut where a fold pass supplies the state the resuming blocks start from;
+    # lengths leave a partial last chunk
+    (False, 1, 1, 4100, 3, 64, 128, 3),
+    (False, 1, 2, 4111, 2, 32, 128, 1),
+    (True, 2, 1, 1030, 2, 64, 128, 2),
+    (True, 4, 1, 1021, 3, 32, 128, 1),
+]
+
+
+@pytest.mark.parametrize("case_", SPLIT_CASES, ids=lambda c: "x".join(map(str, c[1:])))
+@pytest.mark.parametrize("reverse", [False, True])
+def test_m3_split_sequences(case_, reverse):
+    """The sequence split (fold pass + resuming blocks), with D, z, biases and groups,
+    forward and reverse, against the float64 oracle: outputs and final states."""
+    import armhackathon_amd as arm_scan
+
+    mimo, rk, b, L, h, dv, dqk, g = case_
+    case(f"split sequences {case_} reverse={reverse}")
+    x = (workloads.m3_mimo(batch=b, length=L, heads=h, dv=dv, dqk=dqk, rank=rk, seed=L)
+         if mimo else workloads.m3_siso(batch=b, length=L, heads=h, dv=dv, dqk=dqk, seed=L))
+    if g != h:
+        x["q"] = np.ascontiguousarray(x["q"][..., :g, :])
+        x["k"] = np.ascontiguousarray(x["k"][..., :g, :])
+    rng = np.random.default_rng(L + 1)
+    x["q_bias"] = (rng.standard_normal(x["q_bias"].shape) * 0.1).astype(np.float32)
+    x["k_bias"] = (rng.standard_normal(x["k_bias"].shape) * 0.1).astype(np.float32)
+    x["D"] = rng.standard_normal(h).astype(np.float32)
+    x["z"] = rng.standard_normal(x["v"].shape).astype(np.float32)
+    if mimo:
+        x["zeta"] = rng.standard_normal(x["zeta"].shape).astype(np.float32)
+    t = dev(x)
+    kw = dict(psi=x["psi"], zeta=x["zeta"], phi=x["phi"]) if mimo else {}
+    ref, rls, rlbx = oracle.mamba3_scan(*[x[k] for k in SISO_KEYS], x["cos"], x["sin"],
+                                        D=x["D"], z=x["z"], reverse=reverse, dtype=np.float64,
+                                        want_state=True, **kw)
+    if mimo:
+        out, ls = arm_scan.mamba3_mimo_scan(*[t[k] for k in SISO_KEYS], t["psi"], t["zeta"],
+                                            t["phi"], cos=t["cos"], sin=t["sin"], D=t["D"],
+                                            z=t["z"], reverse=reverse, return_last_state=True)
+    else:
+        out, ls, lbx = _siso_gpu(x, reverse=reverse, return_last_state=True)
+        assert rel_err(host(lbx), rlbx) < TOL
+    assert rel_err(host(out), ref.transpose(0, 2, 1, 3)) < TOL
+    assert rel_err(host(ls), rls) < TOL
+
+
 def test_m3_head_major_entry_matches_time_major():
     """arm_scan_mamba3_scan_f32 (the reference's head-major out) and its time-major
     twin write the same values, for the chunked and the step-by-step kernels."""
