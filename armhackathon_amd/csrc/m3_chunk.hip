@@ -1039,8 +1039,22 @@ __global__ void __launch_bounds__(64 * kMaxWaves) m3_fold_kernel(M3K p) {
   DmaRun<MD> dr;
   dma_run(dp, dr, cb);
   const int sfl = p.stage_floats;
-  for (int r = 0; r < NS - 1 && cb + r < ce; ++r) dma_next(dr, stages + r * sfl);
-  const int wait_n = (NS - 2) * dp.count;
+  // One stage of DMA per iteration, chunk ch + NS - 1 or, past the range, chunk ce - 1
+  // again (into the slot of a chunk every wave has finished, which nothing reads), so
+  // that behind the stage a wave waits for there are always NS - 2 of its stages in
+  // flight: a vmcnt known at compile time (the loop below is instantiated per count)
+  // in place of a run-time ladder of them, whose scalar branches cost more than the
+  // chunk's work.
+  auto issue = [&](float* stage, bool advance) {
+#pragma unroll
+    for (int k = 0; k < MD; ++k) {
+      if (k < dr.count) {
+        dma16(dr.ptr[k] + dr.off[k], stage + dr.lds[k]);
+        if (advance) dr.ptr[k] += dr.step[k];
+      }
+    }
+  };
+  for (int r = 0; r < NS - 1; ++r) issue(stages + r * sfl, cb + r < ce - 1);
 
   f4 S[PT];
 #pragma unroll
@@ -1052,60 +1066,70 @@ __global__ void __launch_bounds__(64 * kMaxWaves) m3_fold_kernel(M3K p) {
   float etot = 1.0f, decay = 1.0f;
   float* ktw = kt + li * kKtStride + 4 * lj;
   const float* ktr = kt + 4 * lj * kKtStride + li;
-  int slot = 0, dslot = NS - 1;
-  for (int ch = cb; ch < ce; ++ch) {
-    if (ch + NS - 2 < ce - 1) wait_vm_fine(wait_n);
-    else wait_vm_fine((ce - 1 - ch) * dp.count);
-    lds_barrier();
-    const float* sg = stages + slot * sfl;
-    float* dstage = stages + dslot * sfl;
-    const bool dma_now = ch + NS - 1 < ce;
-    const f4 k = ld4(sg + off_k + (nt * 64 + lane) * 4);
-    f4 kp = {0.0f, 0.0f, 0.0f, 0.0f}, cs, sn;
-    if (MIMO) {
-      const int pl = ((m0 >> 4) * 64 + ((m0 & 15) >> 2) * 16 + li) * 4;
-      kp = ld4(sg + off_k + pl);
-      const int u4 = (lo ? n0 : n0 - half) >> 2;
-      cs = ld4(sg + off_cs + (u4 * T + step_i) * 4);
-      sn = ld4(sg + off_sn + (u4 * T + step_i) * 4);
-    } else {
-      const int o = ((2 * nt + (lj >> 1)) * T + li) * 4 + 2 * (lj & 1);
-      const f2 c2 = ld2(sg + off_cs + o), s2 = ld2(sg + off_sn + o);
-      cs = f4{c2[0], c2[1], 0.0f, 0.0f};
-      sn = f4{s2[0], s2[1], 0.0f, 0.0f};
-    }
-    // the deferred update of chunk ch-1
-#pragma unroll
-    for (int j = 0; j < PT; ++j) S[j] *= etot;
-#pragma unroll
-    for (int m = 0; m < 4; ++m)
-#pragma unroll
-      for (int j = 0; j < PT; ++j) S[j] = mfma(kc[m], wx[j][m], S[j]);
-    if (dma_now) dma_part(dr, dstage, 0, 2);
-    const f4 kr = rope<MIMO>(k, kp, bk, bkp, cs, sn, lo);
-    // K transposed: reduction index s = 4lj + m (rows 4lj + m of the chunk)
-    *reinterpret_cast<f4*>(ktw) = kr;
-#pragma unroll
-    for (int m = 0; m < 4; ++m) kc[m] = ktr[m * kKtStride];
-    f4 w;
-    if (R == 1) {
-      w = ld4(sg + off_rec + Rec<R>::W + 4 * lj);
-    } else {
-#pragma unroll
-      for (int m = 0; m < 4; ++m) w[m] = sg[off_rec + Rec<R>::W + (4 * lj + m) / R];
-    }
-    etot = sg[off_rec + Rec<R>::Etot];
-    decay *= etot;
-#pragma unroll
-    for (int j = 0; j < PT; ++j)
-#pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        wx[j][m] = w[m] * (sg[off_v + ((4 * lj + m) / R) * 16 * PT + j * 16 + li] * psi[j][m]);
+  auto run = [&](auto wcount) {
+    constexpr int W = decltype(wcount)::value;
+    int slot = 0, dslot = NS - 1;
+    for (int ch = cb; ch < ce; ++ch) {
+      waitcnt_vm<W>();
+      lds_barrier();
+      const float* sg = stages + slot * sfl;
+      float* dstage = stages + dslot * sfl;
+      const f4 k = ld4(sg + off_k + (nt * 64 + lane) * 4);
+      f4 kp = {0.0f, 0.0f, 0.0f, 0.0f}, cs, sn;
+      if (MIMO) {
+        const int pl = ((m0 >> 4) * 64 + ((m0 & 15) >> 2) * 16 + li) * 4;
+        kp = ld4(sg + off_k + pl);
+        const int u4 = (lo ? n0 : n0 - half) >> 2;
+        cs = ld4(sg + off_cs + (u4 * T + step_i) * 4);
+        sn = ld4(sg + off_sn + (u4 * T + step_i) * 4);
+      } else {
+        const int o = ((2 * nt + (lj >> 1)) * T + li) * 4 + 2 * (lj & 1);
+        const f2 c2 = ld2(sg + off_cs + o), s2 = ld2(sg + off_sn + o);
+        cs = f4{c2[0], c2[1], 0.0f, 0.0f};
+        sn = f4{s2[0], s2[1], 0.0f, 0.0f};
       }
-    if (dma_now) dma_part(dr, dstage, 2, MD);
-    slot = slot + 1 == NS ? 0 : slot + 1;
-    dslot = dslot + 1 == NS ? 0 : dslot + 1;
+      // the deferred update of chunk ch-1
+#pragma unroll
+      for (int j = 0; j < PT; ++j) S[j] *= etot;
+#pragma unroll
+      for (int m = 0; m < 4; ++m)
+#pragma unroll
+        for (int j = 0; j < PT; ++j) S[j] = mfma(kc[m], wx[j][m], S[j]);
+      issue(dstage, ch + NS - 1 < ce - 1);
+      const f4 kr = rope<MIMO>(k, kp, bk, bkp, cs, sn, lo);
+      // K transposed: reduction index s = 4lj + m (rows 4lj + m of the chunk)
+      *reinterpret_cast<f4*>(ktw) = kr;
+#pragma unroll
+      for (int m = 0; m < 4; ++m) kc[m] = ktr[m * kKtStride];
+      f4 w;
+      if (R == 1) {
+        w = ld4(sg + off_rec + Rec<R>::W + 4 * lj);
+      } else {
+#pragma unroll
+        for (int m = 0; m < 4; ++m) w[m] = sg[off_rec + Rec<R>::W + (4 * lj + m) / R];
+      }
+      etot = sg[off_rec + Rec<R>::Etot];
+      decay *= etot;
+#pragma unroll
+      for (int j = 0; j < PT; ++j)
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+          wx[j][m] = w[m] * (sg[off_v + ((4 * lj + m) / R) * 16 * PT + j * 16 + li] * psi[j][m]);
+      slot = slot + 1 == NS ? 0 : slot + 1;
+      dslot = dslot + 1 == NS ? 0 : dslot + 1;
+    }
+  };
+  using std::integral_constant;
+  switch ((NS - 2) * dr.count) {  // wave-uniform
+    case 1: run(integral_constant<int, 1>{}); break;
+    case 2: run(integral_constant<int, 2>{}); break;
+    case 3: run(integral_constant<int, 3>{}); break;
+    case 4: run(integral_constant<int, 4>{}); break;
+    case 6: run(integral_constant<int, 6>{}); break;
+    case 8: run(integral_constant<int, 8>{}); break;
+    default: run(integral_constant<int, 0>{}); break;  // waits for more: always safe
   }
+  waitcnt_vm<0>();  // the re-fetches past the range land before the block's LDS is freed
 #pragma unroll
   for (int j = 0; j < PT; ++j) S[j] *= etot;
 #pragma unroll
