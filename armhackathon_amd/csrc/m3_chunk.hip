@@ -801,11 +801,15 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 4)) m3_chunk_kernel(M3K p) {
   // One chunk. FAST: the chunk this iteration's DMA fetches lies wholly inside the
   // sequence, so the DMA is issued unconditionally and the compiler may schedule the
   // MFMA phases across it.
-  auto chunk = [&](const int ch, auto fast) {
+  // WAIT: the steady state's vmcnt when known at compile time (the steady-state loop
+  // below is instantiated for the common counts), else -1 (a run-time ladder).
+  auto chunk = [&](const int ch, auto fast, auto wait_c) {
     constexpr bool FAST = decltype(fast)::value;
+    constexpr int WAIT = decltype(wait_c)::value;
     // Stage ch has landed once no more of this wave's DMA is outstanding than the
     // stages issued after it.
-    if (FAST || ch + NS - 2 < ce - 1) wait_vm_at_most(wait_n);
+    if constexpr (FAST && WAIT >= 0) waitcnt_vm<WAIT>();
+    else if (FAST || ch + NS - 2 < ce - 1) wait_vm_at_most(wait_n);
     else wait_vm_at_most((ce - 1 - ch) * dp.count);
     lds_barrier();
     const float* sg = stages + slot * sfl;
@@ -936,8 +940,20 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 4)) m3_chunk_kernel(M3K p) {
   const int dend = nfull < ce ? nfull : ce;
   const int nmain = dend - (NS - 1);
   int ch = cb;
-  for (; ch < nmain; ++ch) chunk(ch, std::true_type{});
-  for (; ch < ce; ++ch) chunk(ch, std::false_type{});
+  using std::integral_constant;
+  auto steady = [&](auto wait_c) {
+    for (; ch < nmain; ++ch) chunk(ch, std::true_type{}, wait_c);
+  };
+  switch (wait_n) {  // wave-uniform: (NS - 2) stages of this wave's DMA plan
+    case 2: steady(integral_constant<int, 2>{}); break;
+    case 3: steady(integral_constant<int, 3>{}); break;
+    case 4: steady(integral_constant<int, 4>{}); break;
+    case 6: steady(integral_constant<int, 6>{}); break;
+    case 8: steady(integral_constant<int, 8>{}); break;
+    case 12: steady(integral_constant<int, 12>{}); break;
+    default: steady(integral_constant<int, -1>{}); break;
+  }
+  for (; ch < ce; ++ch) chunk(ch, std::false_type{}, integral_constant<int, -1>{});
   // the last chunk's state update
 #pragma unroll
   for (int j = 0; j < PT; ++j) S[j] *= etot;
