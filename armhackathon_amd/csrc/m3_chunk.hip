@@ -443,12 +443,13 @@ __device__ __forceinline__ void dma_run(const DmaPlan<MD>& d, DmaRun<MD>& r, int
   }
 }
 
-// Instructions k0 .. k1-1 of the next whole chunk.
-template <int MD>
+// Instructions k0 .. k1-1 of the next whole chunk. CNT: the plan's instruction count
+// when known at compile time (no per-instruction branch), else -1 (r.count).
+template <int MD, int CNT = -1>
 __device__ __forceinline__ void dma_part(DmaRun<MD>& r, float* stage, int k0, int k1) {
 #pragma unroll
   for (int k = 0; k < MD; ++k) {
-    if (k >= k0 && k < k1 && k < r.count) {
+    if (k >= k0 && k < k1 && (CNT >= 0 ? k < CNT : k < r.count)) {
       dma16(r.ptr[k] + r.off[k], stage + r.lds[k]);
       r.ptr[k] += r.step[k];
     }
@@ -801,10 +802,14 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 4)) m3_chunk_kernel(M3K p) {
   // One chunk. FAST: the chunk this iteration's DMA fetches lies wholly inside the
   // sequence, so the DMA is issued unconditionally and the compiler may schedule the
   // MFMA phases across it.
-  // WAIT: the steady state's vmcnt when known at compile time (the steady-state loop
-  // below is instantiated for the common counts), else -1 (a run-time ladder).
-  auto chunk = [&](const int ch, auto fast, auto wait_c) {
+  // CNT: this wave's DMA instructions per stage when known at compile time, else -1;
+  // WAIT: the steady state's vmcnt, (NS - 2) stages of them, when known, else -1 (a
+  // run-time ladder). The steady-state loop below is instantiated for the common plans:
+  // scalar branches per chunk (the ladder, a test per DMA instruction) slowed it, and the
+  // compile-time vmcnt took configs 3 and 4 from 0.310 / 1.000 to 0.297 / 0.926 ms.
+  auto chunk = [&](const int ch, auto fast, auto cnt_c, auto wait_c) {
     constexpr bool FAST = decltype(fast)::value;
+    constexpr int CNT = decltype(cnt_c)::value;
     constexpr int WAIT = decltype(wait_c)::value;
     // Stage ch has landed once no more of this wave's DMA is outstanding than the
     // stages issued after it.
@@ -846,7 +851,7 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 4)) m3_chunk_kernel(M3K p) {
     for (int m = 0; m < 4; ++m)
 #pragma unroll
       for (int j = 0; j < PT; ++j) S[j] = mfma(kc[m], wx[j][m], S[j]);
-    if (dma_fast_now) dma_part(dr, dstage, 0, 1);
+    if (dma_fast_now) dma_part<MD, FAST ? CNT : -1>(dr, dstage, 0, 1);
     // ---- rotated q/k rows
     if (ANG) {
       // pairs 4u4 .. 4u4+3 of the lane (MIMO) or 2 at 8nt + 2lj (SISO); past nang 0
@@ -884,7 +889,7 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 4)) m3_chunk_kernel(M3K p) {
     const f4 qr = rope<MIMO>(q, qp, bq, bqp, cs, sn, lo);
     const f4 kr = rope<MIMO>(k, kp, bk, bkp, cs, sn, lo);
     kr_last = kr;
-    if (dma_fast_now) dma_part(dr, dstage, 1, 2);
+    if (dma_fast_now) dma_part<MD, FAST ? CNT : -1>(dr, dstage, 1, 2);
     // ---- K transposed through LDS: the operand of this chunk's (deferred) state
     // update. SISO: in this wave's own q piece of the stage (read above; no other wave
     // reads it), rows of 16 floats, with the reduction index s = lj + 4m so that the
@@ -927,12 +932,12 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 4)) m3_chunk_kernel(M3K p) {
 #pragma unroll
       for (int j = 0; j < PT; ++j) yp[j] = mfma(qr[r], S[j][r], yp[j]);
     }
-    if (dma_fast_now) dma_part(dr, dstage, 2, 3);
+    if (dma_fast_now) dma_part<MD, FAST ? CNT : -1>(dr, dstage, 2, 3);
     *reinterpret_cast<f4*>(gw + par * kMaxWaves * 256) = gp;
 #pragma unroll
     for (int j = 0; j < PT; ++j)
       *reinterpret_cast<f4*>(yw + ((par * PT + j) * kMaxWaves) * 256) = yp[j];
-    if (dma_fast_now) dma_part(dr, dstage, 3, MD);
+    if (dma_fast_now) dma_part<MD, FAST ? CNT : -1>(dr, dstage, 3, MD);
     slot = slot + 1 == NS ? 0 : slot + 1;
     dslot = dslot + 1 == NS ? 0 : dslot + 1;
   };
@@ -941,19 +946,38 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 4)) m3_chunk_kernel(M3K p) {
   const int nmain = dend - (NS - 1);
   int ch = cb;
   using std::integral_constant;
-  auto steady = [&](auto wait_c) {
-    for (; ch < nmain; ++ch) chunk(ch, std::true_type{}, wait_c);
+  auto steady = [&](auto cnt_c, auto wait_c) {
+    for (; ch < nmain; ++ch) chunk(ch, std::true_type{}, cnt_c, wait_c);
   };
-  switch (wait_n) {  // wave-uniform: (NS - 2) stages of this wave's DMA plan
-    case 2: steady(integral_constant<int, 2>{}); break;
-    case 3: steady(integral_constant<int, 3>{}); break;
-    case 4: steady(integral_constant<int, 4>{}); break;
-    case 6: steady(integral_constant<int, 6>{}); break;
-    case 8: steady(integral_constant<int, 8>{}); break;
-    case 12: steady(integral_constant<int, 12>{}); break;
-    default: steady(integral_constant<int, -1>{}); break;
+  using I2 = integral_constant<int, 2>;
+  using I3 = integral_constant<int, 3>;
+  using I4 = integral_constant<int, 4>;
+  using IX = integral_constant<int, -1>;
+  // Rank 1 fixes the instruction count as well (config 3: 0.296 -> 0.293 ms); at rank 4
+  // that schedule came out slower (config 4: 0.918 -> 0.959 ms), so it keeps the count a
+  // run-time value. Both bit-identical.
+  if constexpr (R == 1) {
+    switch (NS * 16 + dp.count) {  // wave-uniform
+      case 4 * 16 + 4: steady(I4{}, integral_constant<int, 8>{}); break;  // config 3, waves 0-3
+      case 4 * 16 + 3: steady(I3{}, integral_constant<int, 6>{}); break;  // config 3, waves 4-7
+      case 4 * 16 + 2: steady(I2{}, I4{}); break;
+      case 3 * 16 + 4: steady(I4{}, I4{}); break;
+      case 3 * 16 + 3: steady(I3{}, I3{}); break;
+      case 3 * 16 + 2: steady(I2{}, I2{}); break;
+      default: steady(IX{}, IX{}); break;
+    }
+  } else {
+    switch (wait_n) {  // wave-uniform
+      case 2: steady(IX{}, I2{}); break;
+      case 3: steady(IX{}, I3{}); break;
+      case 4: steady(IX{}, I4{}); break;                           // config 4, waves 4-7
+      case 6: steady(IX{}, integral_constant<int, 6>{}); break;   // config 4, waves 0-3
+      case 8: steady(IX{}, integral_constant<int, 8>{}); break;
+      case 12: steady(IX{}, integral_constant<int, 12>{}); break;
+      default: steady(IX{}, IX{}); break;
+    }
   }
-  for (; ch < ce; ++ch) chunk(ch, std::false_type{}, integral_constant<int, -1>{});
+  for (; ch < ce; ++ch) chunk(ch, std::false_type{}, IX{}, IX{});
   // the last chunk's state update
 #pragma unroll
   for (int j = 0; j < PT; ++j) S[j] *= etot;
