@@ -532,19 +532,21 @@ __device__ __forceinline__ void issue_tile(float* tile, const float* Bg, const f
   }
 }
 
-// Strided z through LDS: the block's 16 channels of a FULL chunk's 256 steps, as
+// Strided z through LDS: the block's 16 channels of a chunk's 256 steps, as
 // [step][channel] (16 KB). With zs_d == 1 the four channels 4q .. 4q+3 of a step
 // are one 16-byte piece, so the block fetches whole 64-byte runs instead of each
 // wave pulling 16 bytes out of every line it touches. DMA op m holds the steps
 // 16m .. 16m+15 (lane block m of the chunk); its slot L holds piece
 // x = L ^ m: step 16m + x/4, channels 4(x%4) .. +3 — the XOR spreads the 16 lanes
-// that read one step of their blocks over the banks.
+// that read one step of their blocks over the banks. `part`: the row's tail chunk,
+// whose steps past the row's end are read from kZeroPiece (0, as the bounds-checked
+// loads give).
 constexpr int kZStageFloats = 16 * 256;
 
 template <bool REV>
 __device__ __forceinline__ void issue_z_stage(float* zbuf, const float* zslab, long long zs_t,
                                               long long L, long long c0, int d0, int wave,
-                                              int lane) {
+                                              int lane, bool part = false) {
   // recomputed per chunk: hoisting these addresses out of the chunk loop would hold
   // registers through the whole scan
   asm volatile("" : "+v"(lane));
@@ -553,7 +555,8 @@ __device__ __forceinline__ void issue_z_stage(float* zbuf, const float* zslab, l
     const int m = m0 + wave;  // wave-uniform
     const int x = lane ^ m;
     const long long s = c0 + 16 * m + (x >> 2);  // traversal step
-    const float* src = zslab + d0 + 4 * (x & 3) + (REV ? L - 1 - s : s) * zs_t;
+    const float* src = part && s >= L ? kZeroPiece
+                                      : zslab + d0 + 4 * (x & 3) + (REV ? L - 1 - s : s) * zs_t;
     __builtin_amdgcn_global_load_lds((const void*)src,
                                      (__attribute__((address_space(3))) void*)(zbuf + m * 256),
                                      16, 0, 0);
@@ -586,16 +589,19 @@ __device__ __forceinline__ void write_out_stage(float* zbuf, int j, int wave, in
   for (int i = 0; i < 16; ++i) base[16 * (i ^ jh)] = v[i];
 }
 
+// `part`: the row's tail chunk, whose steps past the row's end are not stored.
 template <bool REV>
 __device__ __forceinline__ void store_out_stage(const float* zbuf, float* oslab, long long os_t,
                                                 long long L, long long c0, int d0, int wave,
-                                                int lane) {
+                                                int lane, bool part = false) {
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int m = 4 * r + wave;
     const float4 v = *reinterpret_cast<const float4*>(zbuf + m * 256 + 4 * (lane ^ m));
     const long long s = c0 + 16 * m + (lane >> 2);  // traversal step
-    *reinterpret_cast<float4*>(oslab + d0 + 4 * (lane & 3) + (REV ? L - 1 - s : s) * os_t) = v;
+    if (!part || s < L)
+      *reinterpret_cast<float4*>(oslab + d0 + 4 * (lane & 3) + (REV ? L - 1 - s : s) * os_t) =
+          v;
   }
 }
 
@@ -695,9 +701,9 @@ __device__ __forceinline__ void tile_states(const float* tile, int n0, int N, in
 // registers in it). ALN: rows 16-byte aligned (L % 4 == 0, aligned bases), so that
 // rows move in 16-byte pieces; otherwise single floats (SIO 0 only).
 // The row's tail chunk (L % 256 steps) runs in the tile loop as well: its loads and
-// stores check bounds (per lane, by strides, bypassing the LDS stages of SIO 2 and
-// 3), its B/C positions past the row read zeros, and its steps past the row's end
-// are identity maps (dt = 0). TAIL: compiled only for rows with a tail chunk
+// stores check bounds (per lane, by strides, for SIO 1; in the DMA and the stores of
+// the LDS stages of SIO 2 and 3), its B/C positions past the row read zeros, and its
+// steps past the row's end are identity maps (dt = 0). TAIL: compiled only for rows with a tail chunk
 // (L % 256 != 0), so that the kernels for whole chunks carry none of its code.
 // DWBC: B/C rows are not 16-byte multiples in memory, and the tiles fill by single-float
 // DMA (the allocation-free entry, the multi-traversal launch); otherwise their rows are
@@ -851,11 +857,12 @@ __device__ __forceinline__ void tile_rows(const M1Kern& p, long long blk, int se
   // c's last tile's states.
   const int d0 = (int)(blk * (kWavesPerBlock * RPW) % p.dim);  // the block's first channel
   auto z_stage = [&](long long c) {
-    issue_z_stage<REV>(zbuf, p.z + bib * p.zs_b, p.zs_t, L, c * CH, d0, wave, lane);
+    issue_z_stage<REV>(zbuf, p.z + bib * p.zs_b, p.zs_t, L, c * CH, d0, wave, lane,
+                       TAIL && c >= nfull);
   };
   // u through the stage too: per chunk, u's DMA, its read, then z's DMA
   constexpr bool ustage = SIO == 3;
-  if (SIO == 2 && p.z && ce > cb) z_stage(cb);
+  if (SIO == 2 && p.z && cl > cb) z_stage(cb);
 
   long long k = 0;  // tile counter
   // One chunk; FULL: every step inside the row. The tail chunk is its own compiled
@@ -868,19 +875,20 @@ __device__ __forceinline__ void tile_rows(const M1Kern& p, long long blk, int se
     {
       float dd[I], uu[I];
       load_c(drow, sb, full, dd);
-      if (ustr && !full) {
-        load_tail<I, REV>(urow, L, sb, p.us_t, uu);
-      } else if (ustage) {
+      if (ustage) {
         if constexpr (SIO == 3) {
           // the block's 16 channels of u, 64-byte runs, land with delta's loads; the
           // stage is free (the previous chunk's outputs have left it) and z's DMA
           // follows once every lane has read its u
-          issue_z_stage<REV>(zbuf, p.u + bib * p.us_b, p.us_t, L, c * CH, d0, wave, lane);
+          issue_z_stage<REV>(zbuf, p.u + bib * p.us_b, p.us_t, L, c * CH, d0, wave, lane,
+                             !full);
           tile_sync();
           read_z_stage(zbuf, j, wave, rw, uu);
           lds_barrier();
           if (p.z) z_stage(c);
         }
+      } else if (ustr && !full) {
+        load_tail<I, REV>(urow, L, sb, p.us_t, uu);
       } else if (ustr) {
         const long long tlo = REV ? L - sb - I : sb;  // the block's lowest memory step
         load_block_strided<I, REV>(slab_rsrc(p.u + bib * p.us_b, p.u_bytes),
@@ -928,8 +936,7 @@ __device__ __forceinline__ void tile_rows(const M1Kern& p, long long blk, int se
         // after the states (no registers held through them), before the sync after
         // which the outputs overwrite it
         static_assert(SIO < 2 || I == 16, "the stage holds 16 steps per lane block");
-        if (full) read_z_stage(zbuf, j, wave, rw, zz);
-        else load_tail<I, REV>(zrow, L, sb, p.zs_t, zz);
+        read_z_stage(zbuf, j, wave, rw, zz);
       }
       tile_sync();
     }
@@ -937,12 +944,13 @@ __device__ __forceinline__ void tile_rows(const M1Kern& p, long long blk, int se
 #pragma unroll
       for (int i = 0; i < I; ++i) y[i] *= silu_fast(zz[i]);
     }
-    if (SIO >= 2 && full) {
+    if constexpr (SIO >= 2) {
       write_out_stage(zbuf, j, wave, rw, y);
       lds_barrier();
-      store_out_stage<REV>(zbuf, p.out + bib * p.os_b, p.os_t, L, c * CH, d0, wave, lane);
+      store_out_stage<REV>(zbuf, p.out + bib * p.os_b, p.os_t, L, c * CH, d0, wave, lane,
+                           !full);
       lds_barrier();  // every lane has read its outputs before the next z stage lands
-      if (p.z && c + 1 < ce && !ustage) z_stage(c + 1);
+      if (p.z && c + 1 < cl && !ustage) z_stage(c + 1);
     } else {
       store_out(sb, y, full);
     }

@@ -511,7 +511,9 @@ def test_causal_conv1d_update_token_by_token(width):
 
 
 @pytest.mark.parametrize("shape", [(2, 64, 512, False), (1, 32, 300, False), (2, 64, 512, True),
-                                   (8, 1024, 512, True), (8, 1536, 2048, False)],
+                                   (8, 1024, 512, True), (8, 1536, 2048, False),
+                                   (1, 32, 300, True), (2, 48, 100, False), (2, 64, 1500, True),
+                                   (8, 1024, 700, False), (8, 1024, 700, True)],
                          ids=lambda s: "x".join(map(str, s)))
 @pytest.mark.parametrize("gate", [True, False], ids=["z", "noz"])
 @pytest.mark.parametrize("utm", [True, False], ids=["utm", "ucont"])
@@ -519,8 +521,9 @@ def test_time_major_u(shape, gate, utm):
     """z and out views of time-major storage, and u one too (the HF mixer's convolution
     output laid out for its x_proj) or contiguous: bit-identical to the contiguous
     call. Time-major u goes through the block's LDS stage, with z or without it. Few
-    rows take the segmented scan (its fold reads u by strides too); L = 300 has a tail
-    chunk."""
+    rows take the segmented scan (its fold reads u by strides too); L 300, 1500 and 700
+    end in a tail chunk, and L 100 is one, whose stage reads zeros past the row's end
+    and stores only the steps inside it, forward and reverse."""
     import torch
 
     import armhackathon_amd as arm_scan
