@@ -1165,8 +1165,14 @@ __global__ void __launch_bounds__(64 * kMaxWaves) m3_fold_kernel(M3K p) {
     case 2: run(integral_constant<int, 2>{}); break;
     case 3: run(integral_constant<int, 3>{}); break;
     case 4: run(integral_constant<int, 4>{}); break;
+    case 5: run(integral_constant<int, 5>{}); break;
     case 6: run(integral_constant<int, 6>{}); break;
     case 8: run(integral_constant<int, 8>{}); break;
+    case 9: run(integral_constant<int, 9>{}); break;
+    case 10: run(integral_constant<int, 10>{}); break;
+    case 12: run(integral_constant<int, 12>{}); break;
+    case 15: run(integral_constant<int, 15>{}); break;
+    case 18: run(integral_constant<int, 18>{}); break;
     default: run(integral_constant<int, 0>{}); break;  // waits for more: always safe
   }
   waitcnt_vm<0>();  // the re-fetches past the range land before the block's LDS is freed
@@ -1365,11 +1371,16 @@ hipError_t m3_scan_chunked(const M3Problem& pr, hipStream_t st) {
       fold_plan(k.nparts % 4 == 0 ? 4 : k.ptiles);
       if (kf.n_ins > wide * WN) fold_plan(k.ptiles);
       const long long fblocks = (long long)k.nseq * (k.nparts / kf.ptiles);
-      // three fold blocks per CU (a shallow ring each: latency is covered by the other
-      // blocks' waves), in as many pieces of the head segment as fill the CUs so
+      // up to three fold blocks per CU, as many as fit in LDS with a ring of two stages
+      // (a shallow ring each: latency is covered by the other blocks' waves), and the
+      // head segment in as many pieces as keep every fold block resident at once: a
+      // second round of blocks would double the pass (config 3: two blocks per CU, five
+      // pieces of 12 chunks, 480 blocks; eight pieces, 768 blocks, ran in two rounds)
+      int bpc = 3;
+      while (bpc > 1 && bpc * fold_lds_bytes(kf, 2) > kLdsBudget) --bpc;
       kf.nstages = kFoldStages;
-      while (kf.nstages > 2 && 3 * fold_lds_bytes(kf, kf.nstages) > kLdsBudget) --kf.nstages;
-      int nsub = (int)((3LL * cus + fblocks - 1) / fblocks);
+      while (kf.nstages > 2 && bpc * fold_lds_bytes(kf, kf.nstages) > kLdsBudget) --kf.nstages;
+      int nsub = (int)(bpc * (long long)cus / fblocks);
       nsub = nsub < 1 ? 1 : nsub > split ? split : nsub;
       k.sub_len = kf.sub_len = (split + nsub - 1) / nsub;
       k.nsub = kf.nsub = (split + k.sub_len - 1) / k.sub_len;
