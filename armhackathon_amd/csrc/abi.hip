@@ -78,6 +78,60 @@ int run(hipError_t e, const char* where) {
   return ARM_SCAN_OK;
 }
 
+// The allocation-free entry's calls share one static scratch array per device. A call
+// on a stream other than the previous call's first makes its stream wait for an event
+// recorded after that call's kernels, so calls made on two streams run one after the
+// other instead of racing on the array. The event is created once per device, at the
+// first call there. A stream being captured into a graph is left alone (an event from
+// outside the capture cannot order it), and so is the order of the captured calls:
+// the graph's own dependencies must order them.
+class ScratchOrder {
+ public:
+  // Before the call's launches: order `st` after the previous call, if on another stream.
+  hipError_t enter(hipStream_t st) {
+    mu_.lock();
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    hipError_t e = hipStreamIsCapturing(st, &cs);
+    if (e != hipSuccess) {  // a query refused during another stream's capture: order nothing
+      (void)hipGetLastError();
+      cs = hipStreamCaptureStatusActive;
+      e = hipSuccess;
+    }
+    capturing_ = cs != hipStreamCaptureStatusNone;
+    if (!capturing_) {
+      if (done_ == nullptr) e = hipEventCreateWithFlags(&done_, hipEventDisableTiming);
+      if (e == hipSuccess && used_ && last_ != st) e = hipStreamWaitEvent(st, done_, 0);
+    }
+    if (e != hipSuccess) mu_.unlock();
+    return e;
+  }
+  // After them (only after a successful enter): mark the call's end on its stream.
+  hipError_t leave(hipStream_t st, bool launched) {
+    hipError_t e = hipSuccess;
+    if (launched && !capturing_) {
+      e = hipEventRecord(done_, st);
+      used_ = e == hipSuccess;
+      last_ = st;
+    }
+    mu_.unlock();
+    return e;
+  }
+
+ private:
+  std::mutex mu_;
+  hipEvent_t done_ = nullptr;
+  hipStream_t last_ = nullptr;
+  bool used_ = false, capturing_ = false;
+};
+
+ScratchOrder* scratch_order() {
+  constexpr int kMaxDevices = 64;
+  static ScratchOrder orders[kMaxDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  return &orders[dev];
+}
+
 }  // namespace
 
 namespace armscan {
@@ -171,7 +225,14 @@ int arm_scan_selective_scan_noalloc_f32(const ArmScanDims* dims, const float* u,
   // allocated, and the plan never needs more than the scratch holds
   if (hipError_t e = armscan::m1_noalloc_scratch(&p.scratch, &p.scratch_bytes))
     return hip_fail(e, "scratch lookup");
-  return run(armscan::m1_scan(p, (hipStream_t)stream), "selective_scan (no-alloc) launch");
+  const hipStream_t st = (hipStream_t)stream;
+  ScratchOrder* order = scratch_order();
+  if (order == nullptr) return hip_fail(hipErrorInvalidDevice, "scratch order");
+  if (hipError_t e = order->enter(st)) return hip_fail(e, "ordering after the previous call");
+  const hipError_t e = armscan::m1_scan(p, st);
+  const hipError_t e2 = order->leave(st, e == hipSuccess);
+  if (e != hipSuccess) return hip_fail(e, "selective_scan (no-alloc) launch");
+  return run(e2, "recording the call's end");
 }
 
 int arm_scan_selective_scan_strided_f32(const ArmScanDims* dims, const float* u,

@@ -106,8 +106,11 @@ int arm_scan_selective_scan_f32(const ArmScanDims* dims, const float* u, const f
  * the process ends.
  * No size is rejected for it: a plan whose maps would exceed 4 MiB is cut to fewer
  * segments (whole rows need none). Every map is written before it is read, so no
- * call depends on what the array held before. Calls that overlap on one GPU (two
- * streams at once) share the array and race: serialise them. */
+ * call depends on what the array held before. Calls on two streams of one GPU share
+ * the array: a call made on a stream other than the previous call's makes its stream
+ * wait for that call's kernels (an event, created at the first call on the GPU), so
+ * they run one after the other. Calls recorded into a HIP graph are not ordered so:
+ * the graph's dependencies must order them, or they race. */
 int arm_scan_selective_scan_noalloc_f32(const ArmScanDims* dims, const float* u,
                                         const float* delta, const float* a, const float* b,
                                         const float* c, const float* d_skip, const float* z,

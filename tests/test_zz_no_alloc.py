@@ -149,3 +149,39 @@ def test_noalloc_records_no_allocation(shape):
         case("allocating entry capture (control)")
         types = _captured_node_types("arm_scan_selective_scan_f32", x, False)
         assert types is None or (MEM_ALLOC in types and MEM_FREE in types), types
+
+
+def test_noalloc_calls_on_two_streams():
+    """Calls on two streams share the device's scratch: the library makes each call's
+    stream wait for the previous call's kernels when it was made on the other stream,
+    so the two run one after the other. Long rows on the few-rows plan (maps in the
+    scratch), alternating streams with nothing synchronised in between: every output
+    equals the allocating entry's, bit for bit."""
+    import torch
+
+    shape = (1, 768, 32768, 16)
+    b, d, L, n = shape
+    xs = [workloads.m1_layer(batch=b, dim=d, length=L, state=n, seed=60 + i) for i in range(2)]
+    refs = [_call("arm_scan_selective_scan_f32", x, True) for x in xs]
+    ts = [dev(x) for x in xs]
+    outs = [[torch.empty((b, d, L), device="cuda") for _ in range(3)] for _ in range(2)]
+    lasts = [[torch.empty((b, d, n), device="cuda") for _ in range(3)] for _ in range(2)]
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    torch.cuda.synchronize()
+    lib = _ffi.load()
+    for rnd in range(3):
+        for i in range(2):
+            case(f"noalloc two streams: round {rnd} input {i} on stream {i}")
+            t = ts[i]
+            p = lambda k: None if t.get(k) is None else t[k].data_ptr()  # noqa: E731
+            rc = lib.arm_scan_selective_scan_noalloc_f32(
+                ctypes.byref(_ffi.ArmScanDims(b, d, L, n, 1)), p("u"), p("delta"), p("A"),
+                p("B"), p("C"), p("D"), p("z"), p("delta_bias"), 1, 0, 0, 0,
+                outs[i][rnd].data_ptr(), lasts[i][rnd].data_ptr(), None,
+                streams[i].cuda_stream)
+            assert rc == 0, lib.arm_scan_last_error()
+    torch.cuda.synchronize()
+    for i in range(2):
+        for rnd in range(3):
+            assert np.array_equal(host(outs[i][rnd]), refs[i][0]), (i, rnd)
+            assert np.array_equal(host(lasts[i][rnd]), refs[i][1]), (i, rnd)
