@@ -117,3 +117,37 @@ def test_ss2d_benchmark_shape():
                              dtype=np.float64, want_state=True)
     assert rel_err(host(out), ref.sum(0)) < 1e-4
     assert rel_err(host(last), rlast) < 1e-4
+
+
+@pytest.mark.parametrize("merge", ["sum", "mean", "none"])
+def test_ss2d_out_off_aligned_base(merge):
+    """An 8x8 grid (rows of 16-byte multiples, so the merge may move float4 pieces) with
+    the caller's out one float past an aligned base: the merge checks out's alignment,
+    not only the grid's, and moves single floats there. Through the C ABI, against the
+    oracle, and equal to the same call into an aligned out."""
+    import torch
+
+    from armhackathon_amd import _ffi
+
+    b, d, h, w, n = 2, 16, 8, 8, 16
+    case(f"ss2d 8x8, out one float off an aligned base, merge={merge}")
+    x = workloads.ss2d(batch=b, dim=d, height=h, width=w, state=n, seed=88)
+    t = dev(x)
+    planes = 4 if merge == "none" else 1
+    size = planes * b * d * h * w
+    buf = torch.full((size + 1,), float("nan"), device="cuda")
+    aligned = torch.full((size,), float("nan"), device="cuda")
+    dims = _ffi.ArmSS2DDims(b, d, h, w, n)
+    st = torch.cuda.current_stream().cuda_stream
+    for out in (buf[1:], aligned):
+        _ffi.ss2d_raw(dims, t["u"].data_ptr(), t["delta"].data_ptr(), t["A"].data_ptr(),
+                      t["B4"].data_ptr(), t["C4"].data_ptr(), t["D"].data_ptr(),
+                      t["z"].data_ptr(), 0, False, merge, out.data_ptr(), stream=st)
+    torch.cuda.synchronize()
+    assert np.isnan(host(buf[:1])).all()  # nothing written before out
+    ref = oracle.ss2d(x["u"], x["delta"], x["A"], x["B4"], x["C4"], D=x["D"], z=x["z"],
+                      dtype=np.float64)
+    want = ref if merge == "none" else ref.sum(0) * (0.25 if merge == "mean" else 1.0)
+    got = host(buf[1:]).reshape(want.shape)
+    assert rel_err(got, want) < 1e-4
+    assert np.array_equal(got, host(aligned).reshape(want.shape))
