@@ -133,6 +133,13 @@ struct M3K {
   // resuming blocks combine them in order.
   int nsub, sub_len;
   float* fold_decay;
+  // With the fused angle pre-pass (SISO): fold piece s rotates its keys by theta
+  // relative to its first step and leaves theta's increment over its steps (turns,
+  // reduced to [-1/2, 1/2]) per angle pair, 64 per sequence, at
+  // theta[(s * nseq + seq) * 64 + pair]. Rotations compose, so its state equals the
+  // true one times the rotation by theta at the piece's start (the increments of the
+  // pieces before it), which the resuming blocks apply to the state's key columns.
+  float* theta;
 };
 
 // ---------------------------------------------------------------------------
@@ -224,36 +231,6 @@ __device__ __forceinline__ void wait_vm_at_most(int n) {
   else if (n >= 2) waitcnt_vm<2>();
   else if (n >= 1) waitcnt_vm<1>();
   else waitcnt_vm<0>();
-}
-
-// The same with every count up to 24 (the fold pass's deep ring: up to 6 stages of
-// 2 or 3 instructions in flight per wave), coarser above.
-__device__ __forceinline__ void wait_vm_fine(int n) {
-  if (n >= 32) waitcnt_vm<32>();
-  else if (n >= 24) waitcnt_vm<24>();
-  else if (n >= 16) {
-    if (n >= 21) {
-      if (n >= 22) waitcnt_vm<22>();
-      else waitcnt_vm<21>();
-    } else if (n >= 18) {
-      if (n >= 20) waitcnt_vm<20>();
-      else waitcnt_vm<18>();
-    } else if (n >= 17) waitcnt_vm<17>();
-    else waitcnt_vm<16>();
-  } else if (n >= 8) {
-    if (n >= 12) {
-      if (n >= 15) waitcnt_vm<15>();
-      else if (n >= 14) waitcnt_vm<14>();
-      else if (n >= 13) waitcnt_vm<13>();
-      else waitcnt_vm<12>();
-    } else if (n >= 10) {
-      if (n >= 11) waitcnt_vm<11>();
-      else waitcnt_vm<10>();
-    } else if (n >= 9) waitcnt_vm<9>();
-    else waitcnt_vm<8>();
-  } else {
-    wait_vm_at_most(n);
-  }
 }
 
 // Workgroup barrier that orders LDS only: outstanding global loads and stores
@@ -776,13 +753,36 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 4)) m3_chunk_kernel(M3K p) {
   f4 S[PT];
 #pragma unroll
   for (int j = 0; j < PT; ++j) S[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-  // resuming at chunk cb = split: the head segment's state, its pieces in order
+  // fused angles: theta before the chunk of the pairs the lane computes (SISO: pairs
+  // 8nt + 2lj + e)
+  float carry[2] = {0.0f, 0.0f};       // SISO: 2 per lane
+  // resuming at chunk cb = split: the head segment's state, its pieces in order, and
+  // with fused angles theta there, the pieces' increments summed
   for (int sb = 0; cb > 0 && sb < p.nsub; ++sb) {
     const float dcy = p.fold_decay[sb * p.nseq + seq];
     const float* fold = p.fold + (long long)sb * p.nseq * dv * dqk;
+    float c0 = 1.0f, s0 = 0.0f, c1 = 1.0f, s1 = 0.0f;
+    if (ANG && !MIMO) {  // the piece's keys were rotated from its own start: rotate by
+                         // theta there, the increments of the pieces before it
+      c0 = __builtin_amdgcn_cosf(carry[0]);
+      s0 = __builtin_amdgcn_sinf(carry[0]);
+      c1 = __builtin_amdgcn_cosf(carry[1]);
+      s1 = __builtin_amdgcn_sinf(carry[1]);
+      const float* th = p.theta + ((long long)sb * p.nseq + seq) * 64 + 8 * nt + 2 * lj;
 #pragma unroll
-    for (int j = 0; j < PT; ++j)
-      S[j] = S[j] * dcy + ld4(fold + ((long long)seq * dv + p0 + j * 16 + li) * dqk + n0);
+      for (int e = 0; e < 2; ++e) {
+        carry[e] += th[e];
+        carry[e] -= __builtin_rintf(carry[e]);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < PT; ++j) {
+      const f4 f = ld4(fold + ((long long)seq * dv + p0 + j * 16 + li) * dqk + n0);
+      const f4 r = ANG && !MIMO ? f4{f[0] * c0 - f[1] * s0, f[0] * s0 + f[1] * c0,
+                                     f[2] * c1 - f[3] * s1, f[2] * s1 + f[3] * c1}
+                                : f;
+      S[j] = S[j] * dcy + r;
+    }
   }
   float kc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   f4 wx[PT];
@@ -790,8 +790,6 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 4)) m3_chunk_kernel(M3K p) {
   for (int j = 0; j < PT; ++j) wx[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
   float etot = 1.0f;
   f4 kr_last = {0.0f, 0.0f, 0.0f, 0.0f};
-  // fused angles: theta before the chunk of the pairs the lane computes
-  float carry[2] = {0.0f, 0.0f};       // SISO: 2 per lane
   float carry_m[4 / R] = {};           // MIMO: 4/R per lane
   float* gw = gbuf + (nt * 64 + lane) * 4;         // this wave's G partial, chunk parity 0
   float* yw = ybuf + (nt * 256 + lane * 4);        // its Y partials: + ((par * PT + j) * 8) * 256
@@ -1040,9 +1038,12 @@ __global__ void __launch_bounds__(64 * kMaxWaves) m3_fold_kernel(M3K p) {
   float* stages = sm;
   float* kt = stages + NS * p.stage_floats + nt * 16 * kKtStride;
   const int off_k = 0, off_cs = WN * 256;
-  const int off_sn = off_cs + p.n_cs * 256;
-  const int off_v = off_cs + 2 * p.n_cs * 256;
+  const int off_sn = off_cs + p.n_cs * 256, off_ang = off_cs + 2 * p.n_cs * 256;
+  const int off_v = off_ang + p.n_ang * 256;
   const int off_rec = off_v + p.n_v * 256;
+  // the fused angle pre-pass (SISO): the stage holds raw angles in place of cos/sin,
+  // and theta enters the piece as the sum of the pieces before it
+  const bool ang = !MIMO && p.ang != nullptr;
 
   SeqIn in;
   in.q = p.q + ((long long)bi * L * R * p.groups + grp) * dqk;
@@ -1051,11 +1052,11 @@ __global__ void __launch_bounds__(64 * kMaxWaves) m3_fold_kernel(M3K p) {
   in.sin = p.sin + ((long long)bi * L * H + h) * half;
   in.v = p.v + (long long)bi * p.vb + (long long)h * dv + p0;
   in.z = nullptr;
-  in.ang = nullptr;
+  in.ang = ang ? p.ang + (long long)bi * p.ab + (long long)h * p.ah : nullptr;
   in.rec = p.rec + (long long)seq * p.nchunks * p.rec_floats;
   in.qstride = R * p.groups * dqk;
   in.csstride = H * half;
-  in.angstride = 0;
+  in.angstride = p.at;
   in.vstride = p.vt;
   in.zstride = p.vt;
 
@@ -1104,6 +1105,9 @@ __global__ void __launch_bounds__(64 * kMaxWaves) m3_fold_kernel(M3K p) {
 #pragma unroll
   for (int j = 0; j < PT; ++j) wx[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
   float etot = 1.0f, decay = 1.0f;
+  // fused angles: theta before the chunk (SISO pairs 8nt + 2lj + e), relative to the
+  // piece's first step
+  float carry[2] = {0.0f, 0.0f};
   float* ktw = kt + li * kKtStride + 4 * lj;
   const float* ktr = kt + 4 * lj * kKtStride + li;
   auto run = [&](auto wcount) {
@@ -1122,6 +1126,21 @@ __global__ void __launch_bounds__(64 * kMaxWaves) m3_fold_kernel(M3K p) {
         const int u4 = (lo ? n0 : n0 - half) >> 2;
         cs = ld4(sg + off_cs + (u4 * T + step_i) * 4);
         sn = ld4(sg + off_sn + (u4 * T + step_i) * 4);
+      } else if (ang) {
+        // pairs 8nt + 2lj, +1 (0 past nang); a wave whose pairs all lie past nang
+        // (wave-uniform) takes the identity rotation, as the scan's does
+        if (8 * nt >= p.nang) {
+          cs = f4{1.0f, 1.0f, 0.0f, 0.0f};
+          sn = f4{0.0f, 0.0f, 0.0f, 0.0f};
+        } else {
+          const int u4 = 2 * nt + (lj >> 1);
+          const f2 a2 = 4 * u4 < p.nang ? ld2(sg + off_ang + (u4 * T + li) * 4 + 2 * (lj & 1))
+                                        : f2{0.0f, 0.0f};
+          float a[2] = {a2[0], a2[1]}, c[2], sv[2];
+          fused_angles<R, 2>(a, sg[off_rec + Rec<R>::Hdt + li], li, lane, carry, c, sv);
+          cs = f4{c[0], c[1], 0.0f, 0.0f};
+          sn = f4{sv[0], sv[1], 0.0f, 0.0f};
+        }
       } else {
         const int o = ((2 * nt + (lj >> 1)) * T + li) * 4 + 2 * (lj & 1);
         const f2 c2 = ld2(sg + off_cs + o), s2 = ld2(sg + off_sn + o);
@@ -1187,6 +1206,11 @@ __global__ void __launch_bounds__(64 * kMaxWaves) m3_fold_kernel(M3K p) {
   for (int j = 0; j < PT; ++j)
     *reinterpret_cast<f4*>(fold + ((long long)seq * dv + p0 + j * 16 + li) * dqk + n0) = S[j];
   if (p0 == 0 && nt == 0 && lane == 0) p.fold_decay[sub * p.nseq + seq] = decay;
+  if (ang && p0 == 0 && li == 0) {  // theta's increment over the piece (0 past nang)
+    float* th = p.theta + ((long long)sub * p.nseq + seq) * 64 + 8 * nt + 2 * lj;
+    th[0] = carry[0];
+    th[1] = carry[1];
+  }
 }
 
 size_t chunk_lds_bytes(const M3K& k, int pt, int ns) {
@@ -1199,6 +1223,40 @@ size_t chunk_lds_bytes(const M3K& k, int pt, int ns) {
 size_t fold_lds_bytes(const M3K& k, int ns) {
   const int WN = k.dqk / 16;
   return sizeof(float) * ((size_t)ns * k.stage_floats + (size_t)WN * 16 * kKtStride);
+}
+
+// Blocks of the fold kernel kf launches that one CU holds at once with `lds` bytes of LDS
+// each: its registers limit them as well as its LDS (the rank-4 MIMO fold's 88 VGPRs
+// allow five waves a SIMD, so two blocks of eight waves a CU where LDS would allow three).
+template <int R, bool MIMO>
+int fold_resident(const M3K& kf, size_t lds, bool narrow) {
+  int n = 0;
+  auto occ = [&](const void* kernel) {
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, 64 * (kf.dqk / 16), lds) !=
+        hipSuccess) {
+      (void)hipGetLastError();
+      n = 1;
+    }
+  };
+  const int pt = kf.ptiles;
+  if (narrow) {
+    if (pt == 4) occ(reinterpret_cast<const void*>(&m3_fold_kernel<R, MIMO, false, 4, kNarrowDma>));
+    else if (pt == 2) occ(reinterpret_cast<const void*>(&m3_fold_kernel<R, MIMO, false, 2, kNarrowDma>));
+    else occ(reinterpret_cast<const void*>(&m3_fold_kernel<R, MIMO, false, 1, kNarrowDma>));
+  } else {
+    if (pt == 4) occ(reinterpret_cast<const void*>(&m3_fold_kernel<R, MIMO, false, 4, kMaxDma>));
+    else if (pt == 2) occ(reinterpret_cast<const void*>(&m3_fold_kernel<R, MIMO, false, 2, kMaxDma>));
+    else occ(reinterpret_cast<const void*>(&m3_fold_kernel<R, MIMO, false, 1, kMaxDma>));
+  }
+  return n;
+}
+
+int fold_resident_any(const M3K& kf, size_t lds, bool narrow) {
+  if (kf.psi == nullptr) return fold_resident<1, false>(kf, lds, narrow);
+  const int R = 16 / kf.steps_per_chunk;
+  if (R == 1) return fold_resident<1, true>(kf, lds, narrow);
+  if (R == 2) return fold_resident<2, true>(kf, lds, narrow);
+  return fold_resident<4, true>(kf, lds, narrow);
 }
 
 template <int R, bool MIMO, int PT, int MD>
@@ -1339,13 +1397,15 @@ hipError_t m3_scan_chunked(const M3Problem& pr, hipStream_t st) {
   // of a scan chunk per chunk at rank 1 and 0.4 at rank 4 (rank-4 chunks hold 4 steps
   // whose state update is a quarter of their work), so rank 1 splits from 256 chunks
   // (measured at B4 H24 against whole sequences: L 2048 +5%, 4096 -2%, 8192 -7%) and
-  // other ranks from 64 (rank 4: L 1024 -5%, 2048 -11%, 4096 -14%, 8192 -16%). The fused
-  // angle pre-pass carries theta along the whole sequence, so it keeps whole sequences.
+  // other ranks from 64 (rank 4: L 1024 -5%, 2048 -11%, 4096 -14%, 8192 -16%). With the
+  // fused angle pre-pass (SISO) the fold pieces rotate by theta from their own start and
+  // the resuming blocks rotate each piece's state by theta at the piece's start (the
+  // pieces' increments summed); MIMO keeps whole sequences.
   M3K kf = k;
   const long long blocks = (long long)k.nseq * (k.nparts / k.ptiles);
   const int cus = device_cus();
   const int min_chunks = R == 1 ? kMinSplitChunksRank1 : kMinSplitChunks;
-  if (!pr.angles && cus > 0 && blocks < cus && k.nchunks >= min_chunks &&
+  if ((!pr.angles || !k.psi) && cus > 0 && blocks < cus && k.nchunks >= min_chunks &&
       2 * chunk_lds_bytes(k, k.ptiles, k.nstages) > kLdsBudget) {
     const long long deep = (blocks + (cus - blocks) - 1) / (cus - blocks);
     const int split =
@@ -1364,20 +1424,24 @@ hipError_t m3_scan_chunked(const M3Problem& pr, hipStream_t st) {
       auto fold_plan = [&](int pt) {
         kf.ptiles = pt;
         kf.n_v = (T * 4 * pt + 63) / 64;
-        kf.n_ins = WN + 2 * k.n_cs + kf.n_v + (k.rec_floats / 4 + 63) / 64;
+        kf.n_ins = WN + 2 * k.n_cs + k.n_ang + kf.n_v + (k.rec_floats / 4 + 63) / 64;
         kf.stage_floats = kf.n_ins * 256;
       };
       const int wide = k.n_ins <= kNarrowDma * WN ? kNarrowDma : kMaxDma;  // the scan's plan
       fold_plan(k.nparts % 4 == 0 ? 4 : k.ptiles);
       if (kf.n_ins > wide * WN) fold_plan(k.ptiles);
       const long long fblocks = (long long)k.nseq * (k.nparts / kf.ptiles);
-      // up to three fold blocks per CU, as many as fit in LDS with a ring of two stages
-      // (a shallow ring each: latency is covered by the other blocks' waves), and the
-      // head segment in as many pieces as keep every fold block resident at once: a
-      // second round of blocks would double the pass (config 3: two blocks per CU, five
-      // pieces of 12 chunks, 480 blocks; eight pieces, 768 blocks, ran in two rounds)
+      // up to three fold blocks per CU, as many as the CU holds with a ring of two stages
+      // (a shallow ring each: latency is covered by the other blocks' waves; LDS and
+      // registers both limit them), and the head segment in as many pieces as keep every
+      // fold block resident at once: a second round of blocks would double the pass
+      // (config 3: two blocks per CU, five pieces of 12 chunks, 480 blocks; eight pieces,
+      // 768 blocks, ran in two rounds)
+      const bool narrow = k.n_ins <= kNarrowDma * WN;  // the DMA plan launch_chunk_pt takes
       int bpc = 3;
-      while (bpc > 1 && bpc * fold_lds_bytes(kf, 2) > kLdsBudget) --bpc;
+      while (bpc > 1 && (bpc * fold_lds_bytes(kf, 2) > kLdsBudget ||
+                         fold_resident_any(kf, fold_lds_bytes(kf, 2), narrow) < bpc))
+        --bpc;
       kf.nstages = kFoldStages;
       while (kf.nstages > 2 && bpc * fold_lds_bytes(kf, kf.nstages) > kLdsBudget) --kf.nstages;
       int nsub = (int)(bpc * (long long)cus / fblocks);
@@ -1394,14 +1458,17 @@ hipError_t m3_scan_chunked(const M3Problem& pr, hipStream_t st) {
   kf.rec = k.rec;
   if (k.split) {
     const size_t fs = (size_t)k.nsub * k.nseq * k.dv * k.dqk;
-    e = stream_alloc((void**)&k.fold, (fs + (size_t)k.nsub * k.nseq) * sizeof(float), st);
+    const size_t ds = (size_t)k.nsub * k.nseq, ts = k.ang ? ds * 64 : 0;
+    e = stream_alloc((void**)&k.fold, (fs + ds + ts) * sizeof(float), st);
     if (e != hipSuccess) {
       (void)hipFreeAsync(k.rec, st);
       return e;
     }
     k.fold_decay = k.fold + fs;
+    k.theta = k.ang ? k.fold_decay + ds : nullptr;
     kf.fold = k.fold;
     kf.fold_decay = k.fold_decay;
+    kf.theta = k.theta;
   }
   const unsigned gblocks = (unsigned)((nrec + 15) / 16);
   const int rev = pr.reverse ? 1 : 0;

@@ -252,6 +252,44 @@ def test_m3_split_sequences(case_, reverse):
     assert rel_err(host(ls), rls) < TOL
 
 
+SPLIT_ANGLE_CASES = [
+    # (batch, length, heads, dv, dqk, groups, r): few sequences, so the fused route cuts
+    # them too; theta enters each fold piece and the resuming blocks from a pass that
+    # sums the pieces' angle increments. r = 12 leaves partial waves whose pairs all lie
+    # past r (the identity rotation); lengths leave a partial last chunk
+    (1, 4100, 3, 64, 128, 3, 12),
+    (2, 4111, 2, 32, 128, 1, 32),
+    (1, 4096, 2, 64, 128, 2, 64),
+]
+
+
+@pytest.mark.parametrize("case_", SPLIT_ANGLE_CASES, ids=lambda c: "x".join(map(str, c)))
+def test_m3_split_fused_angles(case_):
+    """The sequence split on the fused angle route (SISO), with D, z, biases and groups,
+    against the float64 pre-pass and oracle: outputs, final states and last_bx."""
+    from armhackathon_amd.mamba3 import _run_angles
+
+    b, L, h, dv, dqk, g, r = case_
+    case(f"split fused angles {case_}")
+    x = workloads.m3_siso(batch=b, length=L, heads=h, dv=dv, dqk=dqk, seed=L + 7)
+    if g != h:
+        x["q"] = np.ascontiguousarray(x["q"][:, :, :g])
+        x["k"] = np.ascontiguousarray(x["k"][:, :, :g])
+    rng = np.random.default_rng(L + 8)
+    x["q_bias"] = (rng.standard_normal((h, dqk)) * 0.1).astype(np.float32)
+    x["k_bias"] = (rng.standard_normal((h, dqk)) * 0.1).astype(np.float32)
+    x["D"] = rng.standard_normal(h).astype(np.float32)
+    x["z"] = rng.standard_normal(x["v"].shape).astype(np.float32)
+    angles, x["cos"], x["sin"] = _angle_inputs(x, r, L + 9)
+    ref, rls, rlbx = _siso_ref(x, want_state=True)
+    t = dev(x)
+    out, ls, lbx = _run_angles(*[t[k] for k in SISO_KEYS], dev(angles), t["D"], t["z"], None,
+                               None, None, True)
+    assert rel_err(host(out), ref.transpose(0, 2, 1, 3)) < TOL
+    assert rel_err(host(ls), rls) < TOL
+    assert rel_err(host(lbx), rlbx) < TOL
+
+
 def test_m3_head_major_entry_matches_time_major():
     """arm_scan_mamba3_scan_f32 (the reference's head-major out) and its time-major
     twin write the same values, for the chunked and the step-by-step kernels."""
