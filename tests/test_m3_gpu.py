@@ -212,6 +212,12 @@ SPLIT_CASES = [
     (False, 1, 2, 4111, 2, 32, 128, 1),
     (True, 2, 1, 1030, 2, 64, 128, 2),
     (True, 4, 1, 1021, 3, 32, 128, 1),
+    # narrower state and odd slice counts: dqk 64 (four partial waves) with dv 48 (three
+    # 16-column slices: one a block, the fold's too); dv 16 with dqk 32, whose blocks
+    # fit two a CU, so those sequences stay whole (the planner's other branch)
+    (False, 1, 1, 4100, 2, 48, 64, 1),
+    (False, 1, 1, 4096, 2, 16, 32, 2),
+    (True, 4, 1, 1030, 2, 48, 64, 2),
 ]
 
 
@@ -260,6 +266,9 @@ SPLIT_ANGLE_CASES = [
     (1, 4100, 3, 64, 128, 3, 12),
     (2, 4111, 2, 32, 128, 1, 32),
     (1, 4096, 2, 64, 128, 2, 64),
+    # dqk 64 with dv 48 (one slice a block); dv 16 with dqk 32 stays whole
+    (1, 4100, 2, 48, 64, 1, 16),
+    (1, 4096, 2, 16, 32, 2, 8),
 ]
 
 
