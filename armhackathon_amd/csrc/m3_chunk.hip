@@ -194,10 +194,13 @@ __global__ void __launch_bounds__(256) m3_gates_kernel(M3K p, int reverse) {
   if (p.rec_floats > RC::Floats) rec[RC::Hdt + row] = hdt;  // 0 past the end: theta holds
   if (row % R == 0) {  // the step's first row writes the step's entries
     if constexpr (R == 1) {
+      // row i's 16-byte pieces rotated by i/2 (piece q at (q + i/2) & 3): the scan's
+      // epilogue reads a piece per lane, rows 64 bytes (16 banks) apart, and rotated the
+      // eight lanes of a 128-byte read phase meet no bank conflict
       f4* mrow = reinterpret_cast<f4*>(rec + RC::M + row * 16);
 #pragma unroll
       for (int q = 0; q < 4; ++q)
-        mrow[q] = f4{m[4 * q], m[4 * q + 1], m[4 * q + 2], m[4 * q + 3]};
+        mrow[(q + (row >> 1)) & 3] = f4{m[4 * q], m[4 * q + 1], m[4 * q + 2], m[4 * q + 3]};
     } else {
 #pragma unroll
       for (int q = 0; q < RC::T; ++q) rec[RC::M + step * RC::T + q] = m[q * R];
@@ -653,7 +656,7 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 4)) m3_chunk_kernel(M3K p) {
     auto stash = [&](const float* sg) {
       using RC = Rec<R>;
       if constexpr (R == 1) {
-        st.m = ld4(sg + off_rec + RC::M + li * 16 + 4 * lj);
+        st.m = ld4(sg + off_rec + RC::M + li * 16 + 4 * ((lj + (li >> 1)) & 3));
         st.ec = ld4(sg + off_rec + RC::Ec + 4 * lj);
       } else {  // rows 4lj + r lie in steps (4lj + r) / R
 #pragma unroll
@@ -894,10 +897,16 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 4)) m3_chunk_kernel(M3K p) {
     // column reads meet no bank conflict. MIMO, whose partner pieces other waves read:
     // in a tile of the wave's own. The round trip and the reads of w x overlap the
     // MFMA chains below.
+    // Row r's 16-byte pieces sit rotated by r/2 (piece c at 4 ((c + r/2) & 3)): rows are
+    // 64 bytes, 16 banks, apart, so unrotated the eight lanes of a 128-byte write phase
+    // (rows 0 .. 7 of one piece) would meet in two bank groups; rotated they cover all
+    // eight, and the column reads stay conflict-free.
     float* const kq = stages + slot * sfl + nt * 256;
-    *reinterpret_cast<f4*>(KQ ? kq + li * 16 + 4 * lj : ktw) = kr;
+    *reinterpret_cast<f4*>(KQ ? kq + li * 16 + 4 * ((lj + (li >> 1)) & 3) : ktw) = kr;
 #pragma unroll
-    for (int m = 0; m < 4; ++m) kc[m] = KQ ? kq[(lj + 4 * m) * 16 + li] : ktr[m * kKtStride];
+    for (int m = 0; m < 4; ++m)
+      kc[m] = KQ ? kq[(lj + 4 * m) * 16 + 4 * (((li >> 2) + (lj >> 1) + 2 * m) & 3) + (li & 3)]
+                 : ktr[m * kKtStride];
     {
       f4 w;
       if (KQ) {  // SISO: rows lj + 4m
