@@ -268,6 +268,16 @@ struct DmaPiece {
   bool on, rec;
 };
 
+// The v and z sections of a stage hold step s's w4 = 4PT pieces rotated by half of them
+// when bits 0 and 2 of s differ: the reads of steps s and s+1 (the partial waves' w x)
+// and of s and s+4 (the epilogue waves' x and z) by a 32-lane half then fall in
+// different banks instead of on the same ones 128 bytes apart. Float offset of (step s,
+// column c) in such a section; the DMA fills it through the inverse map.
+__device__ __forceinline__ int vrot(int s, int w4) { return ((s ^ (s >> 2)) & 1) * (w4 >> 1); }
+__device__ __forceinline__ int vpos(int s, int c, int w4) {
+  return s * 4 * w4 + 4 * (((c >> 2) + vrot(s, w4)) & (w4 - 1)) + (c & 3);
+}
+
 template <int R>
 __device__ __forceinline__ DmaPiece dma_decode(const M3K& p, const SeqIn& s, int ins, int lane) {
   const int WN = p.dqk / 16, T = p.steps_per_chunk;
@@ -308,7 +318,7 @@ __device__ __forceinline__ DmaPiece dma_decode(const M3K& p, const SeqIn& s, int
     d.on = j < T * w4;
     d.src = zz ? s.z : s.v;
     d.step = j / w4;
-    d.col = 4 * (j % w4);
+    d.col = 4 * (((j % w4) - vrot(d.step, w4)) & (w4 - 1));  // slot j % w4 holds that piece
     d.stride = zz ? s.zstride : s.vstride;
   } else {
     const int j = (rel - p.n_v - p.n_z) * 64 + lane;
@@ -667,11 +677,11 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 4)) m3_chunk_kernel(M3K p) {
       }
 #pragma unroll
       for (int m = 0; m < 4; ++m)
-        st.x[m] = sg[off_v + ((4 * lj + m) / R) * 16 * PT + ej * 16 + li] * psi[m];
+        st.x[m] = sg[off_v + vpos((4 * lj + m) / R, ej * 16 + li, 4 * PT)] * psi[m];
       if (has_z) {
 #pragma unroll
         for (int r = 0; r < 4; r += R)
-          st.z[r] = sg[off_z + ((4 * lj + r) / R) * 16 * PT + ej * 16 + li];
+          st.z[r] = sg[off_z + vpos((4 * lj + r) / R, ej * 16 + li, 4 * PT)];
       }
     };
     // chunks cb .. ce-1 (parities by the absolute chunk index, as the partial waves
@@ -924,7 +934,7 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 4)) m3_chunk_kernel(M3K p) {
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
           const int srow = KQ ? lj + 4 * m : (4 * lj + m) / R;  // the step of row s
-          wx[j][m] = w[m] * (sg[off_v + srow * 16 * PT + j * 16 + li] * psi[j][m]);
+          wx[j][m] = w[m] * (sg[off_v + vpos(srow, j * 16 + li, 4 * PT)] * psi[j][m]);
         }
     }
     // ---- partial G^T, and partial Q S0^T per slice: 1 + PT chains, interleaved
@@ -1182,7 +1192,7 @@ __global__ void __launch_bounds__(64 * kMaxWaves) m3_fold_kernel(M3K p) {
       for (int j = 0; j < PT; ++j)
 #pragma unroll
         for (int m = 0; m < 4; ++m)
-          wx[j][m] = w[m] * (sg[off_v + ((4 * lj + m) / R) * 16 * PT + j * 16 + li] * psi[j][m]);
+          wx[j][m] = w[m] * (sg[off_v + vpos((4 * lj + m) / R, j * 16 + li, 4 * PT)] * psi[j][m]);
       slot = slot + 1 == NS ? 0 : slot + 1;
       dslot = dslot + 1 == NS ? 0 : dslot + 1;
     }
