@@ -268,12 +268,16 @@ struct DmaPiece {
   bool on, rec;
 };
 
-// The v and z sections of a stage hold step s's w4 = 4PT pieces rotated by half of them
-// when bits 0 and 2 of s differ: the reads of steps s and s+1 (the partial waves' w x)
-// and of s and s+4 (the epilogue waves' x and z) by a 32-lane half then fall in
-// different banks instead of on the same ones 128 bytes apart. Float offset of (step s,
-// column c) in such a section; the DMA fills it through the inverse map.
-__device__ __forceinline__ int vrot(int s, int w4) { return ((s ^ (s >> 2)) & 1) * (w4 >> 1); }
+// The v and z sections of a stage hold step s's w4 = 4PT pieces rotated by four of them
+// (16 floats, half the banks) when bits 0 and 2 of s differ: the 16-lane reads of steps
+// s and s+1 (the partial waves' w x) and of s and s+4 (the epilogue waves' x and z), a
+// slice of 16 columns each, by one 32-lane half then fall in different banks instead of
+// on the same ones a multiple of 128 bytes apart. With one slice (w4 = 4) a read covers
+// the whole 64-byte step, and no rotation within it changes its banks. Float offset of
+// (step s, column c) in such a section; the DMA fills it through the inverse map.
+__device__ __forceinline__ int vrot(int s, int w4) {
+  return w4 >= 8 ? ((s ^ (s >> 2)) & 1) * 4 : 0;
+}
 __device__ __forceinline__ int vpos(int s, int c, int w4) {
   return s * 4 * w4 + 4 * (((c >> 2) + vrot(s, w4)) & (w4 - 1)) + (c & 3);
 }
