@@ -543,6 +543,12 @@ __device__ __forceinline__ void issue_tile(float* tile, const float* Bg, const f
 // loads give).
 constexpr int kZStageFloats = 16 * 256;
 
+// The zero row after the carries, A*log2e and the tile state's inputs sits 8 floats past
+// their end: a row's first lane reads its carry where the other 15 read the zero row, and
+// both were on bank n (rows of 16 floats from a 32-float-aligned base), a two-way
+// conflict on every state.
+constexpr int kZerosPad = 8;
+
 template <bool REV>
 __device__ __forceinline__ void issue_z_stage(float* zbuf, const float* zslab, long long zs_t,
                                               long long L, long long c0, int d0, int wave,
@@ -746,7 +752,7 @@ __device__ __forceinline__ void tile_rows(const M1Kern& p, long long blk, int se
   const float dskip = p.D ? p.D[d] : 0.0f;
   float* carry = small + (wave * RPW + rw) * N;
   float* a2s = small + (kWavesPerBlock * RPW + wave * RPW + rw) * N;
-  float* zeros = small + 2 * kWavesPerBlock * RPW * N;
+  float* zeros = small + 2 * kWavesPerBlock * RPW * N + kZerosPad;
   const float* cbase = j == 0 ? carry : zeros;
   const long long nch = (L + CH - 1) / CH;
   const long long nfull = L / CH;
@@ -1166,7 +1172,7 @@ hipError_t launch_tile(const M1Kern& k, hipStream_t st) {
   }
   const size_t lds =
       sizeof(float) * (2 * (size_t)Tile<I>::FLOATS + (SIO >= 2 || !ALN ? kZStageFloats : 0) +
-                       (2 * (size_t)RPB + 1) * k.N);
+                       (2 * (size_t)RPB + 1) * k.N + kZerosPad);
   const dim3 grid((unsigned)(segs > 1 ? blocks * segs : blocks)), wg(64 * kWavesPerBlock);
   const bool tail = k.L % Tile<I>::CH != 0;
   if (segs > 1 && tail)
@@ -1230,7 +1236,8 @@ hipError_t m1_scan_jobs(const M1Problem& pr, const M1JobSpec* spec, int n, hipSt
   }
   const long long blocks = 8LL * n * ((jobs.blocks_per_job + 7) / 8);
   const size_t lds = sizeof(float) * (2 * (size_t)Tile<M1_TILE_I>::FLOATS +
-                                      (aln ? 0 : kZStageFloats) + (2 * (size_t)16 + 1) * k.N);
+                                      (aln ? 0 : kZStageFloats) + (2 * (size_t)16 + 1) * k.N +
+                                      kZerosPad);
   const bool tail = k.L % Tile<M1_TILE_I>::CH != 0;
   const dim3 grid((unsigned)blocks), wg(64 * kWavesPerBlock);
   if (aln && tail)
