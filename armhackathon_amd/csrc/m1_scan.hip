@@ -393,7 +393,12 @@ __global__ void __launch_bounds__(256) transpose_batch_kernel(TransposeBatch b, 
   __shared__ float tile[64][65];
   const int tiles_w = (W + 63) / 64;
   const int i0 = (blockIdx.x / tiles_w) * 64, j0 = (blockIdx.x % tiles_w) * 64;
-  const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;  // 16 x 16
+  // 16 x 16 threads: 16 float4 columns (tx) by 16 rows (ty) of the tile. A 32-lane half
+  // takes 8 columns of 4 rows, so that 4 tx + ty, the bank of both the row-wise and the
+  // column-wise accesses of the padded tile (65 floats a row), covers all 32 banks; with
+  // 16 columns of 2 rows, tx and tx + 8 met on one bank.
+  const int t = threadIdx.x;
+  const int tx = (t & 7) | (((t >> 5) & 1) << 3), ty = ((t >> 3) & 3) | ((t >> 6) << 2);
   const bool vec = (W % 4 == 0) && (H % 4 == 0);
   for (long long g = blockIdx.y; g < b.first[b.n]; g += gridDim.y) {
     int k = 0;
@@ -445,7 +450,12 @@ __global__ void __launch_bounds__(256) merge4t_kernel(float* __restrict__ out,
   __shared__ float t2[64][65], t3[64][65];
   const int tiles_w = (W + 63) / 64;
   const int i0 = (blockIdx.x / tiles_w) * 64, j0 = (blockIdx.x % tiles_w) * 64;
-  const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;  // 16 x 16
+  // 16 x 16 threads: 16 float4 columns (tx) by 16 rows (ty) of the tile. A 32-lane half
+  // takes 8 columns of 4 rows, so that 4 tx + ty, the bank of both the row-wise and the
+  // column-wise accesses of the padded tile (65 floats a row), covers all 32 banks; with
+  // 16 columns of 2 rows, tx and tx + 8 met on one bank.
+  const int t = threadIdx.x;
+  const int tx = (t & 7) | (((t >> 5) & 1) << 3), ty = ((t >> 3) & 3) | ((t >> 6) << 2);
   for (long long g = blockIdx.y; g < planes; g += gridDim.y) {
     const long long plane = g * H * W;
     for (int r = ty; r < 64; r += 16) {
