@@ -563,7 +563,7 @@ def test_m3_broadcast_views():
         ang_np = np.broadcast_to(ang_small, (b, L, h, r)) if over_batch else \
             np.broadcast_to(rng.standard_normal((b, L, 1, r)).astype(np.float32), (b, L, h, r))
         ta = (torch.from_numpy(ang_small).cuda().expand(b, L, h, r) if over_batch
-              else torch.from_numpy(np.ascontiguousarray(ang_np[:, :, :1])).cuda()
+              else torch.from_numpy(ang_np[:, :, :1].copy()).cuda()
               .expand(b, L, h, r))
         tv = torch.from_numpy(v_small).cuda().expand(b, L, h, dv) if over_batch else t["v"]
         v_np = np.broadcast_to(v_small, (b, L, h, dv)) if over_batch else x["v"]
