@@ -188,9 +188,12 @@ __global__ void __launch_bounds__(256) m3_gates_kernel(M3K p, int reverse) {
     const int step_s = s / R;
     m[s] = step_s < step ? fexp(c - cs) * ss : (step_s == step && !p.accum ? gamma : 0.0f);
   }
-  if (!valid) return;
   using RC = Rec<R>;
-  float* rec = p.rec + cidx * p.rec_floats;
+  // The block's 16 records are assembled in LDS and leave as one contiguous run of
+  // 16-byte stores (written in place, a store instruction put 16 bytes into each of
+  // 64 rows 64 bytes apart).
+  __shared__ __attribute__((aligned(16))) float img[16 * RC::FloatsAng];
+  float* rec = img + (threadIdx.x >> 4) * p.rec_floats;
   if (p.rec_floats > RC::Floats) rec[RC::Hdt + row] = hdt;  // 0 past the end: theta holds
   if (row % R == 0) {  // the step's first row writes the step's entries
     if constexpr (R == 1) {
@@ -210,6 +213,13 @@ __global__ void __launch_bounds__(256) m3_gates_kernel(M3K p, int reverse) {
   }
   // e^{c_last}, then zeros to the end of the last 16-byte piece
   if (row < RC::Floats - RC::Etot) rec[RC::Etot + row] = row == 0 ? fexp(clast) : 0.0f;
+  __syncthreads();
+  const long long first = (long long)blockIdx.x * 16;
+  const long long left = (long long)p.nseq * p.nchunks - first;
+  const int n4 = (int)(left < 16 ? left : 16) * p.rec_floats / 4;  // rec_floats % 4 == 0
+  const f4* src = reinterpret_cast<const f4*>(img);
+  f4* dst = reinterpret_cast<f4*>(p.rec + first * p.rec_floats);
+  for (int i = threadIdx.x; i < n4; i += 256) dst[i] = src[i];
 }
 
 // ---------------------------------------------------------------------------
