@@ -122,15 +122,15 @@ struct M3K {
   // SISO: no same-step term (gamma on M's diagonal, D x) and out += the result
   int accum;
   // Sequences cut at chunk `split` (0: whole sequences): blocks [0, seg_blocks) run
-  // chunks [split, nchunks) from the state m3_fold_kernel left in `fold` (seq, dv, dqk),
+  // chunks [split, nchunks) from the state m3_fold_kernel left in `fold`,
   // blocks [seg_blocks, 2 seg_blocks) run chunks [0, split) from zero.
   int split, seg_blocks;
   float* fold;
   int skip_q;  // the stage holds no q section (m3_fold_kernel's): k's comes first
   // The fold runs in nsub pieces of sub_len chunks, one block each (per sequence and dv
-  // slices): piece s leaves its state from zero in fold + s * nseq * dv * dqk and its
-  // decay (the product of its chunks' e^{c_last}) in fold_decay[s * nseq + seq]; the
-  // resuming blocks combine them in order.
+  // slices): piece s leaves its state from zero in fold + s * nseq * dv * dqk (in the
+  // order the waves hold it, fold_off) and its decay (the product of its chunks'
+  // e^{c_last}) in fold_decay[s * nseq + seq]; the resuming blocks combine them in order.
   int nsub, sub_len;
   float* fold_decay;
   // With the fused angle pre-pass (SISO): fold piece s rotates its keys by theta
@@ -256,6 +256,16 @@ __device__ __forceinline__ void lds_barrier() {
 
 __device__ __forceinline__ f4 ld4(const float* p) { return *reinterpret_cast<const f4*>(p); }
 __device__ __forceinline__ f2 ld2(const float* p) { return *reinterpret_cast<const f2*>(p); }
+
+// A fold piece's state (dv x dqk per sequence) in the order the waves hold it: the
+// 16-byte unit of lane `lane` of n-tile wave nt for the 16-column dv slice `slice`
+// (rows slice*16 + lane%16, columns nt*16 + 4(lane/16) .. +3) at this float offset, so
+// that a wave stores and loads a slice as one contiguous 1 KB run. In (seq, dv, dqk)
+// order each store put 64 bytes into each of 16 rows 512 bytes apart.
+__device__ __forceinline__ long long fold_off(int seq, int slice, int nt, int lane, int dv,
+                                              int wn) {
+  return ((((long long)seq * (dv / 16) + slice) * wn + nt) * 64 + lane) * 4;
+}
 
 // Base pointers of a block's sequence.
 struct SeqIn {
@@ -804,7 +814,7 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 4)) m3_chunk_kernel(M3K p) {
     }
 #pragma unroll
     for (int j = 0; j < PT; ++j) {
-      const f4 f = ld4(fold + ((long long)seq * dv + p0 + j * 16 + li) * dqk + n0);
+      const f4 f = ld4(fold + fold_off(seq, p0 / 16 + j, nt, lane, dv, WN));
       const f4 r = ANG && !MIMO ? f4{f[0] * c0 - f[1] * s0, f[0] * s0 + f[1] * c0,
                                      f[2] * c1 - f[3] * s1, f[2] * s1 + f[3] * c1}
                                 : f;
@@ -1036,7 +1046,7 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 4)) m3_chunk_kernel(M3K p) {
 }
 
 // The state a sequence reaches after its chunks [0, p.split), from zero, written to
-// p.fold (seq, dv, dqk): the partial waves' state update alone (no q, no outputs, no
+// p.fold (in fold_off's order): the partial waves' state update alone (no q, no outputs, no
 // epilogue waves), S = e^{c_last} S + K^T diag(w) X per chunk, for the blocks of
 // m3_chunk_kernel that resume at chunk p.split. Its stage is the scan's without q and z
 // (the host builds this kernel's M3K so: skip_q), about 20 KB at config 3, so that a
@@ -1237,7 +1247,7 @@ __global__ void __launch_bounds__(64 * kMaxWaves) m3_fold_kernel(M3K p) {
   float* fold = p.fold + (long long)sub * p.nseq * dv * dqk;
 #pragma unroll
   for (int j = 0; j < PT; ++j)
-    *reinterpret_cast<f4*>(fold + ((long long)seq * dv + p0 + j * 16 + li) * dqk + n0) = S[j];
+    *reinterpret_cast<f4*>(fold + fold_off(seq, p0 / 16 + j, nt, lane, dv, WN)) = S[j];
   if (p0 == 0 && nt == 0 && lane == 0) p.fold_decay[sub * p.nseq + seq] = decay;
   if (ang && p0 == 0 && li == 0) {  // theta's increment over the piece (0 past nang)
     float* th = p.theta + ((long long)sub * p.nseq + seq) * 64 + 8 * nt + 2 * lj;
