@@ -638,7 +638,16 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 4)) m3_chunk_kernel(M3K p) {
     // inter-chunk Y[4lj + r][p]); it reads the partial buffers right after the
     // barrier that publishes them
     f4 G = {0.0f, 0.0f, 0.0f, 0.0f}, Y = {0.0f, 0.0f, 0.0f, 0.0f};
+    // ACC: the output rows chunk ch adds to, loaded in its part A so that part B, an
+    // interval later, does not wait for them before its stores
+    float accp[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     auto part_a = [&](int ch) {
+      if constexpr (ACC) {
+        const float* orow = out_lane + (long long)ch * chstep;
+#pragma unroll
+        for (int r = 0; r < 4; r += R)
+          if (ch * T + (4 * lj + r) / R < L) accp[r] = orow[(REV ? -(r / R) : r / R) * ostep];
+      }
       const float* gb = gbuf + (ch & 1) * kMaxWaves * 256;
       const float* yb = ybuf + ((ch & 1) * PT + ej) * kMaxWaves * 256;
       f4 gs[kMaxWaves], ys[kMaxWaves];  // all reads in flight at once
@@ -666,8 +675,7 @@ __global__ void __launch_bounds__(64 * (kMaxWaves + 4)) m3_chunk_kernel(M3K p) {
       float prev[4] = {0.0f, 0.0f, 0.0f, 0.0f};
       if constexpr (ACC) {
 #pragma unroll
-        for (int r = 0; r < 4; r += R)
-          if (valid(r)) prev[r] = orow[(REV ? -(r / R) : r / R) * ostep];
+        for (int r = 0; r < 4; r += R) prev[r] = accp[r];
       }
       f4 Yc = Y;
 #pragma unroll
