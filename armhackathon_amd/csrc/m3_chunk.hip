@@ -143,21 +143,25 @@ struct M3K {
 };
 
 // ---------------------------------------------------------------------------
-// Gate pre-pass: 16 lanes per (sequence, chunk), lane = row i. Traversal step g
-// maps to memory t = g (forward) or L-1-g (reverse); the trapezoid's "next" step
-// is traversal step g+1 (mamba3/scalar.rs:95-115), absent at the end.
+// Gate pre-pass: one lane per step, T = 16/R lanes per (sequence, chunk), a 16-lane
+// group holding R chunks. Traversal step g maps to memory t = g (forward) or L-1-g
+// (reverse); the trapezoid's "next" step is traversal step g+1 (mamba3/scalar.rs:95-115),
+// absent at the end.
 template <int R>
 __global__ void __launch_bounds__(256) m3_gates_kernel(M3K p, int reverse) {
-  const int row = threadIdx.x & 15;
-  const long long cidx = (long long)blockIdx.x * 16 + (threadIdx.x >> 4);
-  const bool valid = cidx < (long long)p.nseq * p.nchunks;
-  const int L = p.len, T = p.steps_per_chunk;
+  using RC = Rec<R>;
+  constexpr int T = RC::T;
+  const int step = threadIdx.x & (T - 1);
+  const long long nrec = (long long)p.nseq * p.nchunks;
+  const int slot = threadIdx.x / T;  // the block's record of this lane
+  const long long cidx = (long long)blockIdx.x * (256 / T) + slot;
+  const bool valid = cidx < nrec;
+  const int L = p.len;
   int seq = 0, ch = 0;
   if (valid) {
     seq = (int)(cidx / p.nchunks);
     ch = (int)(cidx - (long long)seq * p.nchunks);
   }
-  const int step = row / R;
   const long long g = (long long)ch * T + step;
   float a = 0.0f, gamma = 0.0f, scale = 0.0f, hdt = 0.0f;
   if (valid && g < L) {
@@ -172,51 +176,51 @@ __global__ void __launch_bounds__(256) m3_gates_kernel(M3K p, int reverse) {
       scale = gamma + p.dt[base + tn] * (1.0f - sigmoid(p.trap[base + tn]));
     }
   }
-  // c_i: inclusive sum over the rows up to i of one adt per step (its rank-0 row)
-  float c = row % R == 0 ? a : 0.0f;
+  // c_i: inclusive sum of adt over the chunk's steps up to i
+  float c = a;
 #pragma unroll
-  for (int d = 1; d < 16; d <<= 1) {
-    const float o = __shfl_up(c, d, 16);
-    if (row >= d) c += o;
+  for (int d = 1; d < T; d <<= 1) {
+    const float o = __shfl_up(c, d, T);
+    if (step >= d) c += o;
   }
-  const float clast = __shfl(c, 15, 16);
-  float m[16];
+  const float clast = __shfl(c, T - 1, T);
+  float m[T];
 #pragma unroll
-  for (int s = 0; s < 16; ++s) {
-    const float cs = __shfl(c, s, 16);
-    const float ss = __shfl(scale, s, 16);
-    const int step_s = s / R;
-    m[s] = step_s < step ? fexp(c - cs) * ss : (step_s == step && !p.accum ? gamma : 0.0f);
+  for (int s = 0; s < T; ++s) {
+    const float cs = __shfl(c, s, T);
+    const float ss = __shfl(scale, s, T);
+    m[s] = s < step ? fexp(c - cs) * ss : (s == step && !p.accum ? gamma : 0.0f);
   }
-  using RC = Rec<R>;
-  // The block's 16 records are assembled in LDS and leave as one contiguous run of
+  // The block's 256/T records are assembled in LDS and leave as one contiguous run of
   // 16-byte stores (written in place, a store instruction put 16 bytes into each of
-  // 64 rows 64 bytes apart).
-  __shared__ __attribute__((aligned(16))) float img[16 * RC::FloatsAng];
-  float* rec = img + (threadIdx.x >> 4) * p.rec_floats;
-  if (p.rec_floats > RC::Floats) rec[RC::Hdt + row] = hdt;  // 0 past the end: theta holds
-  if (row % R == 0) {  // the step's first row writes the step's entries
-    if constexpr (R == 1) {
-      // row i's 16-byte pieces rotated by i/2 (piece q at (q + i/2) & 3): the scan's
-      // epilogue reads a piece per lane, rows 64 bytes (16 banks) apart, and rotated the
-      // eight lanes of a 128-byte read phase meet no bank conflict
-      f4* mrow = reinterpret_cast<f4*>(rec + RC::M + row * 16);
+  // 64 rows 64 bytes apart at rank 1).
+  __shared__ __attribute__((aligned(16))) float img[(256 / T) * RC::FloatsAng];
+  float* rec = img + slot * p.rec_floats;
+  if (p.rec_floats > RC::Floats) {  // 0 past the end: theta holds
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        mrow[(q + (row >> 1)) & 3] = f4{m[4 * q], m[4 * q + 1], m[4 * q + 2], m[4 * q + 3]};
-    } else {
-#pragma unroll
-      for (int q = 0; q < RC::T; ++q) rec[RC::M + step * RC::T + q] = m[q * R];
-    }
-    rec[RC::Ec + step] = fexp(c);
-    rec[RC::W + step] = fexp(clast - c) * scale;
+    for (int r = 0; r < R; ++r) rec[RC::Hdt + step * R + r] = hdt;  // the step's R rows
   }
+  if constexpr (R == 1) {
+    // row i's 16-byte pieces rotated by i/2 (piece q at (q + i/2) & 3): the scan's
+    // epilogue reads a piece per lane, rows 64 bytes (16 banks) apart, and rotated the
+    // eight lanes of a 128-byte read phase meet no bank conflict
+    f4* mrow = reinterpret_cast<f4*>(rec + RC::M + step * 16);
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      mrow[(q + (step >> 1)) & 3] = f4{m[4 * q], m[4 * q + 1], m[4 * q + 2], m[4 * q + 3]};
+  } else {
+#pragma unroll
+    for (int q = 0; q < T; ++q) rec[RC::M + step * T + q] = m[q];
+  }
+  rec[RC::Ec + step] = fexp(c);
+  rec[RC::W + step] = fexp(clast - c) * scale;
   // e^{c_last}, then zeros to the end of the last 16-byte piece
-  if (row < RC::Floats - RC::Etot) rec[RC::Etot + row] = row == 0 ? fexp(clast) : 0.0f;
+  static_assert(RC::Floats - RC::Etot <= T, "the padding fits the chunk's lanes");
+  if (step < RC::Floats - RC::Etot) rec[RC::Etot + step] = step == 0 ? fexp(clast) : 0.0f;
   __syncthreads();
-  const long long first = (long long)blockIdx.x * 16;
-  const long long left = (long long)p.nseq * p.nchunks - first;
-  const int n4 = (int)(left < 16 ? left : 16) * p.rec_floats / 4;  // rec_floats % 4 == 0
+  const long long first = (long long)blockIdx.x * (256 / T);
+  const long long left = nrec - first;
+  const int n4 = (int)(left < 256 / T ? left : 256 / T) * p.rec_floats / 4;  // rec_floats % 4 == 0
   const f4* src = reinterpret_cast<const f4*>(img);
   f4* dst = reinterpret_cast<f4*>(p.rec + first * p.rec_floats);
   for (int i = threadIdx.x; i < n4; i += 256) dst[i] = src[i];
@@ -1521,7 +1525,7 @@ hipError_t m3_scan_chunked(const M3Problem& pr, hipStream_t st) {
     kf.fold_decay = k.fold_decay;
     kf.theta = k.theta;
   }
-  const unsigned gblocks = (unsigned)((nrec + 15) / 16);
+  const unsigned gblocks = (unsigned)((nrec + 16 * R - 1) / (16 * R));  // 16R records a block
   const int rev = pr.reverse ? 1 : 0;
   if (R == 1) hipLaunchKernelGGL(m3_gates_kernel<1>, dim3(gblocks), dim3(256), 0, st, k, rev);
   else if (R == 2) hipLaunchKernelGGL(m3_gates_kernel<2>, dim3(gblocks), dim3(256), 0, st, k, rev);
